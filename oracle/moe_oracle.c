@@ -1,0 +1,297 @@
+/*
+ * moe_oracle.c — CPU restatement of Reframework's MoE layer forward.
+ *
+ * TEST INFRASTRUCTURE ONLY. The parity tests, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or the timed CPU baseline). The product (reframework_amd, libmoe355) never
+ * calls it.
+ *
+ * Every function restates the reference algorithm in double precision, from
+ * the files cited at each function (paths relative to the reference repo):
+ *   oracle_router_logits  reframework/moe/moe_layer.py:323-324 (F.linear in the model dtype)
+ *   oracle_topk           reframework/moe/fused.py:32-46 (+ moe_layer.py:326-342 entropy branch)
+ *   oracle_permute        reframework/moe/fused.py:70-80, moe_layer.py:477-511 (remap/drop)
+ *   oracle_fused_experts  reframework/moe/fused.py:49-87, reframework/layers/activation.py:15-59
+ *
+ * Inputs are given in their storage type (fp32, or raw bf16/f16 bits) and are
+ * widened exactly. Results are fp64 (outputs) or fp32 rounded once (weights).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORACLE_F32 0
+#define ORACLE_BF16 1
+#define ORACLE_F16 2
+
+/* ------------------------------------------------------------ conversions */
+static double half_to_double(uint16_t h) {
+  const int sign = (h >> 15) & 1, exp = (h >> 10) & 0x1f, man = h & 0x3ff;
+  double v;
+  if (exp == 0)
+    v = ldexp((double)man, -24); /* subnormal: man * 2^-24 */
+  else if (exp == 31)
+    v = man ? NAN : INFINITY;
+  else
+    v = ldexp((double)(man | 0x400), exp - 25); /* (1024+man) * 2^(exp-25) */
+  return sign ? -v : v;
+}
+
+static double bf16_to_double(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return (double)f;
+}
+
+static double g_half_table[65536];
+static int g_half_ready = 0;
+
+static void init_half_table(void) {
+  if (g_half_ready) return;
+#pragma omp critical(oracle_half_table)
+  {
+    if (!g_half_ready) {
+      for (int i = 0; i < 65536; ++i) g_half_table[i] = half_to_double((uint16_t)i);
+      g_half_ready = 1;
+    }
+  }
+}
+
+static double load_elem(const void* base, size_t i, int type) {
+  if (type == ORACLE_F32) return (double)((const float*)base)[i];
+  if (type == ORACLE_BF16) return bf16_to_double(((const uint16_t*)base)[i]);
+  return half_to_double(((const uint16_t*)base)[i]);
+}
+
+/* sum_i base[off + i] * v[i] over n elements of storage type `type`. */
+static double dot_row(const void* base, size_t off, int type, const double* v, int n) {
+  double acc = 0.0;
+  if (type == ORACLE_F32) {
+    const float* p = (const float*)base + off;
+    for (int i = 0; i < n; ++i) acc += (double)p[i] * v[i];
+  } else if (type == ORACLE_BF16) {
+    const uint16_t* p = (const uint16_t*)base + off;
+    for (int i = 0; i < n; ++i) acc += bf16_to_double(p[i]) * v[i];
+  } else {
+    const uint16_t* p = (const uint16_t*)base + off;
+    for (int i = 0; i < n; ++i) acc += g_half_table[p[i]] * v[i];
+  }
+  return acc;
+}
+
+/* Round a double to the nearest bf16 (ties to even), returned as a double. */
+static double round_bf16(double d) {
+  float f = (float)d;
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) != 0x7f800000u) {
+    u += 0x7fffu + ((u >> 16) & 1u);
+  }
+  u &= 0xffff0000u;
+  memcpy(&f, &u, 4);
+  return (double)f;
+}
+
+/* Round a double to the nearest IEEE half (ties to even), returned as a double. */
+static double round_f16(double d) {
+  if (isnan(d) || isinf(d)) return d;
+  const double a = fabs(d);
+  if (a >= 65520.0) return d > 0 ? INFINITY : -INFINITY;
+  int e;
+  frexp(a, &e); /* a = m * 2^e, m in [0.5, 1) */
+  int q = e - 11; /* spacing of halfs near a: 2^(e-11) for normals */
+  if (q < -24) q = -24; /* subnormal spacing */
+  const double scaled = ldexp(a, -q);
+  double r = nearbyint(scaled); /* default rounding mode: ties to even */
+  const double v = ldexp(r, q);
+  return d < 0 ? -v : v;
+}
+
+static double round_to(double d, int mode) {
+  switch (mode) {
+    case 1: return round_bf16(d);
+    case 2: return round_f16(d);
+    case 3: return (double)(float)d;
+    default: return d;
+  }
+}
+
+/* -------------------------------------------------------------- activation */
+static double gate_act(int act, double g) {
+  if (act == 0) return g / (1.0 + exp(-g));
+  if (act == 1) return 0.5 * g * (1.0 + erf(g / sqrt(2.0)));
+  return 0.5 * g * (1.0 + tanh(sqrt(2.0 / M_PI) * (g + 0.044715 * g * g * g)));
+}
+
+/* ------------------------------------------------------------------ router */
+/* logits[t,e] = round_model(sum_h x[t,h] gate[e,h]) + bias[e], in fp32.
+ * round_mode: 0 keep fp32, 1 round to bf16, 2 round to f16 (the model dtype of
+ * the reference's F.linear output). */
+void oracle_router_logits(const void* x, const void* gate, int in_type, const float* bias, int T,
+                          int H, int E, int round_mode, float* logits) {
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < T; ++t) {
+    for (int e = 0; e < E; ++e) {
+      double acc = 0.0;
+      for (int h = 0; h < H; ++h)
+        acc += load_elem(x, (size_t)t * H + h, in_type) * load_elem(gate, (size_t)e * H + h, in_type);
+      float l = (float)acc;
+      if (round_mode) l = (float)round_to((double)l, round_mode);
+      if (bias) l = l + bias[e];
+      logits[(size_t)t * E + e] = l;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------- top-k */
+/* Softmax over E (fp64), the K largest logits in descending order with exact
+ * ties going to the lower expert id, weights renormalised when asked.
+ * kmin > 0: entropy-adaptive k (weights past k_dyn zeroed, always renormalised
+ * with a 1e-9 floor on the sum). */
+int oracle_topk(const float* logits, int T, int E, int K, int renorm, int kmin, float* w_out,
+                int32_t* id_out) {
+  if (E < 1 || E > 256 || K < 1 || K > E) return -1;
+#pragma omp parallel
+  {
+    char* taken = (char*)malloc((size_t)E);
+    double* p = (double*)malloc(sizeof(double) * (size_t)E);
+#pragma omp for schedule(static)
+    for (int t = 0; t < T; ++t) {
+      const float* l = logits + (size_t)t * E;
+      double m = -INFINITY, s = 0.0;
+      for (int e = 0; e < E; ++e) m = l[e] > m ? l[e] : m;
+      for (int e = 0; e < E; ++e) {
+        p[e] = exp((double)l[e] - m);
+        s += p[e];
+      }
+      for (int e = 0; e < E; ++e) p[e] /= s;
+      memset(taken, 0, (size_t)E);
+      double sel[256];
+      int ids[256];
+      for (int k = 0; k < K; ++k) {
+        int best = -1;
+        for (int e = 0; e < E; ++e) {
+          if (taken[e]) continue;
+          if (best < 0 || l[e] > l[best]) best = e; /* strict: equal values keep the lower id */
+        }
+        taken[best] = 1;
+        ids[k] = best;
+        sel[k] = p[best];
+      }
+      int kd = K;
+      if (kmin > 0) {
+        double hs = 0.0;
+        for (int e = 0; e < E; ++e) hs -= p[e] * log(p[e] > 1e-9 ? p[e] : 1e-9);
+        const double hn = E > 1 ? hs / log((double)E) : 0.0;
+        double kf = nearbyint((double)kmin + (double)(K - kmin) * hn);
+        if (kf < kmin) kf = kmin;
+        if (kf > K) kf = K;
+        kd = (int)kf;
+      }
+      double sum = 0.0;
+      for (int k = 0; k < K; ++k) {
+        if (k >= kd) sel[k] = 0.0;
+        sum += sel[k];
+      }
+      const int norm = kmin > 0 || renorm;
+      const double denom = kmin > 0 ? (sum > 1e-9 ? sum : 1e-9) : sum;
+      for (int k = 0; k < K; ++k) {
+        w_out[(size_t)t * K + k] = (float)(norm ? sel[k] / denom : sel[k]);
+        id_out[(size_t)t * K + k] = ids[k];
+      }
+    }
+    free(taken);
+    free(p);
+  }
+  return 0;
+}
+
+/* ----------------------------------------------------------------- permute */
+/* Stable grouping of the T*K routed slots by (mapped) expert: experts
+ * ascending, slots ascending within an expert. map: optional global->local
+ * rename (negative = dropped); ids outside range are dropped. */
+int oracle_permute(const int64_t* ids, int T, int K, int E, const int32_t* map, int map_len,
+                   int32_t* offsets, int32_t* slot_to_row, int32_t* row_src) {
+  const int64_t R = (int64_t)T * K;
+  int32_t* local = (int32_t*)malloc(sizeof(int32_t) * (size_t)(R > 0 ? R : 1));
+  int64_t* count = (int64_t*)calloc((size_t)E + 1, sizeof(int64_t));
+  for (int64_t s = 0; s < R; ++s) {
+    int64_t id = ids[s];
+    if (map_len > 0) id = (id >= 0 && id < map_len) ? map[id] : -1;
+    local[s] = (id >= 0 && id < E) ? (int32_t)id : -1;
+    if (local[s] >= 0) count[local[s]]++;
+  }
+  int64_t acc = 0;
+  for (int e = 0; e < E; ++e) {
+    offsets[e] = (int32_t)acc;
+    acc += count[e];
+  }
+  offsets[E] = (int32_t)acc;
+  int64_t* next = (int64_t*)malloc(sizeof(int64_t) * (size_t)E);
+  for (int e = 0; e < E; ++e) next[e] = offsets[e];
+  for (int64_t r = 0; r < R; ++r) row_src[r] = -1;
+  for (int64_t s = 0; s < R; ++s) {
+    if (local[s] < 0) {
+      slot_to_row[s] = -1;
+      continue;
+    }
+    const int64_t row = next[local[s]]++;
+    slot_to_row[s] = (int32_t)row;
+    row_src[row] = (int32_t)(s / K);
+  }
+  free(local);
+  free(count);
+  free(next);
+  return 0;
+}
+
+/* ----------------------------------------------------------- fused_experts */
+/* out[t] = sum_k w[t,k] * down_e(act(gate_e x_t) * up_e x_t), e = ids[t,k],
+ * all in fp64. w1[e] is [2I,H] (gate rows first), w2[e] is [H,I], given as
+ * per-expert pointers of `w_type` elements. inter_round rounds the activated
+ * intermediate to the product's storage type (0 none, 1 bf16, 2 f16, 3 f32).
+ * Slots with id outside [0,E) contribute nothing. tokens (optional) restricts
+ * the computation to the listed token indices (others left untouched). */
+int oracle_fused_experts(const void* x, int x_type, const void* const* w1, const void* const* w2,
+                         int w_type, const float* topk_w, const int64_t* ids, int T, int H, int I,
+                         int E, int K, int act, int inter_round, const int32_t* tokens,
+                         int n_tokens, double* out) {
+  const int n = tokens ? n_tokens : T;
+  init_half_table();
+#pragma omp parallel
+  {
+    double* xr = (double*)malloc(sizeof(double) * (size_t)H);
+    double* inter = (double*)malloc(sizeof(double) * (size_t)I);
+#pragma omp for schedule(dynamic, 1)
+    for (int j = 0; j < n; ++j) {
+      const int t = tokens ? tokens[j] : j;
+      double* o = out + (size_t)t * H;
+      for (int h = 0; h < H; ++h) {
+        xr[h] = load_elem(x, (size_t)t * H + h, x_type);
+        o[h] = 0.0;
+      }
+      for (int k = 0; k < K; ++k) {
+        const int64_t e = ids[(size_t)t * K + k];
+        if (e < 0 || e >= E) continue;
+        const double wt = (double)topk_w[(size_t)t * K + k];
+        for (int i = 0; i < I; ++i) {
+          const double g = dot_row(w1[e], (size_t)i * H, w_type, xr, H);
+          const double u = dot_row(w1[e], (size_t)(I + i) * H, w_type, xr, H);
+          inter[i] = round_to(gate_act(act, g) * u, inter_round);
+        }
+        for (int h = 0; h < H; ++h) o[h] += wt * dot_row(w2[e], (size_t)h * I, w_type, inter, I);
+      }
+    }
+    free(xr);
+    free(inter);
+  }
+  return 0;
+}
+
+/* Round n doubles to `mode` (1 bf16, 2 f16, 3 f32) in place; exposes the
+ * rounding helpers to the Python side of the oracle. */
+void oracle_round(double* v, size_t n, int mode) {
+  for (size_t i = 0; i < n; ++i) v[i] = round_to(v[i], mode);
+}

@@ -1,0 +1,272 @@
+"""ctypes binding of libmoe355.so (declared in include/moe355.h).
+
+The library is built in-tree (``make -C reframework_amd/csrc``) and loaded from
+this package directory. Nothing here computes: every function forwards raw
+device pointers and a HIP stream to the C ABI and turns a non-zero status into
+:class:`MoeLibError`. There is deliberately no fallback: if the library is
+missing, :func:`lib` raises, so a GPU run can never silently take another path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import threading
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+LIB_NAME = "libmoe355.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                           "include", "moe355.h")
+
+F32, BF16, F16 = 0, 1, 2
+ACT_CODES = {"silu": 0, "gelu": 1, "gelu_tanh": 2}
+PATH_MFMA_TILED, PATH_MFMA_SKINNY, PATH_SIMT = 0, 1, 2
+MAX_EXPERTS = 256
+
+_DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+
+class MoeLibError(RuntimeError):
+    """A libmoe355 entry point returned a non-zero status."""
+
+
+class Plan(ctypes.Structure):
+    """Mirror of ``moe355_plan``."""
+
+    _fields_ = [
+        ("path", ctypes.c_int),
+        ("tile_rows", ctypes.c_int),
+        ("max_tiles", ctypes.c_int),
+        ("down_splits", ctypes.c_int),
+        ("rows", ctypes.c_int),
+        ("n_blocks", ctypes.c_int),
+        ("T", ctypes.c_int),
+        ("H", ctypes.c_int),
+        ("I", ctypes.c_int),
+        ("E", ctypes.c_int),
+        ("K", ctypes.c_int),
+        ("dtype", ctypes.c_int),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("off_block_counts", ctypes.c_size_t),
+        ("off_offsets", ctypes.c_size_t),
+        ("off_slot_to_row", ctypes.c_size_t),
+        ("off_row_src", ctypes.c_size_t),
+        ("off_tile_map", ctypes.c_size_t),
+        ("off_inter", ctypes.c_size_t),
+        ("off_y", ctypes.c_size_t),
+    ]
+
+
+_I, _Z, _P = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_PI32 = ctypes.POINTER(ctypes.c_int32)
+_PPLAN = ctypes.POINTER(Plan)
+
+# name -> (restype, argtypes)
+_SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
+    "moe355_version": (_I, []),
+    "moe355_last_error": (ctypes.c_char_p, []),
+    "moe355_router_topk": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "moe355_topk_from_logits": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
+    "moe355_make_plan": (_I, [_I, _I, _I, _I, _I, _I, _PPLAN]),
+    "moe355_permute": (_I, [_PPLAN, _P, _I, _PI32, _I, _P, _P]),
+    "moe355_gate_up": (_I, [_PPLAN, _P, _PP, _I, _P, _P]),
+    "moe355_down": (_I, [_PPLAN, _PP, _P, _P]),
+    "moe355_combine": (_I, [_PPLAN, _P, _P, _I, _P, _P]),
+    "moe355_fused_experts": (_I, [_P, _PP, _PP, _P, _P, _I, _PI32, _I, _I, _I, _I, _I, _I, _I,
+                                  _I, _P, _I, _P, _Z, _P]),
+    "moe355_cast_f32": (_I, [_P, _P, _Z, _I, _P]),
+    "moe355_h2d_async": (_I, [_P, _P, _Z, _P]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+
+def lib() -> ctypes.CDLL:
+    """Load libmoe355.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise MoeLibError(
+                        f"{LIB_NAME} is not built at {LIB_PATH}; run "
+                        "`make -C reframework_amd/csrc` (or __graft_entry__.build())"
+                    )
+                handle = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in _SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = handle
+    return _lib
+
+
+def header_symbols(path: str = HEADER_PATH) -> List[str]:
+    """Entry points declared in include/moe355.h."""
+    with open(path, "r", encoding="utf-8") as f:
+        text = f.read()
+    return sorted(set(re.findall(r"\b(moe355_[a-z0-9_]+)\s*\(", text)))
+
+
+def _check(name: str, rc: int) -> None:
+    if rc != 0:
+        msg = lib().moe355_last_error()
+        raise MoeLibError(f"{name} failed (status {rc}): {msg.decode() if msg else ''}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"libmoe355 handles float32/bfloat16/float16, not {dtype}") from None
+
+
+def act_code(activation: str) -> int:
+    try:
+        return ACT_CODES[activation]
+    except KeyError:
+        raise ValueError(
+            f"unknown gated activation {activation!r}; known: {tuple(ACT_CODES)}"
+        ) from None
+
+
+def stream_handle(device: torch.device, stream: Optional[torch.cuda.Stream] = None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream(device)
+    return int(s.cuda_stream)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else int(t.data_ptr())
+
+
+def _ptr_table(ptrs: Sequence[int]):
+    arr = (ctypes.c_void_p * len(ptrs))(*ptrs)
+    return ctypes.cast(arr, _PP), arr
+
+
+# ------------------------------------------------------------------ wrappers
+def version() -> int:
+    return int(lib().moe355_version())
+
+
+def make_plan(T: int, H: int, I: int, E: int, K: int, dtype: int) -> Plan:
+    plan = Plan()
+    _check("moe355_make_plan", lib().moe355_make_plan(T, H, I, E, K, dtype, ctypes.byref(plan)))
+    return plan
+
+
+def router_topk(x: torch.Tensor, gate: torch.Tensor, bias: Optional[torch.Tensor], K: int,
+                renormalize: bool, round_logits: bool, entropy_k_min: int,
+                topk_w: torch.Tensor, topk_ids: torch.Tensor,
+                logits_out: Optional[torch.Tensor] = None, stream: Optional[int] = None) -> None:
+    T, H = x.shape
+    E = gate.shape[0]
+    s = stream if stream is not None else stream_handle(x.device)
+    _check("moe355_router_topk", lib().moe355_router_topk(
+        _ptr(x), _ptr(gate), _ptr(bias), T, H, E, K, dtype_code(x.dtype), int(renormalize),
+        int(round_logits), int(entropy_k_min), _ptr(logits_out), _ptr(topk_w), _ptr(topk_ids), s))
+
+
+def topk_from_logits(logits: torch.Tensor, K: int, renormalize: bool, topk_w: torch.Tensor,
+                     topk_ids: torch.Tensor, stream: Optional[int] = None) -> None:
+    T, E = logits.shape
+    s = stream if stream is not None else stream_handle(logits.device)
+    _check("moe355_topk_from_logits", lib().moe355_topk_from_logits(
+        _ptr(logits), T, E, K, int(renormalize), _ptr(topk_w), _ptr(topk_ids), s))
+
+
+def permute(plan: Plan, topk_ids: torch.Tensor, workspace: torch.Tensor,
+            expert_map: Optional[Sequence[int]] = None, stream: Optional[int] = None) -> None:
+    s = stream if stream is not None else stream_handle(topk_ids.device)
+    if expert_map:
+        m = (ctypes.c_int32 * len(expert_map))(*expert_map)
+        mp, mlen = ctypes.cast(m, _PI32), len(expert_map)
+    else:
+        mp, mlen = None, 0
+    _check("moe355_permute", lib().moe355_permute(
+        ctypes.byref(plan), _ptr(topk_ids), int(topk_ids.dtype == torch.int64), mp, mlen,
+        _ptr(workspace), s))
+
+
+def gate_up(plan: Plan, x: torch.Tensor, w1_ptrs: Sequence[int], act: int,
+            workspace: torch.Tensor, stream: Optional[int] = None) -> None:
+    s = stream if stream is not None else stream_handle(x.device)
+    tab, _keep = _ptr_table(w1_ptrs)
+    _check("moe355_gate_up", lib().moe355_gate_up(ctypes.byref(plan), _ptr(x), tab, act,
+                                                  _ptr(workspace), s))
+
+
+def down(plan: Plan, w2_ptrs: Sequence[int], workspace: torch.Tensor,
+         stream: Optional[int] = None) -> None:
+    s = stream if stream is not None else stream_handle(workspace.device)
+    tab, _keep = _ptr_table(w2_ptrs)
+    _check("moe355_down", lib().moe355_down(ctypes.byref(plan), tab, _ptr(workspace), s))
+
+
+def combine(plan: Plan, topk_w: torch.Tensor, out: torch.Tensor, accumulate_f32: bool,
+            workspace: torch.Tensor, stream: Optional[int] = None) -> None:
+    s = stream if stream is not None else stream_handle(out.device)
+    _check("moe355_combine", lib().moe355_combine(ctypes.byref(plan), _ptr(topk_w), _ptr(out),
+                                                  int(accumulate_f32), _ptr(workspace), s))
+
+
+def fused_experts(x: torch.Tensor, w1_ptrs: Sequence[int], w2_ptrs: Sequence[int], I: int,
+                  topk_w: torch.Tensor, topk_ids: torch.Tensor, act: int, out: torch.Tensor,
+                  workspace: torch.Tensor, expert_map: Optional[Sequence[int]] = None,
+                  accumulate_f32: bool = False, stream: Optional[int] = None) -> None:
+    T, H = x.shape
+    K = topk_ids.shape[1]
+    E = len(w1_ptrs)
+    s = stream if stream is not None else stream_handle(x.device)
+    t1, _k1 = _ptr_table(w1_ptrs)
+    t2, _k2 = _ptr_table(w2_ptrs)
+    if expert_map:
+        m = (ctypes.c_int32 * len(expert_map))(*expert_map)
+        mp, mlen = ctypes.cast(m, _PI32), len(expert_map)
+    else:
+        mp, mlen = None, 0
+    _check("moe355_fused_experts", lib().moe355_fused_experts(
+        _ptr(x), t1, t2, _ptr(topk_w), _ptr(topk_ids), int(topk_ids.dtype == torch.int64), mp,
+        mlen, T, H, I, E, K, dtype_code(x.dtype), act, _ptr(out), int(accumulate_f32),
+        _ptr(workspace), workspace.numel() * workspace.element_size(), s))
+
+
+def cast_f32(src: torch.Tensor, dst: torch.Tensor, stream: Optional[int] = None) -> None:
+    s = stream if stream is not None else stream_handle(src.device)
+    _check("moe355_cast_f32", lib().moe355_cast_f32(_ptr(src), _ptr(dst), src.numel(),
+                                                    dtype_code(dst.dtype), s))
+
+
+def h2d_async(dst_ptr: int, src_ptr: int, nbytes: int, stream: int) -> None:
+    _check("moe355_h2d_async", lib().moe355_h2d_async(dst_ptr, src_ptr, nbytes, stream))
+
+
+# ------------------------------------------------------------------ workspace
+class WorkspacePool:
+    """One growable device byte buffer per (device, stream).
+
+    libmoe355 allocates nothing; the host hands it this buffer. Calls on one
+    stream are ordered, so reusing the buffer across calls is safe; calls on
+    different streams get different buffers.
+    """
+
+    def __init__(self) -> None:
+        self._bufs: Dict[Tuple[int, int], torch.Tensor] = {}
+
+    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            self._bufs.pop(key, None)
+            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+workspaces = WorkspacePool()

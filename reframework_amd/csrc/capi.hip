@@ -1,0 +1,305 @@
+// The extern "C" boundary of libmoe355.so: argument checks, the execution
+// plan, and dispatch to the kernel launchers. Declarations and their reference
+// counterparts are in include/moe355.h.
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "common.h"
+
+using namespace moe355;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MOE355_OK;
+  return fail(MOE355_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+bool valid_dtype(int d) { return d == MOE355_F32 || d == MOE355_BF16 || d == MOE355_F16; }
+
+int elem_size(int d) { return d == MOE355_F32 ? 4 : 2; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+template <typename T>
+T* at(void* ws, size_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
+}
+
+int check_plan(const moe355_plan* p) {
+  if (!p) return fail(MOE355_EINVAL, "plan is NULL");
+  if (p->E < 1 || p->E > MOE355_MAX_EXPERTS || p->K < 1 || p->K > p->E || !valid_dtype(p->dtype) ||
+      p->path < 0 || p->path > MOE355_PATH_SIMT || p->rows != p->T * p->K)
+    return fail(MOE355_EINVAL, "plan is not one filled by moe355_make_plan");
+  return MOE355_OK;
+}
+
+int check_banks(const moe355_plan* p, const void* const* w, const char* name) {
+  if (!w) return fail(MOE355_EINVAL, "%s pointer table is NULL", name);
+  for (int e = 0; e < p->E; ++e) {
+    if (!w[e]) return fail(MOE355_EINVAL, "%s[%d] is NULL", name, e);
+    if (p->path != MOE355_PATH_SIMT && !aligned16(w[e]))
+      return fail(MOE355_EINVAL, "%s[%d] is not 16-byte aligned", name, e);
+  }
+  return MOE355_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe355_version(void) { return 100; }
+
+const char* moe355_last_error(void) { return g_err; }
+
+int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* p) {
+  if (!p) return fail(MOE355_EINVAL, "plan is NULL");
+  if (T < 0 || H <= 0 || I <= 0) return fail(MOE355_EINVAL, "bad sizes T=%d H=%d I=%d", T, H, I);
+  if (E < 1 || E > MOE355_MAX_EXPERTS)
+    return fail(MOE355_EUNSUPPORTED, "E=%d outside [1, %d]", E, MOE355_MAX_EXPERTS);
+  if (K < 1 || K > E) return fail(MOE355_EINVAL, "top-k K=%d outside [1, E=%d]", K, E);
+  if (!valid_dtype(dtype)) return fail(MOE355_EINVAL, "unknown dtype %d", dtype);
+  const int esz = elem_size(dtype);
+  const int vec = 16 / esz;
+  if (H % vec || I % vec)
+    return fail(MOE355_EUNSUPPORTED, "H=%d and I=%d must be multiples of %d", H, I, vec);
+  const long long R = static_cast<long long>(T) * K;
+  if (R > INT_MAX / 2) return fail(MOE355_EUNSUPPORTED, "T*K=%lld too large", R);
+
+  std::memset(p, 0, sizeof(*p));
+  p->T = T; p->H = H; p->I = I; p->E = E; p->K = K; p->dtype = dtype;
+  p->rows = static_cast<int>(R);
+  p->n_blocks = static_cast<int>((R + kPermuteChunk - 1) / kPermuteChunk);
+  const int act_e = static_cast<int>(R < E ? (R > 0 ? R : 1) : E);
+  const long long avg = R / act_e;
+
+  const bool mfma = dtype != MOE355_F32;
+  const bool tiled_ok = mfma && H % 256 == 0 && I % 128 == 0 &&
+                        static_cast<long long>(T) * H * esz < (1ll << 32) &&
+                        2ll * I * H * esz < (1ll << 32);
+  const bool skinny_ok = mfma && H % 32 == 0 && I % 32 == 0;
+  if (tiled_ok && avg > 32) {
+    p->path = MOE355_PATH_MFMA_TILED;
+    p->tile_rows = 256;
+  } else if (skinny_ok) {
+    p->path = MOE355_PATH_MFMA_SKINNY;
+    p->tile_rows = 16;
+  } else {
+    p->path = MOE355_PATH_SIMT;
+    p->tile_rows = 64;
+  }
+  p->max_tiles = R > 0 ? static_cast<int>((R + static_cast<long long>(act_e) * (p->tile_rows - 1)) /
+                                          p->tile_rows)
+                       : 0;
+  p->down_splits = 1;
+  if (p->path == MOE355_PATH_MFMA_SKINNY) {
+    // Spread the down projection (H/16 row groups per tile) over >= 4096 waves.
+    const long long waves = static_cast<long long>(H / 16) * (p->max_tiles > 0 ? p->max_tiles : 1);
+    int s = 1;
+    while (s < 16 && waves * s < 4096 && (I / 32) % (2 * s) == 0) s *= 2;
+    p->down_splits = s;
+  }
+
+  size_t off = 0;
+  p->off_block_counts = off; off = align256(off + static_cast<size_t>(p->n_blocks) * E * 4);
+  p->off_offsets = off;      off = align256(off + static_cast<size_t>(E + 1) * 4);
+  p->off_slot_to_row = off;  off = align256(off + static_cast<size_t>(R) * 4);
+  p->off_row_src = off;      off = align256(off + static_cast<size_t>(R) * 4);
+  p->off_tile_map = off;     off = align256(off + static_cast<size_t>(2 + 2 * p->max_tiles) * 4);
+  p->off_inter = off;        off = align256(off + static_cast<size_t>(R) * I * esz);
+  p->off_y = off;            off = align256(off + static_cast<size_t>(p->down_splits) * R * H * 4);
+  p->workspace_bytes = off;
+  return MOE355_OK;
+}
+
+int moe355_router_topk(const void* x, const void* gate, const float* bias, int T, int H, int E,
+                       int K, int dtype, int renormalize, int round_logits, int entropy_k_min,
+                       float* logits_out, float* topk_w, int32_t* topk_ids, void* stream) {
+  if (T < 0 || H <= 0) return fail(MOE355_EINVAL, "bad sizes T=%d H=%d", T, H);
+  if (E < 1 || E > MOE355_MAX_EXPERTS)
+    return fail(MOE355_EUNSUPPORTED, "E=%d outside [1, %d]", E, MOE355_MAX_EXPERTS);
+  if (K < 1 || K > E) return fail(MOE355_EINVAL, "top-k K=%d outside [1, E=%d]", K, E);
+  if (!valid_dtype(dtype)) return fail(MOE355_EINVAL, "unknown dtype %d", dtype);
+  if (entropy_k_min < 0 || entropy_k_min > K)
+    return fail(MOE355_EINVAL, "entropy_k_min=%d outside [0, K=%d]", entropy_k_min, K);
+  const int vec = 16 / elem_size(dtype);
+  if (H % vec || H / vec > 256 * 8)
+    return fail(MOE355_EUNSUPPORTED, "router needs H %% %d == 0 and H <= %d", vec, vec * 2048);
+  if (T == 0) return MOE355_OK;
+  if (!x || !gate || !topk_w || !topk_ids) return fail(MOE355_EINVAL, "NULL tensor argument");
+  if (!aligned16(x) || !aligned16(gate)) return fail(MOE355_EINVAL, "x/gate not 16-byte aligned");
+  RouterArgs a{};
+  a.x = x; a.gate = gate; a.bias = bias; a.logits_in = nullptr; a.logits_out = logits_out;
+  a.topk_w = topk_w; a.topk_ids = topk_ids;
+  a.T = T; a.H = H; a.E = E; a.K = K;
+  a.renormalize = renormalize != 0; a.round_logits = round_logits != 0;
+  a.entropy_k_min = entropy_k_min;
+  return check_hip(launch_router(a, dtype, as_stream(stream)), "router_topk launch");
+}
+
+int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renormalize,
+                            float* topk_w, int32_t* topk_ids, void* stream) {
+  if (T < 0) return fail(MOE355_EINVAL, "bad T=%d", T);
+  if (E < 1 || E > MOE355_MAX_EXPERTS)
+    return fail(MOE355_EUNSUPPORTED, "E=%d outside [1, %d]", E, MOE355_MAX_EXPERTS);
+  if (K < 1 || K > E) return fail(MOE355_EINVAL, "top-k K=%d outside [1, E=%d]", K, E);
+  if (T == 0) return MOE355_OK;
+  if (!logits || !topk_w || !topk_ids) return fail(MOE355_EINVAL, "NULL tensor argument");
+  RouterArgs a{};
+  a.logits_in = logits; a.topk_w = topk_w; a.topk_ids = topk_ids;
+  a.T = T; a.E = E; a.K = K; a.renormalize = renormalize != 0;
+  return check_hip(launch_topk_from_logits(a, as_stream(stream)), "topk_from_logits launch");
+}
+
+int moe355_permute(const moe355_plan* p, const void* topk_ids, int ids_int64,
+                   const int32_t* expert_map, int map_len, void* workspace, void* stream) {
+  int rc = check_plan(p);
+  if (rc) return rc;
+  if (map_len < 0 || map_len > MOE355_MAX_EXPERTS)
+    return fail(MOE355_EUNSUPPORTED, "expert_map length %d outside [0, %d]", map_len,
+                MOE355_MAX_EXPERTS);
+  if (map_len > 0 && !expert_map) return fail(MOE355_EINVAL, "expert_map is NULL");
+  if (p->rows == 0) return MOE355_OK;
+  if (!topk_ids || !workspace) return fail(MOE355_EINVAL, "NULL topk_ids or workspace");
+  PermuteArgs a{};
+  a.ids = topk_ids;
+  a.block_counts = at<int32_t>(workspace, p->off_block_counts);
+  a.offsets = at<int32_t>(workspace, p->off_offsets);
+  a.slot_to_row = at<int32_t>(workspace, p->off_slot_to_row);
+  a.row_src = at<int32_t>(workspace, p->off_row_src);
+  a.tile_map = at<int32_t>(workspace, p->off_tile_map);
+  a.R = p->rows; a.K = p->K; a.E = p->E; a.n_blocks = p->n_blocks;
+  a.tile_rows = p->tile_rows; a.max_tiles = p->max_tiles;
+  a.ids_int64 = ids_int64 != 0; a.map_len = map_len;
+  for (int i = 0; i < map_len; ++i) a.map[i] = expert_map[i];
+  return check_hip(launch_permute(a, as_stream(stream)), "permute launch");
+}
+
+int moe355_gate_up(const moe355_plan* p, const void* x, const void* const* w1, int act,
+                   void* workspace, void* stream) {
+  int rc = check_plan(p);
+  if (rc) return rc;
+  if (act < MOE355_ACT_SILU || act > MOE355_ACT_GELU_TANH)
+    return fail(MOE355_EINVAL, "unknown activation %d", act);
+  if (p->rows == 0) return MOE355_OK;
+  if (!x || !workspace) return fail(MOE355_EINVAL, "NULL x or workspace");
+  if (p->path != MOE355_PATH_SIMT && !aligned16(x)) return fail(MOE355_EINVAL, "x not 16-byte aligned");
+  if ((rc = check_banks(p, w1, "w1"))) return rc;
+  FfnArgs a{};
+  a.x = x;
+  a.row_src = at<int32_t>(workspace, p->off_row_src);
+  a.tile_map = at<int32_t>(workspace, p->off_tile_map);
+  a.offsets = at<int32_t>(workspace, p->off_offsets);
+  a.out = at<void>(workspace, p->off_inter);
+  a.H = p->H; a.I = p->I; a.R = p->rows; a.max_tiles = p->max_tiles;
+  a.splits = 1; a.k_per_split = p->H; a.act = act;
+  for (int e = 0; e < p->E; ++e) a.w[e] = w1[e];
+  hipError_t err;
+  if (p->path == MOE355_PATH_MFMA_TILED) {
+    a.n_wtiles = p->I / 128;
+    err = launch_gate_up_tiled(a, p->dtype, as_stream(stream));
+  } else if (p->path == MOE355_PATH_MFMA_SKINNY) {
+    a.n_wtiles = p->I / 16;
+    err = launch_gate_up_skinny(a, p->dtype, as_stream(stream));
+  } else {
+    a.n_wtiles = (p->I + 63) / 64;
+    err = launch_gate_up_simt(a, p->dtype, as_stream(stream));
+  }
+  return check_hip(err, "gate_up launch");
+}
+
+int moe355_down(const moe355_plan* p, const void* const* w2, void* workspace, void* stream) {
+  int rc = check_plan(p);
+  if (rc) return rc;
+  if (p->rows == 0) return MOE355_OK;
+  if (!workspace) return fail(MOE355_EINVAL, "NULL workspace");
+  if ((rc = check_banks(p, w2, "w2"))) return rc;
+  FfnArgs a{};
+  a.x = at<void>(workspace, p->off_inter);
+  a.row_src = at<int32_t>(workspace, p->off_row_src);
+  a.tile_map = at<int32_t>(workspace, p->off_tile_map);
+  a.offsets = at<int32_t>(workspace, p->off_offsets);
+  a.out = at<void>(workspace, p->off_y);
+  a.H = p->H; a.I = p->I; a.R = p->rows; a.max_tiles = p->max_tiles;
+  a.splits = p->down_splits; a.k_per_split = p->I / p->down_splits; a.act = 0;
+  for (int e = 0; e < p->E; ++e) a.w[e] = w2[e];
+  hipError_t err;
+  if (p->path == MOE355_PATH_MFMA_TILED) {
+    a.n_wtiles = p->H / 256;
+    err = launch_down_tiled(a, p->dtype, as_stream(stream));
+  } else if (p->path == MOE355_PATH_MFMA_SKINNY) {
+    a.n_wtiles = p->H / 16;
+    err = launch_down_skinny(a, p->dtype, as_stream(stream));
+  } else {
+    a.n_wtiles = (p->H + 63) / 64;
+    err = launch_down_simt(a, p->dtype, as_stream(stream));
+  }
+  return check_hip(err, "down launch");
+}
+
+int moe355_combine(const moe355_plan* p, const float* topk_w, void* out, int accumulate_f32,
+                   void* workspace, void* stream) {
+  int rc = check_plan(p);
+  if (rc) return rc;
+  if (p->T == 0) return MOE355_OK;
+  if (!topk_w || !out || !workspace) return fail(MOE355_EINVAL, "NULL topk_w, out or workspace");
+  if (!aligned16(out)) return fail(MOE355_EINVAL, "out not 16-byte aligned");
+  CombineArgs a{};
+  a.y = at<float>(workspace, p->off_y);
+  a.topk_w = topk_w;
+  a.slot_to_row = at<int32_t>(workspace, p->off_slot_to_row);
+  a.out = out;
+  a.T = p->T; a.K = p->K; a.H = p->H; a.R = p->rows; a.splits = p->down_splits;
+  a.accumulate = accumulate_f32 != 0;
+  return check_hip(launch_combine(a, p->dtype, as_stream(stream)), "combine launch");
+}
+
+int moe355_fused_experts(const void* x, const void* const* w1, const void* const* w2,
+                         const float* topk_w, const void* topk_ids, int ids_int64,
+                         const int32_t* expert_map, int map_len, int T, int H, int I, int E,
+                         int K, int dtype, int act, void* out, int accumulate_f32,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  moe355_plan p;
+  int rc = moe355_make_plan(T, H, I, E, K, dtype, &p);
+  if (rc) return rc;
+  if (T == 0) return MOE355_OK;
+  if (!workspace || workspace_bytes < p.workspace_bytes)
+    return fail(MOE355_EWORKSPACE, "workspace of %zu bytes, plan needs %zu", workspace_bytes,
+                p.workspace_bytes);
+  if ((rc = moe355_permute(&p, topk_ids, ids_int64, expert_map, map_len, workspace, stream))) return rc;
+  if ((rc = moe355_gate_up(&p, x, w1, act, workspace, stream))) return rc;
+  if ((rc = moe355_down(&p, w2, workspace, stream))) return rc;
+  return moe355_combine(&p, topk_w, out, accumulate_f32, workspace, stream);
+}
+
+int moe355_cast_f32(const float* src, void* dst, size_t n, int dtype, void* stream) {
+  if (!valid_dtype(dtype)) return fail(MOE355_EINVAL, "unknown dtype %d", dtype);
+  if (n == 0) return MOE355_OK;
+  if (!src || !dst) return fail(MOE355_EINVAL, "NULL src or dst");
+  return check_hip(launch_cast_f32(src, dst, n, dtype, as_stream(stream)), "cast launch");
+}
+
+int moe355_h2d_async(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return MOE355_OK;
+  if (!dst || !src) return fail(MOE355_EINVAL, "NULL dst or src");
+  return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)),
+                   "hipMemcpyAsync H2D");
+}
+
+}  // extern "C"

@@ -1,0 +1,201 @@
+// Shared device types, conversions and launcher declarations of libmoe355.
+//
+// Everything here is gfx950 (CDNA4) code: 64-lane wavefronts, bf16/f16 MFMA,
+// 160 KB of LDS per CU. Storage types are the raw 16-bit formats; all
+// arithmetic accumulates in fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/moe355.h"
+
+namespace moe355 {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kMaxExperts = MOE355_MAX_EXPERTS;
+constexpr int kPermuteChunk = 1024;  // routed slots per permute block
+
+// ---------------------------------------------------------------- conversions
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+  return static_cast<float>(v);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) {
+  return static_cast<T>(v);  // round-to-nearest-even for bf16 and f16
+}
+
+// Unpack a 16-byte vector of storage elements to fp32.
+template <typename T>
+struct Vec16;
+
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void unpack(u32x4 v, float* o) {
+    o[0] = __uint_as_float(v.x);
+    o[1] = __uint_as_float(v.y);
+    o[2] = __uint_as_float(v.z);
+    o[3] = __uint_as_float(v.w);
+  }
+};
+
+template <>
+struct Vec16<bf16> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void unpack(u32x4 v, float* o) {
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+
+template <>
+struct Vec16<f16> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void unpack(u32x4 v, float* o) {
+    f16x8 h = __builtin_bit_cast(f16x8, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = static_cast<float>(h[i]);
+  }
+};
+
+// Pack four fp32 values into four storage elements (8 bytes for 16-bit types).
+template <typename T>
+__device__ __forceinline__ void store4(T* dst, float a, float b, float c, float d) {
+  dst[0] = from_f32<T>(a);
+  dst[1] = from_f32<T>(b);
+  dst[2] = from_f32<T>(c);
+  dst[3] = from_f32<T>(d);
+}
+
+template <>
+__device__ __forceinline__ void store4<bf16>(bf16* dst, float a, float b, float c, float d) {
+  typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+  bf16x4 v = {from_f32<bf16>(a), from_f32<bf16>(b), from_f32<bf16>(c), from_f32<bf16>(d)};
+  *reinterpret_cast<bf16x4*>(dst) = v;
+}
+
+template <>
+__device__ __forceinline__ void store4<f16>(f16* dst, float a, float b, float c, float d) {
+  typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+  f16x4 v = {from_f32<f16>(a), from_f32<f16>(b), from_f32<f16>(c), from_f32<f16>(d)};
+  *reinterpret_cast<f16x4*>(dst) = v;
+}
+
+template <>
+__device__ __forceinline__ void store4<float>(float* dst, float a, float b, float c, float d) {
+  *reinterpret_cast<f32x4*>(dst) = f32x4{a, b, c, d};
+}
+
+// ---------------------------------------------------------------- activations
+// Gated activations of reframework/layers/activation.py:15-59 applied to the
+// gate half: silu(g) = g * sigmoid(g); gelu(g) = g/2 * (1 + erf(g/sqrt2));
+// gelu_tanh(g) = g/2 * (1 + tanh(sqrt(2/pi) * (g + 0.044715 g^3))).
+__device__ __forceinline__ float gate_act(int act, float g) {
+  if (act == MOE355_ACT_SILU) return g / (1.0f + expf(-g));
+  if (act == MOE355_ACT_GELU) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
+  const float c = 0.79788456080286536f;  // sqrt(2/pi)
+  return 0.5f * g * (1.0f + tanhf(c * (g + 0.044715f * g * g * g)));
+}
+
+// ---------------------------------------------------------------- wave helpers
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Map a flat workgroup id so that ids dispatched to the same XCD (the hardware
+// deals workgroups round-robin over the 8 XCDs) get consecutive logical ids.
+// Tiles that share a weight slab then run on one XCD and share its L2.
+__device__ __forceinline__ int xcd_remap(int pid, int nwg) {
+  const int xcd = pid & 7, slot = pid >> 3;
+  const int q = nwg >> 3, rem = nwg & 7;
+  const int base = xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q;
+  return base + slot;
+}
+
+// ---------------------------------------------------------------- kernel args
+struct RouterArgs {
+  const void* x;        // [T,H] or nullptr when logits_in is given
+  const void* gate;     // [E,H]
+  const float* bias;    // [E] or nullptr
+  const float* logits_in;  // [T,E] fp32 (topk_from_logits mode)
+  float* logits_out;    // [T,E] or nullptr
+  float* topk_w;        // [T,K]
+  int32_t* topk_ids;    // [T,K]
+  int T, H, E, K;
+  int renormalize, round_logits, entropy_k_min;
+};
+
+struct PermuteArgs {
+  const void* ids;       // [R] int32 or int64
+  int32_t* block_counts; // [n_blocks, E]
+  int32_t* offsets;      // [E+1]
+  int32_t* slot_to_row;  // [R]
+  int32_t* row_src;      // [R]
+  int32_t* tile_map;     // [2 + 2*max_tiles]
+  int R, K, E, n_blocks, tile_rows, max_tiles;
+  int ids_int64, map_len;  // map_len 0: no map
+  int32_t map[kMaxExperts];
+};
+
+struct FfnArgs {
+  const void* x;           // gate_up: tokens [T,H]; down: inter [R,I]
+  const int32_t* row_src;  // [R]
+  const int32_t* tile_map; // [2 + 2*max_tiles]
+  const int32_t* offsets;  // [E+1]
+  void* out;               // gate_up: inter [R,I]; down: y [S,R,H] fp32
+  int H, I, R;
+  int max_tiles, n_wtiles, splits, k_per_split;
+  int act;
+  const void* w[kMaxExperts];  // w1[e] ([2I,H]) or w2[e] ([H,I])
+};
+
+struct CombineArgs {
+  const float* y;            // [S,R,H]
+  const float* topk_w;       // [T,K]
+  const int32_t* slot_to_row;  // [T*K]
+  void* out;                 // [T,H]
+  int T, K, H, R, splits;
+  int accumulate;
+};
+
+// ---------------------------------------------------------------- launchers
+// Each returns the hipError_t of the launch (hipSuccess when nothing to do).
+hipError_t launch_router(const RouterArgs& a, int dtype, hipStream_t s);
+hipError_t launch_topk_from_logits(const RouterArgs& a, hipStream_t s);
+hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
+hipError_t launch_gate_up_tiled(const FfnArgs& a, int dtype, hipStream_t s);
+hipError_t launch_down_tiled(const FfnArgs& a, int dtype, hipStream_t s);
+hipError_t launch_gate_up_skinny(const FfnArgs& a, int dtype, hipStream_t s);
+hipError_t launch_down_skinny(const FfnArgs& a, int dtype, hipStream_t s);
+hipError_t launch_gate_up_simt(const FfnArgs& a, int dtype, hipStream_t s);
+hipError_t launch_down_simt(const FfnArgs& a, int dtype, hipStream_t s);
+hipError_t launch_combine(const CombineArgs& a, int out_dtype, hipStream_t s);
+hipError_t launch_cast_f32(const float* src, void* dst, size_t n, int dtype, hipStream_t s);
+
+}  // namespace moe355

@@ -1,0 +1,154 @@
+// Stable counting sort of routed slots by expert.
+//
+// Replaces the grouping of fused_experts (reframework/moe/fused.py:70-80),
+// which visits experts in ascending id and, inside an expert, slots in
+// ascending flat (t,k) order. Two launches, no host round trip:
+//   1. count:   each block histograms kPermuteChunk slots into LDS and writes
+//               its per-expert counts;
+//   2. scatter: each block rebuilds the global expert starts and its own
+//               prefix from the count table, ranks its slots stably with
+//               wavefront ballots, and writes slot_to_row / row_src. Block 0
+//               also writes expert_offsets and the tile map the expert-FFN
+//               kernels are launched over.
+// Only indices move here (4*T*K bytes each way); token rows are gathered later
+// by the gate_up kernel straight from x, so no permuted copy of x is written.
+#include "common.h"
+
+namespace moe355 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRounds = kPermuteChunk / kThreads;
+constexpr int kWaves = kThreads / kWave;
+
+// Local expert of a routed slot, or -1 when the slot is dropped.
+__device__ __forceinline__ int slot_expert(const PermuteArgs& a, int slot) {
+  long long id = a.ids_int64 ? static_cast<const int64_t*>(a.ids)[slot]
+                             : static_cast<long long>(static_cast<const int32_t*>(a.ids)[slot]);
+  if (a.map_len > 0) {
+    if (id < 0 || id >= a.map_len) return -1;
+    id = a.map[id];
+  }
+  return (id >= 0 && id < a.E) ? static_cast<int>(id) : -1;
+}
+
+__global__ __launch_bounds__(kThreads) void count_kernel(const PermuteArgs a) {
+  __shared__ int hist[kMaxExperts];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  for (int e = tid; e < a.E; e += kThreads) hist[e] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int slot = b * kPermuteChunk + r * kThreads + tid;
+    if (slot < a.R) {
+      const int e = slot_expert(a, slot);
+      if (e >= 0) atomicAdd(&hist[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < a.E; e += kThreads) a.block_counts[b * a.E + e] = hist[e];
+}
+
+__global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) {
+  __shared__ int base[kMaxExperts];     // first row of this block's slots of expert e
+  __shared__ int start[kMaxExperts + 1];  // expert_offsets
+  __shared__ int total[kMaxExperts];
+  __shared__ int tile_start[kMaxExperts + 1];
+  __shared__ int wave_cnt[kWaves][kMaxExperts];
+
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+
+  for (int e = tid; e < a.E; e += kThreads) {
+    int tot = 0, pre = 0;
+    for (int bb = 0; bb < a.n_blocks; ++bb) {
+      const int c = a.block_counts[bb * a.E + e];
+      tot += c;
+      if (bb < b) pre += c;
+    }
+    total[e] = tot;
+    base[e] = pre;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0, tacc = 0;
+    for (int e = 0; e < a.E; ++e) {
+      start[e] = acc;
+      tile_start[e] = tacc;
+      acc += total[e];
+      tacc += (total[e] + a.tile_rows - 1) / a.tile_rows;
+    }
+    start[a.E] = acc;
+    tile_start[a.E] = tacc < a.max_tiles ? tacc : a.max_tiles;
+  }
+  __syncthreads();
+  for (int e = tid; e < a.E; e += kThreads) base[e] += start[e];
+
+  if (b == 0) {
+    for (int e = tid; e <= a.E; e += kThreads) a.offsets[e] = start[e];
+    const int ntiles = tile_start[a.E];
+    if (tid == 0) {
+      a.tile_map[0] = ntiles;
+      a.tile_map[1] = a.tile_rows;
+    }
+    for (int j = tid; j < ntiles; j += kThreads) {
+      int lo = 0, hi = a.E - 1;  // last expert with tile_start[e] <= j
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tile_start[mid] <= j) lo = mid; else hi = mid - 1;
+      }
+      a.tile_map[2 + 2 * j] = lo;
+      a.tile_map[3 + 2 * j] = start[lo] + (j - tile_start[lo]) * a.tile_rows;
+    }
+  }
+
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  for (int r = 0; r < kRounds; ++r) {
+    for (int i = tid; i < kWaves * a.E; i += kThreads) (&wave_cnt[0][0])[i] = 0;
+    __syncthreads();
+    const int slot = b * kPermuteChunk + r * kThreads + tid;
+    const int e = slot < a.R ? slot_expert(a, slot) : -1;
+    // Rank among lanes of this wave routed to the same expert, lower lanes first.
+    int rank = 0;
+    unsigned long long todo = __ballot(e >= 0);
+    while (todo) {
+      const int leader = __ffsll(static_cast<long long>(todo)) - 1;
+      const int ev = __shfl(e, leader, kWave);
+      const unsigned long long m = __ballot(e == ev);
+      if (e == ev) rank = __popcll(m & lt_mask);
+      if (lane == leader) wave_cnt[wave][ev] = __popcll(m);
+      todo &= ~m;
+    }
+    __syncthreads();
+    if (slot < a.R) {
+      if (e >= 0) {
+        int row = base[e] + rank;
+        for (int w = 0; w < wave; ++w) row += wave_cnt[w][e];
+        a.slot_to_row[slot] = row;
+        a.row_src[row] = slot / a.K;
+      } else {
+        a.slot_to_row[slot] = -1;
+      }
+    }
+    __syncthreads();
+    for (int ee = tid; ee < a.E; ee += kThreads) {
+      int add = 0;
+      for (int w = 0; w < kWaves; ++w) add += wave_cnt[w][ee];
+      base[ee] += add;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+hipError_t launch_permute(const PermuteArgs& a, hipStream_t s) {
+  if (a.R == 0) return hipSuccess;
+  count_kernel<<<dim3(a.n_blocks), dim3(kThreads), 0, s>>>(a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  scatter_kernel<<<dim3(a.n_blocks), dim3(kThreads), 0, s>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace moe355

@@ -1,0 +1,146 @@
+"""Routing and grouped expert compute on libmoe355 (MI355X HIP kernels).
+
+Same call surface as the reference's module (reframework/moe/fused.py):
+
+  * ``torch_fused_topk(gating_output, topk, renormalize)`` -> (weights fp32
+    [M,K], ids int64 [M,K]): softmax over experts, the K largest, optional
+    renormalisation (fused.py:32-46).
+  * ``fused_experts(hidden_states, w1, w2, topk_weights, topk_ids, activation)``
+    -> [M,H] in the dtype of ``hidden_states`` (fused.py:49-87).
+
+The reference loops over experts in Python (gather, two torch.mm, activation,
+scale, index_add_). Here one C call runs the whole thing on the current HIP
+stream: a stable counting sort of the routed slots, the grouped gate|up GEMM
+with the activation fused, the grouped down GEMM, and a deterministic
+weighted combine. Expert banks are passed as a table of per-expert device
+pointers, so ``w1``/``w2`` may be a stacked ``[E,2I,H]`` tensor or a list of
+per-expert tensors (the offload cache's HBM slots) without a stacking copy.
+Exact ties in top-k go to the lower expert id.
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional, Sequence, Tuple, Union
+
+import torch
+
+from reframework_amd import _capi
+from reframework_amd.layers import activation_code
+
+Bank = Union[torch.Tensor, Sequence[torch.Tensor]]
+
+
+def require_gpu(t: torch.Tensor, what: str = "input") -> None:
+    """The MoE kernels run only on a ROCm GPU; anything else is an error."""
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"reframework_amd MoE kernels run on a ROCm GPU; {what} is on {t.device}"
+        )
+
+
+def bank_pointers(bank: Bank) -> Tuple[List[int], Tuple[int, ...]]:
+    """Per-expert device pointers of a stacked bank or a list of expert tensors.
+
+    Returns (pointers, matrix shape). Every expert matrix must be contiguous.
+    """
+    if isinstance(bank, torch.Tensor):
+        if bank.dim() != 3:
+            raise ValueError(f"expected a stacked [E, rows, cols] bank, got {tuple(bank.shape)}")
+        if not bank.is_contiguous():
+            raise ValueError("stacked expert bank must be contiguous")
+        base = bank.data_ptr()
+        step = bank.stride(0) * bank.element_size()
+        return [base + e * step for e in range(bank.shape[0])], tuple(bank.shape[1:])
+    mats = list(bank)
+    if not mats:
+        raise ValueError("empty expert bank")
+    shape = tuple(mats[0].shape)
+    for m in mats:
+        if tuple(m.shape) != shape or not m.is_contiguous():
+            raise ValueError("per-expert tensors must be contiguous and share one shape")
+    return [m.data_ptr() for m in mats], shape
+
+
+def _bank_dtype(bank: Bank) -> torch.dtype:
+    return bank.dtype if isinstance(bank, torch.Tensor) else bank[0].dtype
+
+
+def torch_fused_topk(
+    gating_output: torch.Tensor,
+    topk: int,
+    renormalize: bool,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Softmax over all experts, keep the top-k, renormalise the kept weights."""
+    require_gpu(gating_output, "gating_output")
+    E = gating_output.shape[-1]
+    logits = gating_output.reshape(-1, E).float().contiguous()
+    T = logits.shape[0]
+    w = torch.empty((T, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((T, topk), dtype=torch.int32, device=logits.device)
+    _capi.topk_from_logits(logits, topk, renormalize, w, ids)
+    shape = tuple(gating_output.shape[:-1]) + (topk,)
+    return w.reshape(shape), ids.long().reshape(shape)
+
+
+def run_experts(
+    x: torch.Tensor,
+    w1_ptrs: Sequence[int],
+    w2_ptrs: Sequence[int],
+    intermediate_size: int,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    act: int,
+    out: Optional[torch.Tensor] = None,
+    expert_map: Optional[Sequence[int]] = None,
+    accumulate_f32: bool = False,
+) -> torch.Tensor:
+    """One libmoe355 fused_experts call on the current stream.
+
+    x [T,H] contiguous in the bank dtype; topk_weights [T,K] fp32; topk_ids
+    [T,K] int32/int64; ids are local bank rows unless ``expert_map`` renames
+    them. With ``accumulate_f32`` the result is added to the fp32 ``out``.
+    """
+    T, H = x.shape
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.float32 if accumulate_f32 else x.dtype,
+                          device=x.device)
+    if T == 0:
+        return out
+    stream = _capi.stream_handle(x.device)
+    plan = _capi.make_plan(T, H, intermediate_size, len(w1_ptrs), topk_ids.shape[1],
+                           _capi.dtype_code(x.dtype))
+    ws = _capi.workspaces.get(x.device, stream, plan.workspace_bytes)
+    _capi.fused_experts(x, w1_ptrs, w2_ptrs, intermediate_size, topk_weights, topk_ids, act, out,
+                        ws, expert_map=expert_map, accumulate_f32=accumulate_f32, stream=stream)
+    return out
+
+
+def fused_experts(
+    hidden_states: torch.Tensor,
+    w1: Bank,  # [E, 2I, H] gate|up rows (gate first), or E tensors [2I, H]
+    w2: Bank,  # [E, H, I], or E tensors [H, I]
+    topk_weights: torch.Tensor,  # [M, K] fp32
+    topk_ids: torch.Tensor,  # [M, K] int64 (or int32)
+    activation: str = "silu",
+) -> torch.Tensor:
+    """Run the routed experts and return the summed output ``[M, H]``."""
+    act = activation_code(activation)
+    require_gpu(hidden_states, "hidden_states")
+    w1_ptrs, s1 = bank_pointers(w1)
+    w2_ptrs, s2 = bank_pointers(w2)
+    if len(w1_ptrs) != len(w2_ptrs):
+        raise ValueError("w1 and w2 hold different expert counts")
+    M, H = hidden_states.shape
+    I = s1[0] // 2
+    if s1 != (2 * I, H) or s2 != (H, I):
+        raise ValueError(f"bank shapes {s1} / {s2} do not match hidden size {H}")
+    dtype = _bank_dtype(w1)
+    x = hidden_states.to(dtype).contiguous()
+    ids = topk_ids if topk_ids.dtype in (torch.int32, torch.int64) else topk_ids.long()
+    ids = ids.reshape(M, -1).contiguous()
+    w = topk_weights.reshape(M, -1).float().contiguous()
+    out = run_experts(x, w1_ptrs, w2_ptrs, I, w, ids, act)
+    return out if out.dtype == hidden_states.dtype else out.to(hidden_states.dtype)
+
+
+__all__ = ["torch_fused_topk", "fused_experts", "run_experts", "bank_pointers", "require_gpu"]

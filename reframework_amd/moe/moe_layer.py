@@ -1,0 +1,330 @@
+"""FusedMoE: the routed MoE block on libmoe355 (MI355X HIP kernels).
+
+Drop-in for the reference's ``FusedMoE`` (reframework/moe/moe_layer.py:132-
+660): same constructor, ``from_config`` fields, parameters (``gate [E,H]``,
+``experts_w1[e] [2I,H]`` gate rows first, ``experts_w2[e] [H,I]``), HF-named
+state dict, offload wiring (``build_offload_cache``, ``attach_predictor``,
+``enable_cpu_split``, ``set_shuttle``) and forward semantics:
+
+  * resident forward: route, then all routed experts (moe_layer.py:443-447,
+    513). The reference stacks every expert into fresh ``[E,2I,H]``/``[E,H,I]``
+    banks on each call; here the kernels read the parameters in place through
+    a pointer table.
+  * offload forward (``RE_CHUNK_SIZE`` unset or 0): experts ranked by summed
+    routing weight, the first ``RE_MAX_PACK`` (default 2) kept and prefetched,
+    the other slots dropped (weight 0), the routed set recorded for the
+    lookahead, then the experts run (moe_layer.py:426-442, 477-513).
+  * streaming offload (``RE_CHUNK_SIZE`` > 0): every routed expert, in chunks
+    of that many experts, accumulated in fp32 (moe_layer.py:354-420). Chunk
+    i+1's host->HBM copies are queued on the cache's side stream while chunk
+    i's kernels run.
+
+All compute is in libmoe355: the router kernel (GEMV + softmax + top-k) and
+one fused_experts call per forward (or per chunk). A CPU tensor is an error,
+not a slower path.
+"""
+
+from __future__ import annotations
+
+import logging
+import time
+from collections import deque
+from typing import Deque, Dict, List, Optional, Tuple
+
+import torch
+
+from reframework_amd import _capi, env
+from reframework_amd.layers import BaseOP, activation_code
+from reframework_amd.moe.fused import require_gpu, run_experts
+from reframework_amd.moe.offload_cache import ExpertOffloadCache, Prediction
+
+logger = logging.getLogger(__name__)
+
+
+class CpuShuttle:
+    """Byte-accounting stand-in for a device-to-device token shuttle.
+
+    ``send`` ages every in-flight transfer by one step and appends the new one;
+    each transfer decays by ``bytes / n_steps`` per step, so it is visible to
+    ``inflight_bytes`` for exactly ``n_steps`` reads (reference:
+    moe_layer.py:58-129). No data moves: ``send`` returns a clone.
+    """
+
+    def __init__(self, n_steps: int = 2) -> None:
+        self.n_steps = max(1, int(n_steps))
+        self._transfers: Deque[Tuple[float, float]] = deque()
+
+    def send(self, hidden: torch.Tensor, to: str = "") -> torch.Tensor:
+        self.advance_step()
+        if hidden is not None and hidden.numel() > 0:
+            nbytes = float(hidden.numel() * hidden.element_size())
+            self._transfers.append((nbytes, nbytes / self.n_steps))
+        return hidden.clone() if hidden is not None else hidden
+
+    def advance_step(self) -> None:
+        self._transfers = deque((r - per, per) for r, per in self._transfers if r - per > 0.0)
+
+    def inflight_bytes(self) -> float:
+        return float(sum(r for r, _ in self._transfers))
+
+    def sync(self) -> None:
+        self._transfers.clear()
+
+
+class FusedMoE(BaseOP):
+    """A routed MoE block: ``gate`` -> top-k -> grouped SwiGLU experts."""
+
+    def __init__(
+        self,
+        num_experts: int,
+        top_k: int,
+        hidden_size: int,
+        intermediate_size: int,
+        activation: str = "silu",
+        renormalize: bool = True,
+        dtype: torch.dtype = torch.float16,
+    ) -> None:
+        super().__init__()
+        self.num_experts = num_experts
+        self.top_k = top_k
+        self.hidden_size = hidden_size
+        self.intermediate_size = intermediate_size
+        self.activation = activation
+        self.renormalize = renormalize
+        self.dtype = dtype
+        self.gate = torch.nn.Parameter(torch.empty(num_experts, hidden_size, dtype=dtype))
+        self.experts_w1 = torch.nn.ParameterList([
+            torch.nn.Parameter(torch.empty(2 * intermediate_size, hidden_size, dtype=dtype))
+            for _ in range(num_experts)
+        ])
+        self.experts_w2 = torch.nn.ParameterList([
+            torch.nn.Parameter(torch.empty(hidden_size, intermediate_size, dtype=dtype))
+            for _ in range(num_experts)
+        ])
+        self._cache: Optional[ExpertOffloadCache] = None
+        self._cpu_split_enabled: bool = False
+        self._predictor: Optional[Prediction] = None
+        self._shuttle: Optional[CpuShuttle] = None
+        self._last_step_t: Optional[float] = None
+        self.entropy_adaptive_k: bool = False
+        self.entropy_k_min: int = 2
+
+    # --------------------------------------------------------------- factories
+    @classmethod
+    def from_config(cls, cfg, dtype: Optional[torch.dtype] = None) -> "FusedMoE":
+        """Build from a model config with the reference's MoE fields
+        (num_experts, num_experts_per_tok, hidden_size, moe_inter,
+        moe_activation, moe_renormalize, dtype; optional entropy_adaptive_k,
+        entropy_k_min), honouring RE_ENTROPY_K / RE_ENTROPY_K_MIN."""
+        moe = cls(
+            num_experts=cfg.num_experts,
+            top_k=cfg.num_experts_per_tok,
+            hidden_size=cfg.hidden_size,
+            intermediate_size=cfg.moe_inter,
+            activation=cfg.moe_activation,
+            renormalize=cfg.moe_renormalize,
+            dtype=dtype or cfg.dtype,
+        )
+        moe.entropy_adaptive_k = bool(getattr(cfg, "entropy_adaptive_k", False)) or env.get_entropy_k()
+        moe.entropy_k_min = env.get_entropy_k_min(getattr(cfg, "entropy_k_min", 2))
+        logger.info("[entropy] adaptive_k=%s k_min=%d top_k=%d num_experts=%d",
+                    moe.entropy_adaptive_k, moe.entropy_k_min, moe.top_k, moe.num_experts)
+        return moe
+
+    # ----------------------------------------------------------- offload setup
+    def build_offload_cache(self, device: torch.device, lru_capacity: int) -> ExpertOffloadCache:
+        """Stage this layer's experts into a pinned-host cache on ``device``
+        and drop the per-expert parameters."""
+        self._cache = ExpertOffloadCache(device=device, lru_capacity=lru_capacity, dtype=self.dtype)
+        self._cache.load([{"w1": self.experts_w1[e], "w2": self.experts_w2[e]}
+                          for e in range(self.num_experts)])
+        self.experts_w1 = torch.nn.ParameterList()
+        self.experts_w2 = torch.nn.ParameterList()
+        if torch.cuda.is_available():
+            torch.cuda.empty_cache()
+        return self._cache
+
+    def attach_predictor(self, window: int = 32) -> None:
+        if self._cache is None:
+            return
+        self._cache.attach_predictor(window=window)
+        self._predictor = self._cache._predictor
+
+    def enable_cpu_split(self) -> None:
+        """Accepted for interface compatibility; the split stays off.
+
+        The reference computes non-resident experts on the host with int8
+        GEMMs (moe_layer.py:263-282, 523-627). On MI355X a miss streams from
+        the pinned pool over PCIe on a side stream instead, so every expert is
+        computed by the GPU kernels; ``cpu_split`` remains False.
+        """
+        if self._cache is None:
+            return
+        logger.warning("RE_MOE_CPU_SPLIT: host-side expert compute is not used on MI355X; "
+                       "misses stream to HBM on a side stream instead")
+
+    def set_shuttle(self, shuttle: Optional[CpuShuttle]) -> None:
+        self._shuttle = shuttle
+
+    @property
+    def cpu_split(self) -> bool:
+        return self._cpu_split_enabled and self.uses_offload and self._cache.cpu_split
+
+    @property
+    def uses_offload(self) -> bool:
+        return self._cache is not None
+
+    def _since_last_step_ms(self) -> float:
+        """Milliseconds since this layer's previous forward; 0.0 on the first."""
+        t = time.perf_counter()
+        prev, self._last_step_t = self._last_step_t, t
+        return 0.0 if prev is None else max(0.0, (t - prev) * 1000.0)
+
+    # ----------------------------------------------------------------- routing
+    def _route32(self, xd: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Router kernel on ``xd`` ([T,H], model dtype, contiguous, on GPU):
+        (weights fp32 [T,K], ids int32 [T,K])."""
+        gate = self.gate.detach()
+        if gate.device != xd.device:
+            gate = gate.to(xd.device)
+        gate = gate.to(self.dtype).contiguous()
+        T = xd.shape[0]
+        w = torch.empty((T, self.top_k), dtype=torch.float32, device=xd.device)
+        ids = torch.empty((T, self.top_k), dtype=torch.int32, device=xd.device)
+        kmin = 0
+        if self.entropy_adaptive_k:
+            if self.entropy_k_min < 1:
+                raise ValueError("entropy-adaptive routing needs entropy_k_min >= 1")
+            kmin = min(int(self.entropy_k_min), self.top_k)
+        _capi.router_topk(xd, gate, None, self.top_k, self.renormalize, True, kmin, w, ids)
+        return w, ids
+
+    def route(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Return (topk_weights [M,K] fp32, topk_ids [M,K] int64) for ``x``."""
+        x2 = x.reshape(-1, self.hidden_size)
+        require_gpu(x2)
+        w, ids = self._route32(x2.to(self.dtype).contiguous())
+        return w, ids.long()
+
+    def prefetch_ids(self, x: torch.Tensor) -> torch.Tensor:
+        _, ids = self.route(x)
+        return ids
+
+    # ----------------------------------------------------------------- forward
+    def _resident_banks(self) -> Tuple[List[int], List[int]]:
+        if len(self.experts_w1) != self.num_experts:
+            raise RuntimeError("expert parameters are not resident (offload cache built?)")
+        w1p, w2p = [], []
+        for p1, p2 in zip(self.experts_w1, self.experts_w2):
+            if p1.device.type != "cuda" or p2.device.type != "cuda":
+                raise RuntimeError("expert parameters must be on the GPU")
+            if p1.dtype != self.dtype or p2.dtype != self.dtype:
+                raise RuntimeError("expert parameters must be in the layer dtype")
+            if not (p1.is_contiguous() and p2.is_contiguous()):
+                raise RuntimeError("expert parameters must be contiguous")
+            w1p.append(p1.data_ptr())
+            w2p.append(p2.data_ptr())
+        return w1p, w2p
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        M = x.shape[0] if x.dim() > 1 else x.numel()
+        x2 = x.reshape(-1, self.hidden_size)
+        require_gpu(x2)
+        xd = x2.to(self.dtype).contiguous()
+        w, ids = self._route32(xd)
+        act = activation_code(self.activation)
+
+        if self.uses_offload and env.get_chunk_size(0) > 0:
+            out = self._forward_streaming(xd, w, ids, act)
+        elif self.uses_offload:
+            out = self._forward_offload(M, xd, w, ids, act)
+        else:
+            w1p, w2p = self._resident_banks()
+            out = run_experts(xd, w1p, w2p, self.intermediate_size, w, ids, act)
+        if out.dtype != x2.dtype:
+            out = out.to(x2.dtype)
+        return out.reshape(x.shape[:1] + (self.hidden_size,)) if x.dim() > 1 else out
+
+    def _forward_offload(self, M: int, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
+                         act: int) -> torch.Tensor:
+        cache = self._cache
+        ids_host = ids.reshape(-1).tolist()
+        w_host = w.reshape(-1).tolist()
+        # Rank experts by summed routing weight (ties: first appearance) and keep
+        # the first RE_MAX_PACK (moe_layer.py:426-442).
+        weight_sum: Dict[int, float] = {}
+        for eid, wt in zip(ids_host, w_host):
+            if eid >= 0:
+                weight_sum[eid] = weight_sum.get(eid, 0.0) + wt
+        kept = [eid for eid, _ in sorted(weight_sum.items(), key=lambda kv: -kv[1])]
+        kept = kept[:env.get_max_pack(2)]
+        w1s, w2s, local_index = cache.prefetch_slots(kept)
+        # Dropped slots contribute nothing; in the routed set recorded for the
+        # lookahead they read as the smallest kept id (moe_layer.py:479-486).
+        expert_map = [-1] * self.num_experts
+        for g, loc in local_index.items():
+            expert_map[g] = loc
+        if self._predictor is not None:
+            fallback = next(iter(local_index)) if local_index else -1
+            routed = [i if i in local_index else fallback for i in ids_host]
+            self._predictor.record_step(routed, is_prefill=(M > 1),
+                                        forward_ms=self._since_last_step_ms())
+        w1p = [t.data_ptr() for t in w1s]
+        w2p = [t.data_ptr() for t in w2s]
+        if not w1p:
+            return torch.zeros_like(xd)
+        return run_experts(xd, w1p, w2p, self.intermediate_size, w, ids, act,
+                           expert_map=expert_map)
+
+    def _forward_streaming(self, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
+                           act: int) -> torch.Tensor:
+        """Every routed expert, ``RE_CHUNK_SIZE`` experts at a time, summed in
+        fp32 and cast once at the end (moe_layer.py:354-420)."""
+        cache = self._cache
+        chunk_size = env.get_chunk_size(8)
+        uniq = sorted({i for i in ids.reshape(-1).tolist() if i >= 0})
+        acc = torch.zeros((xd.shape[0], self.hidden_size), dtype=torch.float32, device=xd.device)
+        for start in range(0, len(uniq), chunk_size):
+            chunk = uniq[start:start + chunk_size]
+            w1s, w2s, local_index = cache.prefetch_slots(chunk)
+            expert_map = [-1] * self.num_experts
+            for g, loc in local_index.items():
+                expert_map[g] = loc
+            run_experts(xd, [t.data_ptr() for t in w1s], [t.data_ptr() for t in w2s],
+                        self.intermediate_size, w, ids, act, out=acc, expert_map=expert_map,
+                        accumulate_f32=True)
+        out = torch.empty((xd.shape[0], self.hidden_size), dtype=xd.dtype, device=xd.device)
+        _capi.cast_f32(acc, out)
+        return out
+
+    # -------------------------------------------------------------- (de)serial
+    def state_dict(self, *, prefix: str = "", result: Optional[dict] = None,
+                   destination=None, keep_vars: bool = False) -> Dict[str, torch.Tensor]:
+        result = destination if destination is not None else ({} if result is None else result)
+        result[f"{prefix}.gate.weight" if prefix else "gate.weight"] = self.gate
+        I = self.intermediate_size
+        for e in range(len(self.experts_w1)):
+            p = f"{prefix}.experts.{e}" if prefix else f"experts.{e}"
+            result[f"{p}.gate_proj.weight"] = self.experts_w1[e][:I]
+            result[f"{p}.up_proj.weight"] = self.experts_w1[e][I:]
+            result[f"{p}.down_proj.weight"] = self.experts_w2[e]
+        return result
+
+    def load_state_dict(self, state_dict: Dict[str, torch.Tensor], *, prefix: str = "",
+                        strict: bool = True, assign: bool = False) -> None:
+        with torch.no_grad():
+            g = f"{prefix}.gate.weight" if prefix else "gate.weight"
+            if g in state_dict:
+                self.gate.copy_(state_dict[g].detach().to(dtype=self.dtype))
+            I = self.intermediate_size
+            for e in range(len(self.experts_w1)):
+                p = f"{prefix}.experts.{e}" if prefix else f"experts.{e}"
+                for name, param in (("gate_proj", self.experts_w1[e][:I]),
+                                    ("up_proj", self.experts_w1[e][I:]),
+                                    ("down_proj", self.experts_w2[e])):
+                    key = f"{p}.{name}.weight"
+                    if key in state_dict:
+                        param.copy_(state_dict[key].detach().to(dtype=self.dtype))
+
+
+__all__ = ["FusedMoE", "CpuShuttle"]

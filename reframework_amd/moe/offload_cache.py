@@ -1,0 +1,572 @@
+"""Pinned-host expert pool with an HBM LRU window, for one MoE layer.
+
+Drop-in for the reference's ``ExpertOffloadCache`` / ``Prediction`` /
+``OffloadStats`` (reframework/moe/offload_cache.py:75-751): same constructor,
+methods, counters, eviction policies (``RE_CACHE_POLICY`` = ``lru`` |
+``least_stale``), two-tier hard/soft protection, lookahead ``reserve`` with a
+bandwidth- and room-bounded dynamic k, and similarity substitution. The policy
+is host bookkeeping and stays in Python, decision for decision the
+reference's.
+
+What changes on MI355X is how bytes move:
+
+  * Resident experts live in fixed HBM *slots*, each one buffer holding w1
+    ``[2I,H]`` followed by w2 ``[H,I]``. Evicted slots go to a free list and
+    are reused; nothing is reallocated per miss.
+  * A miss is one ``hipMemcpyAsync`` (libmoe355 ``moe355_h2d_async``) from the
+    pinned pool into a slot on a side stream, with an event recorded behind it.
+    The host does not wait: compute streams wait on the slot's event right
+    before the kernels that read it (:meth:`prefetch_slots`), so the copy of
+    one expert overlaps whatever is already queued, e.g. the lookahead loads
+    of ``reserve`` overlap the current step's expert FFN.
+  * A freed slot remembers an event recorded on the compute stream at
+    eviction time; the next copy into that slot waits for it, so an in-flight
+    kernel never sees its weights overwritten.
+  * :meth:`prefetch_slots` hands the FFN a list of per-slot views, which
+    libmoe355 consumes as a pointer table: the reference's per-step
+    ``torch.stack`` of the banks (``_pack``) disappears from the hot path.
+    :meth:`prefetch` still returns stacked banks for callers that want them.
+
+With ``device="cpu"`` (unit tests) the "HBM" is host memory and resident
+entries are views of the host pool, as in the reference, where ``.to("cpu")``
+of a CPU tensor is the tensor itself.
+"""
+
+from __future__ import annotations
+
+import logging
+import time
+from collections import OrderedDict, deque
+from dataclasses import dataclass
+from typing import Deque, Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from reframework_amd import _capi, env
+
+logger = logging.getLogger(__name__)
+
+
+def _sym_int8_quantize(w: torch.Tensor) -> Tuple[torch.Tensor, float]:
+    """Symmetric per-tensor int8 codes and scale, ``w ~= q * scale``.
+
+    The largest magnitude maps to +-127; an all-zero tensor gets scale 1.0
+    (reference: offload_cache.py:58-72).
+    """
+    amax = float(w.abs().max().float()) if w.numel() else 0.0
+    if amax <= 0:
+        return torch.zeros_like(w, dtype=torch.int8), 1.0
+    scale = amax / 127.0
+    q = torch.clamp(torch.round(w.float() / scale), -127, 127).to(torch.int8).contiguous()
+    return q, float(scale)
+
+
+@dataclass
+class OffloadStats:
+    """Counters for observability / benchmarking."""
+
+    hits: int = 0
+    misses: int = 0
+    evictions: int = 0
+    transfers_bytes: int = 0
+    subs: int = 0
+    predicts: int = 0
+    inflight_bytes: int = 0
+
+    def reset(self) -> None:
+        for name in ("hits", "misses", "evictions", "transfers_bytes", "subs", "predicts",
+                     "inflight_bytes"):
+            setattr(self, name, 0)
+
+    def as_dict(self) -> dict:
+        return {
+            "hits": self.hits,
+            "misses": self.misses,
+            "evictions": self.evictions,
+            "subs": self.subs,
+            "predicts": self.predicts,
+            "inflight_bytes": self.inflight_bytes,
+            "transfer_mb": self.transfers_bytes / (1024 * 1024),
+        }
+
+
+class Prediction:
+    """Rolling routed-set history of one layer that drives the lookahead.
+
+    ``record_step`` on a decode step ages every seen expert, stores the routed
+    set, ranks the next step's experts and hands them to
+    :meth:`ExpertOffloadCache.reserve`; a prefill step clears the history
+    instead (reference: offload_cache.py:108-223).
+    """
+
+    def __init__(self, cache: "ExpertOffloadCache", window: int = 32) -> None:
+        self.cache = cache
+        self.window = max(1, int(window))
+        self._history: Deque[frozenset] = deque(maxlen=self.window)
+        self._age: Dict[int, int] = {}  # decode steps since the expert last routed
+
+    def reset(self) -> None:
+        self._history.clear()
+        self._age.clear()
+
+    def record_step(self, routed: Sequence[int], *, is_prefill: bool, forward_ms: float,
+                    inflight_bytes: float = 0.0) -> None:
+        routed_set = frozenset(int(i) for i in routed)
+        if is_prefill:
+            self.reset()
+            return
+        for e in self._age:
+            self._age[e] += 1
+        for e in routed_set:
+            self._age[e] = 0
+        self._history.append(routed_set)
+        predicted = self.predict_next()
+        if predicted:
+            self.cache.reserve(predicted, forward_ms=forward_ms, protect_current=routed,
+                               inflight_bytes=inflight_bytes)
+
+    def predict_next(self, limit: Optional[int] = None) -> List[int]:
+        """Non-resident experts ranked by window frequency, then recency, then id.
+
+        score = 1000 * (#steps routed in the window) + (window - age); an expert
+        never aged counts as age = window.
+        """
+        freq: Dict[int, int] = {}
+        for step in self._history:
+            for e in step:
+                freq[e] = freq.get(e, 0) + 1
+        if not freq:
+            return []
+        ranked = sorted(
+            freq, key=lambda e: (-(freq[e] * 1000 + self.window - self._age.get(e, self.window)), e)
+        )
+        out: List[int] = []
+        for e in ranked:
+            if e in self.cache._lru:
+                continue
+            out.append(e)
+            if limit is not None and len(out) >= limit:
+                break
+        return out
+
+
+class _Slot:
+    """One HBM buffer holding an expert's w1 then w2, plus its stream events."""
+
+    __slots__ = ("buf", "w1", "w2", "ready", "free_after", "refs")
+
+    def __init__(self, buf: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor) -> None:
+        self.buf = buf
+        self.w1 = w1
+        self.w2 = w2
+        self.ready: Optional[torch.cuda.Event] = None  # copy into the slot finished
+        self.free_after: Optional[torch.cuda.Event] = None  # last reader finished
+        self.refs = 0
+
+
+class ExpertOffloadCache:
+    """Pinned-host expert pool + an HBM LRU window of expert slots.
+
+    Parameters
+    ----------
+    device: where resident experts live (``cuda:N``; ``cpu`` for policy tests).
+    lru_capacity: resident expert slots kept (one slot = one expert's w1+w2).
+    dtype: storage dtype of the experts.
+    """
+
+    def __init__(self, device, lru_capacity: int, dtype: torch.dtype = torch.float16) -> None:
+        self.device = torch.device(device)
+        self.lru_capacity = int(lru_capacity)
+        self.dtype = dtype
+        self._host: List[Tuple[torch.Tensor, torch.Tensor]] = []
+        self._host_buf: Optional[torch.Tensor] = None
+        self._host_off: List[int] = []
+        self._pinned = False
+        self._lru: "OrderedDict[int, Tuple[torch.Tensor, torch.Tensor]]" = OrderedDict()
+        self.stats = OffloadStats()
+        self._next_reserve: frozenset = frozenset()
+        self.sim_table: Optional[torch.Tensor] = None
+        self._predictor: Optional[Prediction] = None
+        self._bw_gb_s: Optional[float] = None
+        self._bw_headroom: float = 0.9
+        self._cpu_split = False
+        self._int8_host: List[Tuple[torch.Tensor, torch.Tensor, float, float]] = []
+        # HBM slot pool (cuda devices only)
+        self._slot_of: Dict[int, _Slot] = {}
+        self._free_slots: List[_Slot] = []
+        self._n_slots = 0
+        self._copy_stream: Optional[torch.cuda.Stream] = None
+        self._n1 = 0
+        self._n2 = 0
+
+    # ----------------------------------------------------------------- factory
+    @classmethod
+    def from_config(cls, cfg, *, device=None, lru_capacity: Optional[int] = None):
+        return cls(
+            device=torch.device(device or cfg.device),
+            lru_capacity=lru_capacity if lru_capacity is not None else env.get_moe_cache_size(),
+            dtype=cfg.dtype,
+        )
+
+    # ------------------------------------------------------------------- setup
+    def load(self, experts: Sequence[Dict[str, torch.Tensor]]) -> None:
+        """Stage per-expert ``{"w1": [2I,H], "w2": [H,I]}`` in one host pool.
+
+        The pool is pinned (hipHostMalloc through torch) when a GPU is present,
+        else pageable, as on a CPU-only box in the reference.
+        """
+        w1s = [e["w1"].detach().to(dtype=self.dtype).contiguous() for e in experts]
+        w2s = [e["w2"].detach().to(dtype=self.dtype).contiguous() for e in experts]
+        total = sum(w.numel() for w in w1s) + sum(w.numel() for w in w2s)
+        try:
+            buf = torch.empty(total, dtype=self.dtype, pin_memory=True)
+            self._pinned = True
+        except (RuntimeError, AssertionError):
+            buf = torch.empty(total, dtype=self.dtype)
+            self._pinned = False
+        self._host_buf = buf
+        self._host, self._host_off = [], []
+        off = 0
+        for w1, w2 in zip(w1s, w2s):
+            self._host_off.append(off)
+            v1 = buf[off:off + w1.numel()].view_as(w1)
+            v1.copy_(w1)
+            off += w1.numel()
+            v2 = buf[off:off + w2.numel()].view_as(w2)
+            v2.copy_(w2)
+            off += w2.numel()
+            self._host.append((v1, v2))
+        del w1s, w2s
+        if self._host:
+            self._n1 = self._host[0][0].numel()
+            self._n2 = self._host[0][1].numel()
+        self._release_all()
+        self._lru = OrderedDict()
+        self.stats.reset()
+        logger.info("ExpertOffloadCache staged %d experts (%s) in %s host pool; LRU cap=%d",
+                    len(self._host), self.dtype, "pinned" if self._pinned else "pageable",
+                    self.lru_capacity)
+
+    @property
+    def num_experts(self) -> int:
+        return len(self._host)
+
+    @property
+    def cpu_split(self) -> bool:
+        return self._cpu_split
+
+    def resident_set(self) -> frozenset:
+        return frozenset(self._lru.keys())
+
+    def set_sim_table(self, sim: torch.Tensor) -> None:
+        E = len(self._host)
+        sim = torch.as_tensor(sim, dtype=torch.float32).cpu()
+        if tuple(sim.shape) != (E, E):
+            raise ValueError(f"sim_table shape {tuple(sim.shape)} != [E,E]=[{E},{E}]")
+        self.sim_table = sim
+
+    def attach_predictor(self, window: int = 32) -> None:
+        self._predictor = Prediction(self, window=window)
+        self._bw_headroom = max(0.05, min(1.0, env.get_moe_predict_headroom()))
+        self.measure_bandwidth()
+
+    def quantize_int8_host(self) -> None:
+        """Per-expert symmetric int8 host bank (reference: offload_cache.py:386-407)."""
+        if not self._host:
+            return
+        self._int8_host = []
+        for w1, w2 in self._host:
+            q1, s1 = _sym_int8_quantize(w1)
+            q2, s2 = _sym_int8_quantize(w2)
+            self._int8_host.append((q1, q2, s1, s2))
+        self._cpu_split = True
+
+    def cpu_banks(self, indices: Sequence[int]):
+        """Stacked int8 banks + scales of ``indices`` (ascending, at most
+        ``RE_MAX_PACK`` (default 4) of them) and their local index."""
+        uniq = sorted(set(int(i) for i in indices))
+        max_pack = env.get_max_pack(4)
+        if len(uniq) > max_pack:
+            uniq = uniq[:max_pack]
+        local_index = {idx: k for k, idx in enumerate(uniq)}
+        if not uniq:
+            H = self._host[0][0].shape[1]
+            I = self._host[0][1].shape[1]
+            return (torch.empty((0, 2 * I, H), dtype=torch.int8),
+                    torch.empty((0, H, I), dtype=torch.int8),
+                    torch.empty((0,), dtype=torch.float32),
+                    torch.empty((0,), dtype=torch.float32), local_index)
+        q1 = torch.stack([self._int8_host[i][0] for i in uniq], dim=0)
+        q2 = torch.stack([self._int8_host[i][1] for i in uniq], dim=0)
+        s1 = torch.tensor([self._int8_host[i][2] for i in uniq], dtype=torch.float32)
+        s2 = torch.tensor([self._int8_host[i][3] for i in uniq], dtype=torch.float32)
+        return q1, q2, s1, s2, local_index
+
+    def measure_bandwidth(self) -> Optional[float]:
+        """Host->HBM GB/s over the same pinned hipMemcpyAsync path ``_fill`` uses,
+        timed with HIP events; None without a GPU."""
+        if not torch.cuda.is_available() or self.device.type != "cuda":
+            return None
+        try:
+            n = 1 << 20
+            src = torch.empty(n, dtype=self.dtype, pin_memory=self._pinned)
+            dst = torch.empty(n, dtype=self.dtype, device=self.device)
+            cs = self._side_stream()
+            nbytes = n * src.element_size()
+            _capi.h2d_async(dst.data_ptr(), src.data_ptr(), nbytes, cs.cuda_stream)  # warm-up
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 3
+            start.record(cs)
+            for _ in range(reps):
+                _capi.h2d_async(dst.data_ptr(), src.data_ptr(), nbytes, cs.cuda_stream)
+            stop.record(cs)
+            stop.synchronize()
+            ms = start.elapsed_time(stop)
+            if ms > 0:
+                self._bw_gb_s = nbytes * reps / (ms / 1000.0) / 1e9
+            return self._bw_gb_s
+        except Exception as exc:  # best effort, like the reference's probe
+            logger.warning("host->HBM bandwidth measure failed: %s", exc)
+            return None
+
+    def reset_lru(self) -> None:
+        self._release_all()
+        self._lru = OrderedDict()
+        self._next_reserve = frozenset()
+        if self._predictor is not None:
+            self._predictor.reset()
+
+    # ------------------------------------------------------------------ access
+    def _admit(self, indices: Sequence[int]) -> List[int]:
+        """Residency bookkeeping shared by prefetch and prefetch_slots
+        (reference: offload_cache.py:478-506)."""
+        uniq = sorted(set(int(i) for i in indices if int(i) >= 0))
+        hits = sum(1 for i in uniq if i in self._lru)
+        logger.debug("[offload] prefetch: requested=%d unique=%d hit=%d miss=%d lru_size=%d",
+                     len(indices), len(uniq), hits, len(uniq) - hits, len(self._lru))
+        for idx in uniq:
+            if idx in self._lru:
+                self.stats.hits += 1
+            elif self._substitute(idx) is None:
+                self._fill(idx)
+            self._lru.move_to_end(idx)
+        self._evict(uniq, self._next_reserve - set(uniq))
+        return uniq
+
+    def prefetch(self, indices: Sequence[int]) -> Tuple[torch.Tensor, torch.Tensor, Dict[int, int]]:
+        """Bring ``indices`` resident; return stacked banks ``[N,2I,H]``,
+        ``[N,H,I]`` (ascending ids) and the global->row map."""
+        return self._pack(self._admit(indices))
+
+    def prefetch_slots(self, indices: Sequence[int]):
+        """Like :meth:`prefetch` but without the stacking copy: returns the
+        per-expert resident views (w1 list, w2 list) in ascending id order and
+        the global->row map, after making the current stream wait for any copy
+        still filling them."""
+        uniq = self._admit(indices)
+        self._wait_ready(uniq)
+        w1 = [self._lru[i][0] for i in uniq]
+        w2 = [self._lru[i][1] for i in uniq]
+        return w1, w2, {idx: k for k, idx in enumerate(uniq)}
+
+    def split_prefetch(self, indices: Sequence[int]):
+        """Split the routed set by residency: stacked banks of the hits and the
+        list of misses (reference: offload_cache.py:509-552)."""
+        uniq = sorted(set(int(i) for i in indices))
+        hits = [i for i in uniq if i in self._lru]
+        misses = [i for i in uniq if i not in self._lru]
+        for i in hits:
+            self._lru.move_to_end(i)
+            self.stats.hits += 1
+        if hits:
+            banks = self._pack(hits)
+        else:
+            w1r, w2r = self._host[0]
+            H, I = w1r.shape[1], w2r.shape[1]
+            banks = (torch.empty((0, 2 * I, H), dtype=self.dtype, device=self.device),
+                     torch.empty((0, H, I), dtype=self.dtype, device=self.device), {})
+        return banks, misses
+
+    def reactive_load(self, indices: Sequence[int]) -> None:
+        uniq = sorted(set(int(i) for i in indices))
+        for i in uniq:
+            if i not in self._lru:
+                self._fill(i)
+        self._evict(uniq, self._next_reserve - set(uniq))
+
+    def reserve(
+        self,
+        predicted: Sequence[int],
+        *,
+        forward_ms: float = 0.0,
+        bandwidth_gb_s: Optional[float] = None,
+        protect_current: Sequence[int] = (),
+        inflight_bytes: float = 0.0,
+    ) -> int:
+        """Load the predicted next-step experts, most likely first; return how
+        many were loaded (reference: offload_cache.py:569-643).
+
+        k is bounded by the byte budget ``bw * window * headroom - inflight``
+        (stop at the first expert that does not fit, once one is loaded) and by
+        evictable room: only experts outside ``protect_current`` and
+        ``predicted`` are evicted, and loading stops once the LRU is over
+        capacity with nothing stale left.
+        """
+        if not predicted or self.lru_capacity <= 0:
+            return 0
+        protect = {int(i) for i in protect_current} | {int(i) for i in predicted}
+        bw = bandwidth_gb_s if bandwidth_gb_s is not None else self._bw_gb_s
+        budget: Optional[float] = None
+        if forward_ms > 0 and bw and bw > 0:
+            budget = bw * 1e9 * (forward_ms / 1000.0) * self._bw_headroom
+            if inflight_bytes and inflight_bytes > 0:
+                budget = max(0.0, budget - inflight_bytes)
+                self.stats.inflight_bytes += int(inflight_bytes)
+        loaded: List[int] = []
+        for idx in (int(i) for i in predicted):
+            if idx in self._lru:
+                continue
+            w1, w2 = self._host[idx]
+            nbytes = (w1.numel() + w2.numel()) * self.dtype.itemsize
+            if budget is not None:
+                if nbytes > budget and loaded:
+                    break
+                budget -= nbytes
+            self._fill(idx)
+            self.stats.predicts += 1
+            loaded.append(idx)
+            self._evict(protect)
+            if len(self._lru) > self.lru_capacity:
+                break
+        self._next_reserve = frozenset(loaded)
+        return len(loaded)
+
+    # --------------------------------------------------------------- internals
+    def _side_stream(self) -> torch.cuda.Stream:
+        if self._copy_stream is None:
+            self._copy_stream = torch.cuda.Stream(device=self.device)  # default priority
+        return self._copy_stream
+
+    def _acquire_slot(self) -> _Slot:
+        if self._free_slots:
+            return self._free_slots.pop()
+        w1r, w2r = self._host[0]
+        buf = torch.empty(self._n1 + self._n2, dtype=self.dtype, device=self.device)
+        self._n_slots += 1
+        return _Slot(buf, buf[:self._n1].view(w1r.shape), buf[self._n1:].view(w2r.shape))
+
+    def _release(self, slot: _Slot) -> None:
+        slot.refs -= 1
+        if slot.refs > 0:
+            return
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        slot.free_after = ev
+        slot.ready = None
+        self._free_slots.append(slot)
+
+    def _release_all(self) -> None:
+        for slot in set(self._slot_of.values()):
+            slot.refs = 1
+            self._release(slot)
+        self._slot_of = {}
+
+    def _wait_ready(self, ids: Sequence[int]) -> None:
+        if self.device.type != "cuda":
+            return
+        stream = torch.cuda.current_stream(self.device)
+        for i in ids:
+            slot = self._slot_of.get(i)
+            if slot is not None and slot.ready is not None:
+                stream.wait_event(slot.ready)
+
+    def _fill(self, idx: int) -> None:
+        """Make expert ``idx`` resident (a miss): one async H2D into a slot."""
+        w1, w2 = self._host[idx]
+        nbytes = (w1.numel() + w2.numel()) * self.dtype.itemsize
+        if self.device.type == "cuda":
+            slot = self._acquire_slot()
+            cs = self._side_stream()
+            if slot.free_after is not None:
+                cs.wait_event(slot.free_after)
+            src = self._host_buf.data_ptr() + self._host_off[idx] * self._host_buf.element_size()
+            _capi.h2d_async(slot.buf.data_ptr(), src, nbytes, cs.cuda_stream)
+            ev = torch.cuda.Event()
+            ev.record(cs)
+            slot.ready = ev
+            slot.refs = 1
+            self._slot_of[idx] = slot
+            self._lru[idx] = (slot.w1, slot.w2)
+        else:
+            self._lru[idx] = (w1.to(device=self.device), w2.to(device=self.device))
+        self.stats.transfers_bytes += nbytes
+        self.stats.misses += 1
+
+    def _evict(self, hard_protect: Sequence[int], soft_protect: Sequence[int] = ()) -> None:
+        """Evict down to ``lru_capacity``: stale entries first, then soft ones,
+        never hard ones. ``lru`` picks the oldest; ``least_stale`` picks the
+        largest routing age (never seen = window), oldest on ties."""
+        hard = {int(i) for i in hard_protect}
+        soft = {int(i) for i in soft_protect} - hard
+        predictor = self._predictor
+        if env.get_moe_cache_policy() == "least_stale" and predictor is not None:
+            age, window = predictor._age, predictor.window
+
+            def victim_of(cands: List[int]) -> Optional[int]:
+                best, best_age = None, -1
+                for i in cands:  # LRU order, oldest first: strict '>' keeps the oldest on ties
+                    a = age.get(i, window)
+                    if a > best_age:
+                        best, best_age = i, a
+                return best
+        else:
+            def victim_of(cands: List[int]) -> Optional[int]:
+                return cands[0] if cands else None
+
+        while len(self._lru) > self.lru_capacity:
+            victim = victim_of([i for i in self._lru if i not in hard and i not in soft])
+            if victim is None:
+                victim = victim_of([i for i in self._lru if i in soft])
+            if victim is None:
+                return
+            self._lru.pop(victim)
+            slot = self._slot_of.pop(victim, None)
+            if slot is not None:
+                self._release(slot)
+            self.stats.evictions += 1
+
+    def _substitute(self, idx: int) -> Optional[int]:
+        """Serve a miss with the most similar resident expert (argmax of the
+        similarity row over residents, first index on ties)."""
+        if self.sim_table is None or idx in self._lru:
+            return None
+        residents = [i for i in self._lru if i != idx]
+        if not residents:
+            return None
+        row = self.sim_table[idx]
+        cand = torch.full((self.num_experts,), float("-inf"), dtype=row.dtype)
+        cand[residents] = row[residents]
+        best = int(cand.argmax().item())
+        self.stats.subs += 1
+        self._lru[idx] = self._lru[best]
+        slot = self._slot_of.get(best)
+        if slot is not None:
+            slot.refs += 1
+            self._slot_of[idx] = slot
+        return best
+
+    def _pack(self, uniq: Sequence[int]) -> Tuple[torch.Tensor, torch.Tensor, Dict[int, int]]:
+        local_index = {idx: k for k, idx in enumerate(uniq)}
+        self._wait_ready(uniq)
+        w1 = torch.stack([self._lru[i][0] for i in uniq], dim=0)
+        w2 = torch.stack([self._lru[i][1] for i in uniq], dim=0)
+        return w1, w2, local_index
+
+    # ------------------------------------------------------------------- stats
+    def report(self) -> str:
+        s = self.stats.as_dict()
+        return (f"offload: hit={s['hits']} miss={s['misses']} sub={s['subs']} "
+                f"pred={s['predicts']} evict={s['evictions']} transfer={s['transfer_mb']:.1f}MB")
+
+
+__all__ = ["ExpertOffloadCache", "OffloadStats", "Prediction"]

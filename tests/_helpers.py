@@ -1,0 +1,61 @@
+"""Helpers shared by the GPU parity tests (not collected: no test_ prefix)."""
+
+from __future__ import annotations
+
+from typing import List, Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from reframework_amd import _capi
+from reframework_amd.moe.fused import run_experts
+
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+ROUND = {torch.bfloat16: 1, torch.float16: 2, torch.float32: 3}
+
+
+def banner(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+
+
+def make_bank(E: int, H: int, I: int, dtype: torch.dtype, seed: int, scale: float = 0.05):
+    """Per-expert CPU tensors w1 [2I,H], w2 [H,I] of `dtype`."""
+    g = torch.Generator().manual_seed(seed)
+    w1 = [(torch.randn(2 * I, H, generator=g) * scale).to(dtype) for _ in range(E)]
+    w2 = [(torch.randn(H, I, generator=g) * scale).to(dtype) for _ in range(E)]
+    return w1, w2
+
+
+def skewed_ids(T: int, K: int, E: int, seed: int, skew: float = 1.0) -> np.ndarray:
+    """[T,K] distinct expert ids per token with a Zipf-like popularity."""
+    rng = np.random.default_rng(seed)
+    p = (np.arange(1, E + 1, dtype=np.float64)) ** (-skew)
+    p /= p.sum()
+    perm = rng.permutation(E)
+    out = np.empty((T, K), dtype=np.int64)
+    for t in range(T):
+        out[t] = perm[rng.choice(E, size=K, replace=False, p=p)]
+    return out
+
+
+def gpu_fused(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch.Tensor],
+              topk_w: np.ndarray, ids: np.ndarray, act: int = 0,
+              expert_map: Optional[List[int]] = None, ids64: bool = False) -> torch.Tensor:
+    """libmoe355 fused_experts on cuda:0 tensors; returns the device output."""
+    dev = torch.device("cuda:0")
+    xd = x.to(dev).contiguous()
+    w1d = [w.to(dev).contiguous() for w in w1]
+    w2d = [w.to(dev).contiguous() for w in w2]
+    idt = torch.from_numpy(np.ascontiguousarray(ids)).to(dev)
+    idt = idt.long() if ids64 else idt.int()
+    tw = torch.from_numpy(np.ascontiguousarray(topk_w, dtype=np.float32)).to(dev)
+    I = w1[0].shape[0] // 2
+    out = run_experts(xd, [w.data_ptr() for w in w1d], [w.data_ptr() for w in w2d], I, tw, idt,
+                      act, expert_map=expert_map)
+    torch.cuda.synchronize()
+    return out
+
+
+def read_ws(plan: _capi.Plan, ws: torch.Tensor, off: int, n: int) -> np.ndarray:
+    """int32 array of n entries at byte offset `off` of the workspace."""
+    return ws[off:off + 4 * n].cpu().view(torch.int32).numpy().copy()
