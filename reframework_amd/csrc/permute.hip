@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
 
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
   for (int r = 0; r < kRounds; ++r) {
-    for (int i = tid; i < kWaves * a.E; i += kThreads) (&wave_cnt[0][0])[i] = 0;
+    for (int i = tid; i < kWaves * a.E; i += kThreads) wave_cnt[i / a.E][i % a.E] = 0;
     __syncthreads();
     const int slot = b * kPermuteChunk + r * kThreads + tid;
     const int e = slot < a.R ? slot_expert(a, slot) : -1;
