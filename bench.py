@@ -39,10 +39,13 @@ def parse():
     ap.add_argument("--tokens", type=int, default=4096)
     ap.add_argument("--decode", type=str, default="1,16,256",
                     help="comma-separated token counts reported beside the headline ('' = none)")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=256)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", type=str, default="",
-                    help="profiling aid: run only this many tokens, no JSON extras")
+    ap.add_argument("--profile", type=int, default=0,
+                    help="profiling aid: run only the layer at this many tokens")
+    ap.add_argument("--copy-calib", type=int, default=0,
+                    help="profiling aid: device-to-device copies of this many bytes, the "
+                         "known-size reference for HBM byte counters")
     return ap.parse_args()
 
 
@@ -185,12 +188,19 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
+    if args.copy_calib:
+        src = torch.empty(args.copy_calib, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(max(1, args.steps)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": args.copy_calib, "copies": max(1, args.steps)}))
+        return
     layer = Layer(dev)
 
-    if args.only:
-        T = int(args.only)
-        m = measure(layer, T, args.steps, args.warmup)
-        print(json.dumps({"tokens": T, **m}), flush=True)
+    if args.profile:
+        m = measure(layer, args.profile, args.steps, args.warmup)
+        print(json.dumps({"tokens": args.profile, **m}), flush=True)
         return
 
     T = args.tokens
