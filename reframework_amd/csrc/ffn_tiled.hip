@@ -16,10 +16,9 @@
 //            straight from x through row_src (no permuted copy of x).
 //   down:    256 rows of w2 against the permuted inter rows, fp32 partials
 //            per K-split into y.
-// LDS rows are 128 B; the 16-byte chunk c of row r is stored at chunk c^(r&7),
-// which makes both the staging writes and the MFMA operand reads conflict-free.
-// Global loads are staged through registers and double-buffered in LDS (2 x
-// 64 KB), one barrier per k step.
+// LDS rows are 128 B, XOR-swizzled in 16-byte chunks (swz) so that the staging
+// writes and the MFMA operand reads are bank-conflict free. Global loads are
+// staged through registers and double-buffered in LDS (2 x 64 KB).
 #include "common.h"
 
 namespace moe355 {
@@ -35,6 +34,15 @@ constexpr int kPasses = kTileW / kRowsPerPass;        // 8
 constexpr int kRegionBytes = kTileW * kRowBytes;      // 32 KB
 constexpr int kStageBytes = 2 * kRegionBytes;         // weights + tokens
 constexpr int kLdsBytes = 2 * kStageBytes;            // double buffered
+
+// Physical 16-byte chunk of logical chunk c in LDS row r. Rows are 128 B (8
+// chunks). XOR with r&7 spreads 8 consecutive rows over all 8 chunk columns,
+// and the extra bit (r>>3)&1 keeps rows r and r+8, which share a bank set on a
+// 64-bank LDS, in different columns: any 16 consecutive rows read at one
+// logical chunk hit 16 distinct 16-byte bank groups.
+__device__ __forceinline__ uint32_t swz(int c, int r) {
+  return static_cast<uint32_t>(c ^ (r & 7) ^ ((r >> 3) & 1));
+}
 
 template <typename T>
 struct Mfma32;
@@ -98,7 +106,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
     const int xrow = kGateUp ? a.row_src[prow] : prow - row0;
     xoff[p] = static_cast<uint32_t>(xrow) * static_cast<uint32_t>(ld * 2) + chunk * 16;
   }
-  const uint32_t st_off = lrow * kRowBytes + ((chunk ^ (lrow & 7)) << 4);
+  const uint32_t st_off = lrow * kRowBytes + (swz(chunk, lrow) << 4);
 
   // MFMA operand rows of this wave inside the stage.
   const int lr = lane & 31, kh = lane >> 5;
@@ -113,6 +121,11 @@ void ffn_tiled_kernel(const FfnArgs a) {
     arow[b] = (rb + lr) * kRowBytes;
     brow[b] = kRegionBytes + (wave_t * 128 + b * 32 + lr) * kRowBytes;
   }
+  // Swizzled 16-byte chunk offsets of the 4 k16 sub-steps for this lane
+  // (operand rows start at multiples of 32, so row bits 0..3 are lr's).
+  uint32_t coff[kBK / 16];
+#pragma unroll
+  for (int ks = 0; ks < kBK / 16; ++ks) coff[ks] = swz(ks * 2 + kh, lr) << 4;
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -138,30 +151,53 @@ void ffn_tiled_kernel(const FfnArgs a) {
       *reinterpret_cast<u32x4*>(st + kRegionBytes + p * kRowsPerPass * kRowBytes + st_off) = xr[p];
     }
   };
+  auto read_frags = [&](const uint8_t* st, int ks, u32x4* af, u32x4* bf) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      af[b] = *reinterpret_cast<const u32x4*>(st + arow[b] + coff[ks]);
+      bf[b] = *reinterpret_cast<const u32x4*>(st + brow[b] + coff[ks]);
+    }
+  };
 
+  // Pipeline: LDS stage kt is consumed while stage kt+1 (already in
+  // registers) is written to the other LDS buffer during sub-step 1, one LDS
+  // write and one global load of stage kt+2 (clamped to the last stage, so the
+  // loop has no branches) between consecutive MFMAs. Operand fragments of
+  // sub-step ks+1 are read while sub-step ks's 16 MFMAs run; scheduling
+  // fences keep the compiler from pulling those reads in front of the MFMAs
+  // they are meant to overlap. One barrier per stage.
   load_stage(0);
   store_stage(0);
+  load_stage(min(1, nk - 1));
   __syncthreads();
 
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) load_stage(kt + 1);
     const uint8_t* st = lds + cur * kStageBytes;
+    u32x4 fa[2][4], fb[2][4];
+    read_frags(st, 0, fa[0], fb[0]);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      const uint32_t coff = static_cast<uint32_t>(((ks * 2 + kh) ^ (lr & 7)) << 4);
-      u32x4 af[4], bfr[4];
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        af[b] = *reinterpret_cast<const u32x4*>(st + arow[b] + coff);
-        bfr[b] = *reinterpret_cast<const u32x4*>(st + brow[b] + coff);
+      if (ks + 1 < kBK / 16) read_frags(st, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks == 1) {
+        store_stage(cur ^ 1);
+        load_stage(min(kt + 2, nk - 1));
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = Mfma32<T>::mma(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = Mfma32<T>::mma(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
+      if (ks == 1) {
+        for (int q = 0; q < 16; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (kt + 1 < nk) store_stage(cur ^ 1);
     __syncthreads();
   }
 
