@@ -12,28 +12,36 @@ namespace {
 
 constexpr int kThreads = 256;
 
-template <typename OutT>
+// Workgroup (t, hb) produces out[t, hb*1024 .. +1024): each thread one
+// 16-byte group of 4 features. The K slots' rows and weights are uniform per
+// workgroup; the S split partials of every slot are issued as independent
+// loads, so a decode-size combine costs one round trip, not S*K of them.
+template <typename OutT, int S>
 __global__ __launch_bounds__(kThreads) void combine_kernel(const CombineArgs a) {
   const int t = blockIdx.x;
+  const int h = (blockIdx.y * kThreads + threadIdx.x) * 4;
+  if (h >= a.H) return;
   const size_t plane = static_cast<size_t>(a.R) * a.H;
-  for (int h = threadIdx.x * 4; h < a.H; h += kThreads * 4) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < a.K; ++k) {
-      const int row = a.slot_to_row[t * a.K + k];
-      if (row < 0) continue;
-      const float w = a.topk_w[t * a.K + k];
-      const float* yr = a.y + static_cast<size_t>(row) * a.H + h;
-      f32x4 ys = *reinterpret_cast<const f32x4*>(yr);
-      for (int s = 1; s < a.splits; ++s) ys += *reinterpret_cast<const f32x4*>(yr + s * plane);
-      acc += w * ys;
-    }
-    if (a.accumulate) {
-      float* o = static_cast<float*>(a.out) + static_cast<size_t>(t) * a.H + h;
-      *reinterpret_cast<f32x4*>(o) = *reinterpret_cast<const f32x4*>(o) + acc;
-    } else {
-      store4<OutT>(static_cast<OutT*>(a.out) + static_cast<size_t>(t) * a.H + h, acc[0], acc[1],
-                   acc[2], acc[3]);
-    }
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < a.K; ++k) {
+    const int row = a.slot_to_row[t * a.K + k];
+    if (row < 0) continue;
+    const float w = a.topk_w[t * a.K + k];
+    const float* yr = a.y + static_cast<size_t>(row) * a.H + h;
+    f32x4 part[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) part[s] = *reinterpret_cast<const f32x4*>(yr + s * plane);
+    f32x4 ys = part[0];
+#pragma unroll
+    for (int s = 1; s < S; ++s) ys += part[s];
+    acc += w * ys;
+  }
+  if (a.accumulate) {
+    float* o = static_cast<float*>(a.out) + static_cast<size_t>(t) * a.H + h;
+    *reinterpret_cast<f32x4*>(o) = *reinterpret_cast<const f32x4*>(o) + acc;
+  } else {
+    store4<OutT>(static_cast<OutT*>(a.out) + static_cast<size_t>(t) * a.H + h, acc[0], acc[1],
+                 acc[2], acc[3]);
   }
 }
 
@@ -44,18 +52,27 @@ __global__ __launch_bounds__(kThreads) void cast_kernel(const float* src, OutT* 
     dst[i] = from_f32<OutT>(src[i]);
 }
 
+template <typename OutT>
+hipError_t launch_combine_t(const CombineArgs& a, hipStream_t s) {
+  const dim3 grid(a.T, (a.H + kThreads * 4 - 1) / (kThreads * 4)), block(kThreads);
+  switch (a.splits) {
+    case 1: combine_kernel<OutT, 1><<<grid, block, 0, s>>>(a); break;
+    case 2: combine_kernel<OutT, 2><<<grid, block, 0, s>>>(a); break;
+    case 4: combine_kernel<OutT, 4><<<grid, block, 0, s>>>(a); break;
+    case 8: combine_kernel<OutT, 8><<<grid, block, 0, s>>>(a); break;
+    case 16: combine_kernel<OutT, 16><<<grid, block, 0, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_combine(const CombineArgs& a, int out_dtype, hipStream_t s) {
   if (a.T == 0) return hipSuccess;
-  const dim3 grid(a.T), block(kThreads);
-  if (a.accumulate || out_dtype == MOE355_F32)
-    combine_kernel<float><<<grid, block, 0, s>>>(a);
-  else if (out_dtype == MOE355_BF16)
-    combine_kernel<bf16><<<grid, block, 0, s>>>(a);
-  else
-    combine_kernel<f16><<<grid, block, 0, s>>>(a);
-  return hipGetLastError();
+  if (a.accumulate || out_dtype == MOE355_F32) return launch_combine_t<float>(a, s);
+  if (out_dtype == MOE355_BF16) return launch_combine_t<bf16>(a, s);
+  return launch_combine_t<f16>(a, s);
 }
 
 hipError_t launch_cast_f32(const float* src, void* dst, size_t n, int dtype, hipStream_t s) {

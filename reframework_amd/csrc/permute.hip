@@ -49,6 +49,9 @@ __global__ __launch_bounds__(kThreads) void count_kernel(const PermuteArgs a) {
   for (int e = tid; e < a.E; e += kThreads) a.block_counts[b * a.E + e] = hist[e];
 }
 
+// kSingle: all slots fit one block (decode sizes); the block counts them itself
+// and the separate count launch is skipped.
+template <bool kSingle>
 __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) {
   __shared__ int base[kMaxExperts];     // first row of this block's slots of expert e
   __shared__ int start[kMaxExperts + 1];  // expert_offsets
@@ -59,15 +62,31 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
   const int b = blockIdx.x, tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wave = tid / kWave;
 
-  for (int e = tid; e < a.E; e += kThreads) {
-    int tot = 0, pre = 0;
-    for (int bb = 0; bb < a.n_blocks; ++bb) {
-      const int c = a.block_counts[bb * a.E + e];
-      tot += c;
-      if (bb < b) pre += c;
+  if (kSingle) {
+    for (int e = tid; e < a.E; e += kThreads) {
+      total[e] = 0;
+      base[e] = 0;
     }
-    total[e] = tot;
-    base[e] = pre;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      const int slot = r * kThreads + tid;
+      if (slot < a.R) {
+        const int e = slot_expert(a, slot);
+        if (e >= 0) atomicAdd(&total[e], 1);
+      }
+    }
+  } else {
+    for (int e = tid; e < a.E; e += kThreads) {
+      int tot = 0, pre = 0;
+      for (int bb = 0; bb < a.n_blocks; ++bb) {
+        const int c = a.block_counts[bb * a.E + e];
+        tot += c;
+        if (bb < b) pre += c;
+      }
+      total[e] = tot;
+      base[e] = pre;
+    }
   }
   __syncthreads();
   if (tid == 0) {
@@ -144,10 +163,14 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
 
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s) {
   if (a.R == 0) return hipSuccess;
+  if (a.n_blocks == 1) {
+    scatter_kernel<true><<<dim3(1), dim3(kThreads), 0, s>>>(a);
+    return hipGetLastError();
+  }
   count_kernel<<<dim3(a.n_blocks), dim3(kThreads), 0, s>>>(a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  scatter_kernel<<<dim3(a.n_blocks), dim3(kThreads), 0, s>>>(a);
+  scatter_kernel<false><<<dim3(a.n_blocks), dim3(kThreads), 0, s>>>(a);
   return hipGetLastError();
 }
 

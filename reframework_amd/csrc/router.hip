@@ -1,4 +1,4 @@
-// Router GEMV + softmax + top-k, one workgroup per token.
+// Router GEMV + softmax + top-k, one workgroup per 1-8 tokens.
 //
 // Replaces FusedMoE.route (reframework/moe/moe_layer.py:320-344): the router
 // F.linear (:324) and torch_fused_topk (reframework/moe/fused.py:32-46). The
@@ -15,7 +15,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kExpGroup = 8;   // experts accumulated per pass over the row
-constexpr int kMaxChunks = 8;  // 16-byte chunks of x kept in registers per thread
 constexpr int kMaxPerLane = kMaxExperts / kWave;
 
 // Softmax + top-k + renormalisation of one token's logits by one wave.
@@ -107,72 +106,100 @@ __device__ void wave_topk(const float* lg, int E, int K, int renorm, int kmin, f
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
-  __shared__ float part[kThreads / kWave][kMaxExperts];
-  __shared__ float lg[kMaxExperts];
-  __shared__ float psel[kMaxExperts];
-  __shared__ int32_t isel[kMaxExperts];
+// Wave-wide sum of V values per lane in log2(64) shuffle rounds, returning
+// one total per lane: while more than one value is left, each round sends
+// half of the lane's values to its partner and keeps the other half, so the V
+// sums finish after 63 shuffles in total instead of 6*V. Lane l ends up with
+// the sum of value index l >> (6 - log2 V).
+template <int V>
+__device__ __forceinline__ float transpose_reduce(float (&v)[V], int lane) {
+#pragma unroll
+  for (int r = 0; r < 6; ++r) {
+    const int d = 32 >> r;
+    const int n = (V >> r) > 1 ? (V >> r) : 1;
+    if (n > 1) {
+      const bool up = (lane & d) != 0;
+#pragma unroll
+      for (int i = 0; i < n / 2; ++i) {
+        const float send = up ? v[i] : v[i + n / 2];
+        const float keep = up ? v[i + n / 2] : v[i];
+        v[i] = keep + __shfl_xor(send, d, kWave);
+      }
+    } else {
+      v[0] += __shfl_xor(v[0], d, kWave);
+    }
+  }
+  return v[0];
+}
 
+constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
+
+// TB tokens per workgroup share every gate-row load (the gate matrix is read
+// once per TB tokens from L2). Per thread: TB x 8 partial dot products over its
+// slice of H, folded across the wave by transpose_reduce and across the 4
+// waves through LDS.
+template <typename T, int TB>
+__global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
   constexpr int V = Vec16<T>::N;
-  const int t = blockIdx.x;
+  constexpr int NV = TB * kExpGroup;     // partial sums per thread (<= 64)
+  constexpr int SH = 6 - log2i(NV);      // lane bits below the value index
+  __shared__ float part[kThreads / kWave][64];
+  __shared__ float lg[TB][kMaxExperts];
+  __shared__ float psel[kThreads / kWave][kMaxExperts];
+  __shared__ int32_t isel[kThreads / kWave][kMaxExperts];
+
+  const int t0 = blockIdx.x * TB;
+  const int ntok = min(TB, a.T - t0);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int nch = a.H / V;
-  const T* xr = static_cast<const T*>(a.x) + static_cast<size_t>(t) * a.H;
+  const T* x = static_cast<const T*>(a.x) + static_cast<size_t>(t0) * a.H;
   const T* gate = static_cast<const T*>(a.gate);
 
-  u32x4 xraw[kMaxChunks];
-#pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    const int c = tid + kThreads * i;
-    xraw[i] = c < nch ? *reinterpret_cast<const u32x4*>(xr + c * V) : u32x4{0, 0, 0, 0};
-  }
-
   for (int e0 = 0; e0 < a.E; e0 += kExpGroup) {
-    float acc[kExpGroup];
+    float acc[NV];
 #pragma unroll
-    for (int j = 0; j < kExpGroup; ++j) acc[j] = 0.f;
+    for (int i = 0; i < NV; ++i) acc[i] = 0.f;
+    for (int c = tid; c < nch; c += kThreads) {
+      float xf[TB][V];
 #pragma unroll
-    for (int i = 0; i < kMaxChunks; ++i) {
-      const int c = tid + kThreads * i;
-      if (c < nch) {
-        float xf[V];
-        Vec16<T>::unpack(xraw[i], xf);
+      for (int t = 0; t < TB; ++t) {
+        const u32x4 raw = t < ntok ? *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(t) * a.H + c * V)
+                                   : u32x4{0, 0, 0, 0};
+        Vec16<T>::unpack(raw, xf[t]);
+      }
 #pragma unroll
-        for (int j = 0; j < kExpGroup; ++j) {
-          const int e = e0 + j;
-          if (e < a.E) {
-            const u32x4 g =
-                *reinterpret_cast<const u32x4*>(gate + static_cast<size_t>(e) * a.H + c * V);
-            float gf[V];
-            Vec16<T>::unpack(g, gf);
+      for (int j = 0; j < kExpGroup; ++j) {
+        const int e = e0 + j;
+        if (e < a.E) {
+          float gf[V];
+          Vec16<T>::unpack(*reinterpret_cast<const u32x4*>(gate + static_cast<size_t>(e) * a.H + c * V), gf);
 #pragma unroll
-            for (int q = 0; q < V; ++q) acc[j] = fmaf(xf[q], gf[q], acc[j]);
-          }
+          for (int t = 0; t < TB; ++t)
+#pragma unroll
+            for (int q = 0; q < V; ++q) acc[t * kExpGroup + j] = fmaf(xf[t][q], gf[q], acc[t * kExpGroup + j]);
         }
       }
     }
-#pragma unroll
-    for (int j = 0; j < kExpGroup; ++j) {
-      const float r = wave_sum(acc[j]);
-      if (lane == 0 && e0 + j < a.E) part[wave][e0 + j] = r;
+    const float r = transpose_reduce<NV>(acc, lane);
+    if ((lane & ((1 << SH) - 1)) == 0) part[wave][lane >> SH] = r;
+    __syncthreads();
+    for (int i = tid; i < NV; i += kThreads) {
+      const int t = i / kExpGroup, e = e0 + i % kExpGroup;
+      if (t < ntok && e < a.E) {
+        float l = (part[0][i] + part[1][i]) + (part[2][i] + part[3][i]);
+        if (a.round_logits) l = to_f32(from_f32<T>(l));
+        if (a.bias) l += a.bias[e];
+        lg[t][e] = l;
+        if (a.logits_out) a.logits_out[static_cast<size_t>(t0 + t) * a.E + e] = l;
+      }
     }
+    __syncthreads();
   }
-  __syncthreads();
 
-  for (int e = tid; e < a.E; e += kThreads) {
-    float l = (part[0][e] + part[1][e]) + (part[2][e] + part[3][e]);
-    if (a.round_logits) l = to_f32(from_f32<T>(l));
-    if (a.bias) l += a.bias[e];
-    lg[e] = l;
-    if (a.logits_out) a.logits_out[static_cast<size_t>(t) * a.E + e] = l;
-  }
-  __syncthreads();
-
-  if (wave == 0)
-    wave_topk(lg, a.E, a.K, a.renormalize, a.entropy_k_min, psel, isel,
-              a.topk_w + static_cast<size_t>(t) * a.K, a.topk_ids + static_cast<size_t>(t) * a.K,
-              lane);
+  for (int t = wave; t < ntok; t += kThreads / kWave)
+    wave_topk(lg[t], a.E, a.K, a.renormalize, a.entropy_k_min, psel[wave], isel[wave],
+              a.topk_w + static_cast<size_t>(t0 + t) * a.K,
+              a.topk_ids + static_cast<size_t>(t0 + t) * a.K, lane);
 }
 
 // One wave per token on given fp32 logits.
@@ -189,16 +216,23 @@ __global__ __launch_bounds__(kThreads) void topk_logits_kernel(const RouterArgs 
 
 }  // namespace
 
+template <typename T>
+hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
+  const dim3 block(kThreads);
+  if (a.T >= 1024)
+    router_kernel<T, 8><<<dim3((a.T + 7) / 8), block, 0, s>>>(a);
+  else if (a.T >= 256)
+    router_kernel<T, 4><<<dim3((a.T + 3) / 4), block, 0, s>>>(a);
+  else
+    router_kernel<T, 1><<<dim3(a.T), block, 0, s>>>(a);
+  return hipGetLastError();
+}
+
 hipError_t launch_router(const RouterArgs& a, int dtype, hipStream_t s) {
   if (a.T == 0) return hipSuccess;
-  const dim3 grid(a.T), block(kThreads);
-  if (dtype == MOE355_BF16)
-    router_kernel<bf16><<<grid, block, 0, s>>>(a);
-  else if (dtype == MOE355_F16)
-    router_kernel<f16><<<grid, block, 0, s>>>(a);
-  else
-    router_kernel<float><<<grid, block, 0, s>>>(a);
-  return hipGetLastError();
+  if (dtype == MOE355_BF16) return launch_router_t<bf16>(a, s);
+  if (dtype == MOE355_F16) return launch_router_t<f16>(a, s);
+  return launch_router_t<float>(a, s);
 }
 
 hipError_t launch_topk_from_logits(const RouterArgs& a, hipStream_t s) {
