@@ -93,7 +93,7 @@ int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* 
   const bool tiled_ok = mfma && H % 256 == 0 && I % 128 == 0 &&
                         static_cast<long long>(T) * H * esz < (1ll << 32) &&
                         2ll * I * H * esz < (1ll << 32);
-  const bool skinny_ok = mfma && H % 32 == 0 && I % 32 == 0;
+  const bool skinny_ok = mfma && H % 128 == 0 && I % 128 == 0;
   if (tiled_ok && avg > 32) {
     p->path = MOE355_PATH_MFMA_TILED;
     p->tile_rows = 256;
@@ -109,10 +109,11 @@ int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* 
                        : 0;
   p->down_splits = 1;
   if (p->path == MOE355_PATH_MFMA_SKINNY) {
-    // Spread the down projection (H/16 row groups per tile) over >= 4096 waves.
+    // Spread the down projection (H/16 row groups per tile) over >= 4096 waves;
+    // each split covers a multiple of the kernel's 128-element k step.
     const long long waves = static_cast<long long>(H / 16) * (p->max_tiles > 0 ? p->max_tiles : 1);
     int s = 1;
-    while (s < 16 && waves * s < 4096 && (I / 32) % (2 * s) == 0) s *= 2;
+    while (s < 16 && waves * s < 4096 && (I / 128) % (2 * s) == 0) s *= 2;
     p->down_splits = s;
   }
 

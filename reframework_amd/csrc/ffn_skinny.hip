@@ -1,23 +1,31 @@
 // Grouped expert FFN for decode-sized groups (a few tokens per expert).
 //
 // Replaces the same per-expert GEMMs as the tiled kernel
-// (reframework/moe/fused.py:76-83) when each expert sees <= 16-ish rows. Then
-// the layer is a weight stream: every routed expert's 3*H*I weights are read
-// once and each weight meets only a handful of tokens, so the kernel is built
-// for HBM bandwidth, not for MFMA reuse.
+// (reframework/moe/fused.py:76-83) when each expert sees <= ~32 rows. Then the
+// layer is a weight stream: every routed expert's 3*H*I weights are read once
+// and meet only a handful of tokens, so the kernel is built for HBM bandwidth.
 //
 // Each wave owns 16 weight rows (gate_up: 16 gate rows + the 16 matching up
-// rows) of one expert and one 16-token tile, and walks K in 32-element steps
-// with v_mfma_f32_16x16x32 (weights on the M side, tokens on the N side). The
-// weight operand is loaded from HBM straight into the MFMA registers: lane l
-// reads 16 bytes of row l%16 at k offset 8*(l/16), so a wave step touches 64
-// contiguous bytes of each of 16 rows and consecutive steps finish the 128-byte
-// lines. Loads are unrolled 8 steps deep so every wave keeps 16-24 KB in
-// flight; with several waves per SIMD the CU sustains the HBM stream without
-// LDS. The token operand (a few KB per expert) is re-read from L1/L2.
-// gate_up fuses the gated activation; down writes fp32 partials per K-split,
-// which the combine kernel sums, so the short down projection of a decode step
-// still spreads over every CU.
+// rows) of one expert and one 16-token tile, and multiplies with
+// v_mfma_f32_16x16x32 (weights on the M side, tokens on the N side).
+//
+// Weight loads are shaped for DRAM, not for the MFMA operand: one load
+// instruction reads 4 rows x 256 contiguous bytes (16 lanes per row), so a
+// 128-element k step of 16 rows is 4 instructions. The wave stages them in its
+// own slice of LDS, each row's 16-byte chunks XOR-permuted by the row index, and
+// reads them back in the MFMA layout (lane l: row l%16, chunk 4s + l/16), which
+// the permutation makes bank-conflict free. The 16 lanes of one row fetch the
+// row's chunks in permuted order, so each row still reads one contiguous
+// 256-byte run. Loading the operand directly in MFMA layout would split every
+// instruction into 16 separate 64-byte pieces, which measured ~5 TB/s instead of
+// ~7 TB/s on MI355X.
+//
+// Steps are prefetched D deep in registers, LDS slices are double-buffered, and
+// each wave starts its K walk at a rotated step so that concurrent waves hit
+// different HBM channels. No workgroup barrier is needed: every wave only
+// reads what it wrote. gate_up fuses the gated activation; down writes fp32
+// partials per K-split, which the combine kernel sums, so the short down
+// projection of a decode step still spreads over every CU.
 #include "common.h"
 
 namespace moe355 {
@@ -26,8 +34,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 constexpr int kRows = 16;
-constexpr int kStep = 32;
-constexpr int kUnroll = 8;
+constexpr int kKS = 128;                 // k elements per step
+constexpr int kRowStepBytes = kKS * 2;   // 256 bytes of one row per step
+constexpr int kOperandBytes = kRows * kRowStepBytes;  // 4 KB
 
 template <typename T>
 struct Mfma16;
@@ -58,6 +67,11 @@ __device__ __forceinline__ u32x4 load16_stream(const void* p) {
 
 template <typename T, bool kGateUp>
 __global__ __launch_bounds__(kThreads) void ffn_skinny_kernel(const FfnArgs a) {
+  constexpr int NOP = kGateUp ? 2 : 1;   // weight operands: gate (+ up)
+  constexpr int D = kGateUp ? 2 : 4;     // steps in flight per wave
+  constexpr int kSliceBytes = NOP * kOperandBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kWavesPerBlock][2][kSliceBytes];
+
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int group = blockIdx.x * kWavesPerBlock + wave;
   const int ttile = blockIdx.y, split = blockIdx.z;
@@ -66,57 +80,102 @@ __global__ __launch_bounds__(kThreads) void ffn_skinny_kernel(const FfnArgs a) {
   const int row0 = a.tile_map[3 + 2 * ttile];
   const int row_end = min(row0 + kRows, a.offsets[e + 1]);
 
-  const int lr = lane & 15, kq = lane >> 4;
   const int ld = kGateUp ? a.H : a.I;
   const int kbeg = split * a.k_per_split;
-  const int kend = kbeg + a.k_per_split;
+  const int nsteps = a.k_per_split / kKS;
 
+  // Operand o covers weight rows base(o) .. base(o)+15.
   const T* w = static_cast<const T*>(a.w[e]);
-  const T* wg = w + static_cast<size_t>(group * kRows + lr) * ld + kq * 8;
-  const T* wu = kGateUp ? w + static_cast<size_t>(a.I + group * kRows + lr) * ld + kq * 8 : wg;
-  const int prow = row0 + lr;
+  const T* wop[NOP];
+  wop[0] = w + static_cast<size_t>(group * kRows) * ld;
+  if (kGateUp) wop[NOP - 1] = w + static_cast<size_t>(a.I + group * kRows) * ld;
+
+  // Load j of a step: this lane reads row 4j + lane/16, logical chunk
+  // (lane%16) ^ row, so the 16 lanes of a row cover its 256 bytes.
+  uint32_t goff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * j + (lane >> 4);
+    goff[j] = static_cast<uint32_t>(r * ld + (((lane & 15) ^ r) * 8));
+  }
+  // MFMA sub-step s reads row lane%16, logical chunk 4s + lane/16.
+  uint32_t roff[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int r = lane & 15, c = 4 * s + (lane >> 4);
+    roff[s] = static_cast<uint32_t>(r * kRowStepBytes + ((c ^ r) << 4));
+  }
+
+  const int prow = row0 + (lane & 15);
   const bool valid = prow < row_end;
   const int xrow = kGateUp ? a.row_src[valid ? prow : row0] : (valid ? prow : row0);
-  const T* xp = static_cast<const T*>(a.x) + static_cast<size_t>(xrow) * ld + kq * 8;
+  const T* xp = static_cast<const T*>(a.x) + static_cast<size_t>(xrow) * ld + (lane >> 4) * 8;
   const u32x4 zero = {0, 0, 0, 0};
 
-  f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
-  int k = kbeg;
-  for (; k + kUnroll * kStep <= kend; k += kUnroll * kStep) {
-    u32x4 g[kUnroll], u[kUnroll], xv[kUnroll];
+  // Rotated walk over the K steps of this split.
+  const int s0 = nsteps > 0 ? (group * 7 + split * 3) % nsteps : 0;
+
+  u32x4 wr[D][NOP][4], xr[D][4];
+  auto issue = [&](int slot, int st) {
+    int idx = s0 + st;
+    if (idx >= nsteps) idx -= nsteps;
+    const int k = kbeg + idx * kKS;
 #pragma unroll
-    for (int i = 0; i < kUnroll; ++i) {
-      g[i] = load16_stream(wg + k + i * kStep);
-      if (kGateUp) u[i] = load16_stream(wu + k + i * kStep);
-      xv[i] = valid ? load16(xp + k + i * kStep) : zero;
-    }
+    for (int o = 0; o < NOP; ++o)
 #pragma unroll
-    for (int i = 0; i < kUnroll; ++i) {
-      accg = Mfma16<T>::mma(g[i], xv[i], accg);
-      if (kGateUp) accu = Mfma16<T>::mma(u[i], xv[i], accu);
-    }
-  }
-  for (; k + kStep <= kend; k += kStep) {
-    const u32x4 g = load16_stream(wg + k);
-    const u32x4 xv = valid ? load16(xp + k) : zero;
-    accg = Mfma16<T>::mma(g, xv, accg);
-    if (kGateUp) {
-      const u32x4 u = load16_stream(wu + k);
-      accu = Mfma16<T>::mma(u, xv, accu);
+      for (int j = 0; j < 4; ++j) wr[slot][o][j] = load16_stream(wop[o] + k + goff[j]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xr[slot][s] = valid ? load16(xp + k + s * 32) : zero;
+  };
+
+  f32x4 acc[NOP];
+#pragma unroll
+  for (int o = 0; o < NOP; ++o) acc[o] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto consume = [&](int slot) {
+    uint8_t* buf = lds[wave][slot & 1];
+#pragma unroll
+    for (int o = 0; o < NOP; ++o)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<u32x4*>(buf + o * kOperandBytes + (64 * j + lane) * 16) = wr[slot][o][j];
+    // The wave reads back what it just wrote: order the LDS accesses.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int o = 0; o < NOP; ++o) {
+        const u32x4 fa = *reinterpret_cast<const u32x4*>(buf + o * kOperandBytes + roff[s]);
+        acc[o] = Mfma16<T>::mma(fa, xr[slot][s], acc[o]);
+      }
+  };
+
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < nsteps) issue(d, d);
+  for (int st = 0; st < nsteps; st += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (st + d < nsteps) {
+        consume(d);
+        if (st + d + D < nsteps) issue(d, st + d + D);
+      }
     }
   }
 
-  // Lane (lr, kq) holds features 4*kq + 0..3 of this 16-row group for token lr.
+  // Lane (row, kq) holds features 4*kq + 0..3 of this 16-row group for token lane%16.
   if (!valid) return;
-  const int col = group * kRows + 4 * kq;
+  const int col = group * kRows + 4 * (lane >> 4);
   if (kGateUp) {
+    const f32x4 g = acc[0], u = acc[NOP - 1];
     T* inter = static_cast<T*>(a.out) + static_cast<size_t>(prow) * a.I + col;
-    store4<T>(inter, gate_act(a.act, accg[0]) * accu[0], gate_act(a.act, accg[1]) * accu[1],
-              gate_act(a.act, accg[2]) * accu[2], gate_act(a.act, accg[3]) * accu[3]);
+    store4<T>(inter, gate_act(a.act, g[0]) * u[0], gate_act(a.act, g[1]) * u[1],
+              gate_act(a.act, g[2]) * u[2], gate_act(a.act, g[3]) * u[3]);
   } else {
     float* y = static_cast<float*>(a.out) + static_cast<size_t>(split) * a.R * a.H +
                static_cast<size_t>(prow) * a.H + col;
-    store4<float>(y, accg[0], accg[1], accg[2], accg[3]);
+    store4<float>(y, acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
   }
 }
 

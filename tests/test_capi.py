@@ -50,14 +50,14 @@ def test_plan_paths_and_layout(T, H, I, E, K, dtype, path):
     assert p.workspace_bytes - p.off_y >= p.down_splits * T * K * H * 4
     assert p.off_tile_map - p.off_row_src >= 4 * T * K
     if p.path == _capi.PATH_MFMA_SKINNY:
-        assert (I // 32) % p.down_splits == 0
+        assert (I // 128) % p.down_splits == 0
 
 
 @pytest.mark.parametrize("T,K,E,tile", [(4096, 2, 8, 256), (16, 2, 8, 16), (8, 6, 64, 16),
                                         (333, 3, 7, 64)])
 def test_tile_map_capacity_bounds_every_routing(T, K, E, tile):
     dtype = _capi.F32 if tile == 64 else _capi.BF16
-    H, I = (256, 256) if tile != 16 else (256, 64)
+    H, I = (256, 256) if tile != 16 else (256, 128)
     p = _capi.make_plan(T, H, I, E, K, dtype)
     assert p.tile_rows == tile
     rng = np.random.default_rng(0)

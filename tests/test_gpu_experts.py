@@ -86,6 +86,8 @@ CASES = [
     ("fp32_tiny", 96, 2, 8, 256, 352, "f32", _capi.PATH_SIMT),
     ("fp32_decode", 3, 2, 8, 128, 96, "f32", _capi.PATH_SIMT),
     ("bf16_unaligned", 40, 2, 4, 136, 200, "bf16", _capi.PATH_SIMT),
+    ("decode_i1408", 6, 2, 8, 256, 1408, "bf16", _capi.PATH_MFMA_SKINNY),
+    ("decode_unaligned_k", 4, 2, 4, 160, 96, "bf16", _capi.PATH_SIMT),
 ]
 
 
