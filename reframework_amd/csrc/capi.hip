@@ -62,6 +62,28 @@ int check_banks(const moe355_plan* p, const void* const* w, const char* name) {
 
 }  // namespace
 
+namespace moe355 {
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      n = 256;
+    }
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+}  // namespace moe355
+
 extern "C" {
 
 int moe355_version(void) { return 100; }
@@ -108,7 +130,25 @@ int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* 
                                           p->tile_rows)
                        : 0;
   p->down_splits = 1;
-  if (p->path == MOE355_PATH_MFMA_SKINNY) {
+  if (p->path == MOE355_PATH_MFMA_TILED) {
+    // The persistent down kernel runs (H/256 weight tiles x token tiles x
+    // splits) work items of I/(32*splits) k-steps on one workgroup per CU.
+    // Pick the split that minimises the busiest CU's step count, charging each
+    // extra split its fp32 partial plane (written once, read by the combine)
+    // at ~1.8e-6 steps per element; ties keep fewer splits.
+    const long long items = static_cast<long long>(H / 256) * p->max_tiles;
+    const int cus = moe355::device_cu_count();
+    double best = 0.0;
+    for (int s = 1; s <= 8 && (I / 32) % s == 0; s *= 2) {
+      const long long rounds = (items * s + cus - 1) / cus;
+      const double cost = static_cast<double>(rounds) * (I / 32 / s) +
+                          (s - 1) * static_cast<double>(R) * H * 1.8e-6;
+      if (s == 1 || cost < 0.97 * best) {
+        best = cost;
+        p->down_splits = s;
+      }
+    }
+  } else if (p->path == MOE355_PATH_MFMA_SKINNY) {
     // Spread the down projection (H/16 row groups per tile) over >= 4096 waves;
     // each split covers a multiple of the kernel's 128-element k step.
     const long long waves = static_cast<long long>(H / 16) * (p->max_tiles > 0 ? p->max_tiles : 1);

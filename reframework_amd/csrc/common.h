@@ -184,6 +184,10 @@ struct CombineArgs {
   int accumulate;
 };
 
+// Compute units of the current device (256 when it cannot be queried, e.g. on a
+// host without a GPU); cached per device.
+int device_cu_count();
+
 // ---------------------------------------------------------------- launchers
 // Each returns the hipError_t of the launch (hipSuccess when nothing to do).
 hipError_t launch_router(const RouterArgs& a, int dtype, hipStream_t s);

@@ -2,23 +2,28 @@
 //
 // Replaces the per-expert GEMMs of fused_experts (reframework/moe/fused.py:
 // 76-83): `x @ w1[e].t()`, gated_act_and_mul, `inter @ w2[e].t()`. One launch
-// covers every expert: the grid is (weight tile) x (token tile) over the tile
-// map written by the permute, so no host round trip decides group sizes.
+// covers every expert: work items are (K-split, weight tile, token tile) over
+// the tile map written by the permute, so no host round trip decides group
+// sizes.
 //
-// Tile: 256 weight rows x 256 token rows x 64 k per LDS stage, 4 waves in a
-// 2x2 arrangement, each wave owning 4x4 blocks of v_mfma_f32_32x32x16 (a
-// 128x128 sub-tile, 256 fp32 accumulators). Weight rows are the MFMA M side and
-// tokens the N side, so each lane ends up holding 4 consecutive output features
-// of one token and stores them as one vector.
-//   gate_up: the 256 weight rows are 128 gate rows and the 128 matching up rows,
-//            so gate and up of the same (token, feature) land in the same lane
-//            and silu(g)*u is applied in registers; token rows are gathered
-//            straight from x through row_src (no permuted copy of x).
+// Tile: 256 weight rows x 256 token rows, 4 waves in a 2x2 arrangement, each
+// wave owning 4x4 blocks of v_mfma_f32_32x32x16 (a 128x128 sub-tile, 256 fp32
+// accumulators). Weight rows are the MFMA M side and tokens the N side, so each
+// lane ends up holding 4 consecutive output features of one token and stores
+// them as one vector.
+//   gate_up: the 256 weight rows are 128 gate rows and the 128 matching up
+//            rows, so gate and up of the same (token, feature) land in the same
+//            lane and silu(g)*u is applied in registers; token rows are
+//            gathered straight from x through row_src (no permuted copy of x).
 //   down:    256 rows of w2 against the permuted inter rows, fp32 partials
 //            per K-split into y.
-// LDS rows are 128 B, XOR-swizzled in 16-byte chunks (swz) so that the staging
-// writes and the MFMA operand reads are bank-conflict free. Global loads are
-// staged through registers and double-buffered in LDS (2 x 64 KB).
+// Operands move global -> LDS with direct-to-LDS loads (no register staging),
+// 32 k per step in five 32 KB LDS buffers (the whole 160 KB LDS), issued three
+// steps ahead of the MFMAs and interleaved with them. LDS rows are 64 B,
+// XOR-swizzled in 16-byte chunks (swz) so the operand reads are bank-conflict
+// free. The kernel is persistent (one workgroup per CU) and streams its K-steps
+// across tile boundaries, so each tile's pipeline fill overlaps the previous
+// tile's epilogue.
 #include "common.h"
 
 namespace moe355 {
@@ -27,21 +32,49 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kTileW = 256;
 constexpr int kTileT = 256;
-constexpr int kBK = 64;
-constexpr int kRowBytes = kBK * 2;
-constexpr int kRowsPerPass = kThreads / 8;            // 8 threads x 16 B per row
-constexpr int kPasses = kTileW / kRowsPerPass;        // 8
-constexpr int kRegionBytes = kTileW * kRowBytes;      // 32 KB
+constexpr int kBK = 32;
+constexpr int kRowBytes = kBK * 2;                    // 64 B: 4 chunks of 16 B
+constexpr int kRegionBytes = kTileW * kRowBytes;      // 16 KB
 constexpr int kStageBytes = 2 * kRegionBytes;         // weights + tokens
-constexpr int kLdsBytes = 2 * kStageBytes;            // double buffered
+constexpr int kStages = 5;
+constexpr int kLdsBytes = kStages * kStageBytes;      // 160 KB: the whole LDS
+constexpr int kLoadsPerWave = kStageBytes / 1024 / (kThreads / kWave);  // 8 x 1 KB
 
-// Physical 16-byte chunk of logical chunk c in LDS row r. Rows are 128 B (8
-// chunks). XOR with r&7 spreads 8 consecutive rows over all 8 chunk columns,
-// and the extra bit (r>>3)&1 keeps rows r and r+8, which share a bank set on a
-// 64-bank LDS, in different columns: any 16 consecutive rows read at one
-// logical chunk hit 16 distinct 16-byte bank groups.
+// Physical 16-byte chunk of logical chunk c (0..3) in LDS row r (64 B). Four
+// consecutive rows fill one 256-byte span of a 64-bank LDS; XOR with
+// (r >> 2) & 3 gives the four such spans of any 16 consecutive rows different
+// chunk columns, so 16 rows read at one logical chunk hit 16 distinct 16-byte
+// bank groups.
 __device__ __forceinline__ uint32_t swz(int c, int r) {
-  return static_cast<uint32_t>(c ^ (r & 7) ^ ((r >> 3) & 1));
+  return static_cast<uint32_t>(c ^ ((r >> 2) & 3));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt that waits until at most n vector-memory operations are
+// outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
+// left at their maxima, i.e. not waited on).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier after which the direct-to-LDS loads older than the newest
+// n of every wave are visible to all waves. __syncthreads() would wait for all
+// vector-memory operations (vmcnt(0)), draining the load pipeline; the signal
+// fences only stop the compiler from moving memory accesses across.
+template <int n>
+__device__ __forceinline__ void dma_barrier() {
+  wait_vmcnt<n>();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// One 1 KB direct-to-LDS load per wave: lane i's 16 bytes land at dst + 16 i.
+__device__ __forceinline__ void dma16(const void* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)(dst), 16, 0, 0);
 }
 
 template <typename T>
@@ -63,52 +96,122 @@ struct Mfma32<f16> {
   }
 };
 
+struct Tile {
+  int split, wtile, e, row0, row_end;
+};
+
+// Persistent: one workgroup per CU walks work items L = L0, L0 + G, ... (G =
+// grid size) of the (split, weight tile, token tile) space. Its K-steps form
+// one continuous stream: the direct-to-LDS loads run kStages-1 steps ahead of
+// the MFMAs and cross into the next tile while the current one is still being
+// multiplied, so the next tile's first stages are in flight during the
+// epilogue and no workgroup launch or pipeline fill is paid per tile.
 template <typename T, bool kGateUp>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void ffn_tiled_kernel(const FfnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
 
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int wave_w = wave >> 1, wave_t = wave & 1;
 
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int per_split = a.n_wtiles * a.max_tiles;
-  const int split = L / per_split;
-  const int rem = L - split * per_split;
-  const int wtile = rem / a.max_tiles;
-  const int ttile = rem - wtile * a.max_tiles;
-  if (ttile >= a.tile_map[0]) return;
-  const int e = a.tile_map[2 + 2 * ttile];
-  const int row0 = a.tile_map[3 + 2 * ttile];
-  const int row_end = min(row0 + kTileT, a.offsets[e + 1]);
+  const int n_t = a.tile_map[0];
+  const int per_split = a.n_wtiles * n_t;
+  const int n_work = a.splits * per_split;
+  const int G = gridDim.x;
+  int Lc = xcd_remap(blockIdx.x, G);  // work item being multiplied
+  if (Lc >= n_work) return;
 
   const int ld = kGateUp ? a.H : a.I;  // elements per weight row and per token row
-  const int kbeg = split * a.k_per_split;
+  const uint32_t pitch = static_cast<uint32_t>(ld * 2);
   const int nk = a.k_per_split / kBK;
 
-  const char* wbase = static_cast<const char*>(a.w[e]) + static_cast<size_t>(kbeg) * 2;
-  const char* xbase = static_cast<const char*>(a.x) + static_cast<size_t>(kbeg) * 2;
-  if (!kGateUp) xbase += static_cast<size_t>(row0) * ld * 2;
+  auto decode = [&](int L) {
+    Tile t;
+    t.split = L / per_split;
+    const int rem = L - t.split * per_split;
+    t.wtile = rem / n_t;
+    const int tt = rem - t.wtile * n_t;
+    t.e = a.tile_map[2 + 2 * tt];
+    t.row0 = a.tile_map[3 + 2 * tt];
+    t.row_end = min(t.row0 + kTileT, a.offsets[t.e + 1]);
+    return t;
+  };
 
-  // Byte offsets of this thread's 16-byte chunk in each of the 8 load passes.
-  const int lrow = tid >> 3, chunk = tid & 7;
-  uint32_t woff[kPasses], xoff[kPasses];
+  // Stage = 32 loads of 1 KB (16 rows x 64 B each). Waves 0-1 fill the weight
+  // region, waves 2-3 the token region, 8 loads each: load q of wave w covers
+  // region rows 16 * (8 * (w & 1) + q) .. +15. Lane i of a load fills row
+  // 16 * (...) + i / 4, physical chunk i % 4, so it fetches that row's logical
+  // chunk swz(i % 4, row) (the swizzle is an involution) from global memory.
+  const bool wload = wave < 2;
+  auto region_row = [&](int q) { return ((wave & 1) * kLoadsPerWave + q) * 16 + (lane >> 2); };
+
+  // gate_up token rows come through row_src; they are fetched one tile ahead.
+  int grow[kLoadsPerWave];
+  auto fetch_rows = [&](const Tile& t) {
 #pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int r = p * kRowsPerPass + lrow;
-    int wrow;
-    if (kGateUp)
-      wrow = r < kTileW / 2 ? wtile * (kTileW / 2) + r : a.I + wtile * (kTileW / 2) + (r - kTileW / 2);
-    else
-      wrow = wtile * kTileW + r;
-    woff[p] = static_cast<uint32_t>(wrow) * static_cast<uint32_t>(ld * 2) + chunk * 16;
-    const int prow = min(row0 + r, row_end - 1);
-    const int xrow = kGateUp ? a.row_src[prow] : prow - row0;
-    xoff[p] = static_cast<uint32_t>(xrow) * static_cast<uint32_t>(ld * 2) + chunk * 16;
-  }
-  const uint32_t st_off = lrow * kRowBytes + (swz(chunk, lrow) << 4);
+    for (int q = 0; q < kLoadsPerWave; ++q)
+      grow[q] = a.row_src[min(t.row0 + region_row(q), t.row_end - 1)];
+  };
 
-  // MFMA operand rows of this wave inside the stage.
+  // Load cursor: work item Ll, step lkt; source base and per-load offsets.
+  int Ll = Lc, lkt = 0;
+  const char* lsrc;
+  uint32_t lgoff[kLoadsPerWave];
+  auto setup_load = [&](const Tile& t) {
+    const size_t kbeg = static_cast<size_t>(t.split) * a.k_per_split;
+    if (wload) {
+      lsrc = static_cast<const char*>(a.w[t.e]) + kbeg * 2;
+#pragma unroll
+      for (int q = 0; q < kLoadsPerWave; ++q) {
+        const int r = region_row(q);
+        const int wr = kGateUp ? (r < kTileW / 2 ? t.wtile * (kTileW / 2) + r
+                                                 : a.I + t.wtile * (kTileW / 2) + (r - kTileW / 2))
+                               : t.wtile * kTileW + r;
+        lgoff[q] = static_cast<uint32_t>(wr) * pitch + swz(lane & 3, r) * 16;
+      }
+    } else if (kGateUp) {
+      lsrc = static_cast<const char*>(a.x) + kbeg * 2;
+#pragma unroll
+      for (int q = 0; q < kLoadsPerWave; ++q)
+        lgoff[q] = static_cast<uint32_t>(grow[q]) * pitch + swz(lane & 3, region_row(q)) * 16;
+    } else {
+      lsrc = static_cast<const char*>(a.x) + (static_cast<size_t>(t.row0) * ld + kbeg) * 2;
+#pragma unroll
+      for (int q = 0; q < kLoadsPerWave; ++q) {
+        const int r = region_row(q);
+        const int xr = min(t.row0 + r, t.row_end - 1) - t.row0;
+        lgoff[q] = static_cast<uint32_t>(xr) * pitch + swz(lane & 3, r) * 16;
+      }
+    }
+  };
+  auto prefetch_next_rows = [&]() {
+    if (kGateUp && !wload && Ll + G < n_work) fetch_rows(decode(Ll + G));
+  };
+  // Step to the next K-step of the load stream; past the last work item the
+  // cursor stays on its final step, so the tail keeps issuing (harmless,
+  // in-bounds) loads into buffers nobody reads and the vmcnt accounting of
+  // the pipeline stays fixed.
+  auto advance_load = [&]() {
+    if (++lkt < nk) return;
+    if (Ll + G < n_work) {
+      Ll += G;
+      lkt = 0;
+      setup_load(decode(Ll));
+      prefetch_next_rows();
+    } else {
+      lkt = nk - 1;
+    }
+  };
+  // Loads q0 .. q0+n-1 of the current load step into LDS buffer lb.
+  auto issue = [&](uint8_t* lb, int q0, int n) {
+    uint8_t* dst = lb + wave * kLoadsPerWave * 1024;
+#pragma unroll
+    for (int q = q0; q < q0 + n; ++q)
+      dma16(lsrc + lkt * kRowBytes + lgoff[q], dst + q * 1024);
+  };
+
+  // MFMA operand rows of this wave inside a stage.
   const int lr = lane & 31, kh = lane >> 5;
   uint32_t arow[4], brow[4];
 #pragma unroll
@@ -121,8 +224,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
     arow[b] = (rb + lr) * kRowBytes;
     brow[b] = kRegionBytes + (wave_t * 128 + b * 32 + lr) * kRowBytes;
   }
-  // Swizzled 16-byte chunk offsets of the 4 k16 sub-steps for this lane
-  // (operand rows start at multiples of 32, so row bits 0..3 are lr's).
+  // Operand rows start at multiples of 32, so the swizzle bits are lr's.
   uint32_t coff[kBK / 16];
 #pragma unroll
   for (int ks = 0; ks < kBK / 16; ++ks) coff[ks] = swz(ks * 2 + kh, lr) << 4;
@@ -133,24 +235,6 @@ void ffn_tiled_kernel(const FfnArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  u32x4 wr[kPasses], xr[kPasses];
-  auto load_stage = [&](int kt) {
-    const char* wk = wbase + kt * kRowBytes;
-    const char* xk = xbase + kt * kRowBytes;
-#pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      wr[p] = *reinterpret_cast<const u32x4*>(wk + woff[p]);
-      xr[p] = *reinterpret_cast<const u32x4*>(xk + xoff[p]);
-    }
-  };
-  auto store_stage = [&](int s) {
-    uint8_t* st = lds + s * kStageBytes;
-#pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      *reinterpret_cast<u32x4*>(st + p * kRowsPerPass * kRowBytes + st_off) = wr[p];
-      *reinterpret_cast<u32x4*>(st + kRegionBytes + p * kRowsPerPass * kRowBytes + st_off) = xr[p];
-    }
-  };
   auto read_frags = [&](const uint8_t* st, int ks, u32x4* af, u32x4* bf) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -159,94 +243,140 @@ void ffn_tiled_kernel(const FfnArgs a) {
     }
   };
 
-  // Pipeline: LDS stage kt is consumed while stage kt+1 (already in
-  // registers) is written to the other LDS buffer during sub-step 1, one LDS
-  // write and one global load of stage kt+2 (clamped to the last stage, so the
-  // loop has no branches) between consecutive MFMAs. Operand fragments of
-  // sub-step ks+1 are read while sub-step ks's 16 MFMAs run; scheduling
-  // fences keep the compiler from pulling those reads in front of the MFMAs
-  // they are meant to overlap. One barrier per stage.
-  load_stage(0);
-  store_stage(0);
-  load_stage(min(1, nk - 1));
-  __syncthreads();
+  // Pipeline over kStages LDS buffers. Invariant at the top of each step g:
+  // steps g and g+1 are in LDS and visible to every wave, the sub-step 0
+  // operands of step g are in registers, and the loads of steps
+  // g+2 .. g+kStages-2 are in flight. Each step issues step g+kStages-1 (its
+  // buffer was last read in step g-1), runs 32 MFMAs, reads step g+1's first
+  // operands, and waits only for step g+2, so a load has two steps to land.
+  // Other vector-memory operations issued in between (row_src prefetch,
+  // epilogue stores) only make that wait stricter.
+  {
+    const Tile t0 = decode(Ll);
+    if (kGateUp && !wload) fetch_rows(t0);
+    setup_load(t0);
+    prefetch_next_rows();
+  }
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s) {
+    issue(lds + s * kStageBytes, 0, kLoadsPerWave);
+    advance_load();
+  }
+  dma_barrier<(kStages - 3) * kLoadsPerWave>();
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const uint8_t* st = lds + cur * kStageBytes;
-    u32x4 fa[2][4], fb[2][4];
-    read_frags(st, 0, fa[0], fb[0]);
+  u32x4 fa[2][4], fb[2][4];
+  read_frags(lds, 0, fa[0], fb[0]);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+
+  // Each half: wait for its operands (read during the previous half), then 16
+  // MFMAs. The next half's 8 operand reads and half of the next stage's loads
+  // are spread over the first 12 MFMAs (3 MFMA : 2 LDS reads : 1 load), so
+  // neither the LDS nor the texture unit sees a burst from all four waves and
+  // the last read still has 4 MFMAs to land.
+  auto half = [&](const u32x4* af, const u32x4* bf, const uint8_t* src, int ks, u32x4* na,
+                  u32x4* nb, uint8_t* lb, int q0) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      if (ks + 1 < kBK / 16) read_frags(st, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);
-      if (ks == 1) {
-        store_stage(cur ^ 1);
-        load_stage(min(kt + 2, nk - 1));
-      }
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < 4; ++j) acc[i][j] = Mfma32<T>::mma(af[i], bf[j], acc[i][j]);
+    // Memory operations in the order of the schedule below: the compiler keeps
+    // LDS reads and direct-to-LDS loads in program order (it cannot tell that
+    // they touch different buffers).
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = Mfma32<T>::mma(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
-      if (ks == 1) {
-        for (int q = 0; q < 16; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    for (int i = 0; i < 4; ++i) {
+      na[i] = *reinterpret_cast<const u32x4*>(src + arow[i] + coff[ks]);
+      issue(lb, q0 + i, 1);
+      nb[i] = *reinterpret_cast<const u32x4*>(src + brow[i] + coff[ks]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global -> LDS load
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  int cb = 0;  // LDS buffer of the step being multiplied
+  Tile ct = decode(Lc);
+  while (true) {
+    for (int kt = 0; kt < nk; ++kt) {
+      const int nb_ = cb == kStages - 1 ? 0 : cb + 1;
+      const int lb_ = cb == 0 ? kStages - 1 : cb - 1;  // (cb + kStages - 1) % kStages
+      uint8_t* st = lds + cb * kStageBytes;
+      uint8_t* nx = lds + nb_ * kStageBytes;
+      uint8_t* lb = lds + lb_ * kStageBytes;
+      half(fa[0], fb[0], st, 1, fa[1], fb[1], lb, 0);
+      half(fa[1], fb[1], nx, 0, fa[0], fb[0], lb, kLoadsPerWave / 2);
+      advance_load();
+      dma_barrier<(kStages - 3) * kLoadsPerWave>();
+      cb = nb_;
+    }
+
+    // Epilogue. Lane (lr, kh) of block (i, j) holds, for q = 0..3, features
+    // 8q + 4kh + 0..3 of the 32-row weight block and token lr of the token block.
+    if (kGateUp) {
+      T* inter = static_cast<T*>(a.out);
+  #pragma unroll
+      for (int b = 0; b < 2; ++b) {
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int prow = ct.row0 + wave_t * 128 + j * 32 + lr;
+          if (prow < ct.row_end) {
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int col = ct.wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * kh;
+              float v[4];
+  #pragma unroll
+              for (int r = 0; r < 4; ++r)
+                v[r] = gate_act(a.act, acc[b][j][4 * q + r]) * acc[b + 2][j][4 * q + r];
+              store4<T>(inter + static_cast<size_t>(prow) * a.I + col, v[0], v[1], v[2], v[3]);
+            }
+          }
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
-  }
-
-  // Epilogue. Lane (lr, kh) of block (i, j) holds, for q = 0..3, features
-  // 8q + 4kh + 0..3 of the 32-row weight block and token lr of the token block.
-  if (kGateUp) {
-    T* inter = static_cast<T*>(a.out);
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int prow = row0 + wave_t * 128 + j * 32 + lr;
-        if (prow < row_end) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int col = wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * kh;
-            float v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              v[r] = gate_act(a.act, acc[b][j][4 * q + r]) * acc[b + 2][j][4 * q + r];
-            store4<T>(inter + static_cast<size_t>(prow) * a.I + col, v[0], v[1], v[2], v[3]);
+    } else {
+      float* y = static_cast<float*>(a.out) + static_cast<size_t>(ct.split) * a.R * a.H;
+  #pragma unroll
+      for (int b = 0; b < 4; ++b) {
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int prow = ct.row0 + wave_t * 128 + j * 32 + lr;
+          if (prow < ct.row_end) {
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int h = ct.wtile * kTileW + wave_w * 128 + b * 32 + 8 * q + 4 * kh;
+              store4<float>(y + static_cast<size_t>(prow) * a.H + h, acc[b][j][4 * q],
+                            acc[b][j][4 * q + 1], acc[b][j][4 * q + 2], acc[b][j][4 * q + 3]);
+            }
           }
         }
       }
     }
-  } else {
-    float* y = static_cast<float*>(a.out) + static_cast<size_t>(split) * a.R * a.H;
+
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int prow = row0 + wave_t * 128 + j * 32 + lr;
-        if (prow < row_end) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int h = wtile * kTileW + wave_w * 128 + b * 32 + 8 * q + 4 * kh;
-            store4<float>(y + static_cast<size_t>(prow) * a.H + h, acc[b][j][4 * q],
-                          acc[b][j][4 * q + 1], acc[b][j][4 * q + 2], acc[b][j][4 * q + 3]);
-          }
-        }
-      }
-    }
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    Lc += G;
+    if (Lc >= n_work) break;
+    ct = decode(Lc);
   }
+  // No direct-to-LDS write may still be in flight when the workgroup's LDS is
+  // released.
+  wait_vmcnt<0>();
 }
 
 template <bool kGateUp>
 hipError_t launch_tiled(const FfnArgs& a, int dtype, hipStream_t s) {
-  const int nwg = a.n_wtiles * a.max_tiles * a.splits;
-  if (nwg == 0) return hipSuccess;
+  const long work = static_cast<long>(a.n_wtiles) * a.max_tiles * a.splits;
+  if (work == 0) return hipSuccess;
+  const int nwg = static_cast<int>(work < device_cu_count() ? work : device_cu_count());
   if (dtype == MOE355_BF16)
     ffn_tiled_kernel<bf16, kGateUp><<<dim3(nwg), dim3(kThreads), 0, s>>>(a);
   else
