@@ -244,13 +244,15 @@ void ffn_tiled_kernel(const FfnArgs a) {
   };
 
   // Pipeline over kStages LDS buffers. Invariant at the top of each step g:
-  // steps g and g+1 are in LDS and visible to every wave, the sub-step 0
-  // operands of step g are in registers, and the loads of steps
-  // g+2 .. g+kStages-2 are in flight. Each step issues step g+kStages-1 (its
-  // buffer was last read in step g-1), runs 32 MFMAs, reads step g+1's first
-  // operands, and waits only for step g+2, so a load has two steps to land.
-  // Other vector-memory operations issued in between (row_src prefetch,
-  // epilogue stores) only make that wait stricter.
+  // step g is in LDS and visible to every wave, the sub-step 0 operands of
+  // step g are in registers, and the loads of steps g+1 .. g+kStages-2 are in
+  // flight. Step g issues step g+kStages-1 into the buffer of step g-1 (whose
+  // last reads finished before step g-1's mid-step barrier), runs 16 MFMAs
+  // while reading its sub-step 1 operands, then waits at a mid-step barrier
+  // for step g+1 only, and runs 16 more MFMAs while reading step g+1's first
+  // operands. A load thus has about three steps to land. Other vector-memory
+  // operations issued in between (row_src prefetch, epilogue stores) only make
+  // the waits stricter.
   {
     const Tile t0 = decode(Ll);
     if (kGateUp && !wload) fetch_rows(t0);
@@ -262,7 +264,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
     issue(lds + s * kStageBytes, 0, kLoadsPerWave);
     advance_load();
   }
-  dma_barrier<(kStages - 3) * kLoadsPerWave>();
+  dma_barrier<(kStages - 2) * kLoadsPerWave>();  // step 0 landed
 
   u32x4 fa[2][4], fb[2][4];
   read_frags(lds, 0, fa[0], fb[0]);
@@ -312,9 +314,12 @@ void ffn_tiled_kernel(const FfnArgs a) {
       uint8_t* nx = lds + nb_ * kStageBytes;
       uint8_t* lb = lds + lb_ * kStageBytes;
       half(fa[0], fb[0], st, 1, fa[1], fb[1], lb, 0);
+      // Step g+1 landed (everything but steps g+2, g+3 and the first half of
+      // g+4 is done) and every wave finished reading step g-1's buffer.
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      dma_barrier<(kStages - 3) * kLoadsPerWave + kLoadsPerWave / 2>();
       half(fa[1], fb[1], nx, 0, fa[0], fb[0], lb, kLoadsPerWave / 2);
       advance_load();
-      dma_barrier<(kStages - 3) * kLoadsPerWave>();
       cb = nb_;
     }
 
