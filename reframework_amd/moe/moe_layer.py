@@ -19,6 +19,17 @@ state dict, offload wiring (``build_offload_cache``, ``attach_predictor``,
     i+1's host->HBM copies are queued on the cache's side stream while chunk
     i's kernels run.
 
+Optional shared experts (``n_shared_experts``; not in the reference, which
+has none): the dense SwiGLU that fine-grained MoEs add to every token after
+the routed sum, ``out += down(silu(x gate^T) * (x up^T))`` (the semantics of
+litemoe/src/litemoe/model/model.py:192-195), stored under the HF names
+``shared_experts.{gate,up,down}_proj.weight`` with width
+``shared_intermediate_size`` (default ``n_shared_experts * intermediate_size``).
+When that width is a multiple of ``intermediate_size`` it is kept as that many
+expert-sized pieces and folded into the routed call as extra experts that
+every token reaches with weight 1; otherwise it runs as a second call into the
+same fp32 accumulator.
+
 All compute is in libmoe355: the router kernel (GEMV + softmax + top-k) and
 one fused_experts call per forward (or per chunk). A CPU tensor is an error,
 not a slower path.
@@ -83,6 +94,8 @@ class FusedMoE(BaseOP):
         activation: str = "silu",
         renormalize: bool = True,
         dtype: torch.dtype = torch.float16,
+        n_shared_experts: int = 0,
+        shared_intermediate_size: Optional[int] = None,
     ) -> None:
         super().__init__()
         self.num_experts = num_experts
@@ -101,6 +114,26 @@ class FusedMoE(BaseOP):
             torch.nn.Parameter(torch.empty(hidden_size, intermediate_size, dtype=dtype))
             for _ in range(num_experts)
         ])
+        # Shared experts: width Is split into pieces of ``intermediate_size``
+        # when it divides evenly (folded into the routed call), else one piece.
+        shared_I = int(shared_intermediate_size or n_shared_experts * intermediate_size)
+        if shared_I < 0:
+            raise ValueError("shared_intermediate_size must be >= 0")
+        self.n_shared_experts = int(n_shared_experts)
+        self.shared_intermediate_size = shared_I
+        if shared_I and shared_I % intermediate_size == 0:
+            piece, n_pieces = intermediate_size, shared_I // intermediate_size
+        else:
+            piece, n_pieces = shared_I, (1 if shared_I else 0)
+        self._shared_piece = piece
+        self.shared_w1 = torch.nn.ParameterList([
+            torch.nn.Parameter(torch.empty(2 * piece, hidden_size, dtype=dtype))
+            for _ in range(n_pieces)
+        ])
+        self.shared_w2 = torch.nn.ParameterList([
+            torch.nn.Parameter(torch.empty(hidden_size, piece, dtype=dtype))
+            for _ in range(n_pieces)
+        ])
         self._cache: Optional[ExpertOffloadCache] = None
         self._cpu_split_enabled: bool = False
         self._predictor: Optional[Prediction] = None
@@ -115,7 +148,8 @@ class FusedMoE(BaseOP):
         """Build from a model config with the reference's MoE fields
         (num_experts, num_experts_per_tok, hidden_size, moe_inter,
         moe_activation, moe_renormalize, dtype; optional entropy_adaptive_k,
-        entropy_k_min), honouring RE_ENTROPY_K / RE_ENTROPY_K_MIN."""
+        entropy_k_min), honouring RE_ENTROPY_K / RE_ENTROPY_K_MIN. Optional
+        ``n_shared_experts`` / ``shared_intermediate_size`` add shared experts."""
         moe = cls(
             num_experts=cfg.num_experts,
             top_k=cfg.num_experts_per_tok,
@@ -124,6 +158,8 @@ class FusedMoE(BaseOP):
             activation=cfg.moe_activation,
             renormalize=cfg.moe_renormalize,
             dtype=dtype or cfg.dtype,
+            n_shared_experts=int(getattr(cfg, "n_shared_experts", 0) or 0),
+            shared_intermediate_size=getattr(cfg, "shared_intermediate_size", None),
         )
         moe.entropy_adaptive_k = bool(getattr(cfg, "entropy_adaptive_k", False)) or env.get_entropy_k()
         moe.entropy_k_min = env.get_entropy_k_min(getattr(cfg, "entropy_k_min", 2))
@@ -214,8 +250,11 @@ class FusedMoE(BaseOP):
     def _resident_banks(self) -> Tuple[List[int], List[int]]:
         if len(self.experts_w1) != self.num_experts:
             raise RuntimeError("expert parameters are not resident (offload cache built?)")
+        return self._pointers(self.experts_w1, self.experts_w2)
+
+    def _pointers(self, w1s, w2s) -> Tuple[List[int], List[int]]:
         w1p, w2p = [], []
-        for p1, p2 in zip(self.experts_w1, self.experts_w2):
+        for p1, p2 in zip(w1s, w2s):
             if p1.device.type != "cuda" or p2.device.type != "cuda":
                 raise RuntimeError("expert parameters must be on the GPU")
             if p1.dtype != self.dtype or p2.dtype != self.dtype:
@@ -225,6 +264,53 @@ class FusedMoE(BaseOP):
             w1p.append(p1.data_ptr())
             w2p.append(p2.data_ptr())
         return w1p, w2p
+
+    @property
+    def _shared_folded(self) -> bool:
+        return len(self.shared_w1) > 0 and self._shared_piece == self.intermediate_size
+
+    def _experts(self, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor, act: int,
+                 w1p: List[int], w2p: List[int], expert_map: Optional[List[int]] = None,
+                 out: Optional[torch.Tensor] = None, accumulate_f32: bool = False,
+                 with_shared: bool = True) -> torch.Tensor:
+        """Routed experts (bank pointers ``w1p``/``w2p``, ids renamed through
+        ``expert_map`` when given), plus the shared experts when
+        ``with_shared``: folded in as extra ids E.. with weight 1, or as a
+        second call into an fp32 accumulator."""
+        I = self.intermediate_size
+        if not with_shared or not len(self.shared_w1):
+            return run_experts(xd, w1p, w2p, I, w, ids, act, out=out, expert_map=expert_map,
+                               accumulate_f32=accumulate_f32)
+        s1, s2 = self._pointers(self.shared_w1, self.shared_w2)
+        T, n = xd.shape[0], len(s1)
+        if self._shared_folded:
+            ids_x = torch.arange(self.num_experts, self.num_experts + n, dtype=ids.dtype,
+                                 device=ids.device).expand(T, n)
+            ids2 = torch.cat([ids, ids_x], dim=1).contiguous()
+            w2_ = torch.cat([w, torch.ones((T, n), dtype=w.dtype, device=w.device)], dim=1)
+            base = len(w1p)
+            if expert_map is None:
+                emap = None if base == self.num_experts else \
+                    list(range(base)) + [-1] * (self.num_experts - base) + [base + j for j in range(n)]
+            else:
+                emap = list(expert_map) + [-1] * (self.num_experts - len(expert_map)) + \
+                    [base + j for j in range(n)]
+            return run_experts(xd, w1p + s1, w2p + s2, I, w2_.contiguous(), ids2, act, out=out,
+                               expert_map=emap, accumulate_f32=accumulate_f32)
+        acc = out if accumulate_f32 else torch.zeros((T, self.hidden_size), dtype=torch.float32,
+                                                     device=xd.device)
+        run_experts(xd, w1p, w2p, I, w, ids, act, out=acc, expert_map=expert_map,
+                    accumulate_f32=True)
+        run_experts(xd, s1, s2, self._shared_piece,
+                    torch.ones((T, 1), dtype=torch.float32, device=xd.device),
+                    torch.zeros((T, 1), dtype=torch.int32, device=xd.device), act, out=acc,
+                    accumulate_f32=True)
+        if accumulate_f32:
+            return acc
+        res = out if out is not None else torch.empty((T, self.hidden_size), dtype=xd.dtype,
+                                                      device=xd.device)
+        _capi.cast_f32(acc, res)
+        return res
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         M = x.shape[0] if x.dim() > 1 else x.numel()
@@ -240,7 +326,7 @@ class FusedMoE(BaseOP):
             out = self._forward_offload(M, xd, w, ids, act)
         else:
             w1p, w2p = self._resident_banks()
-            out = run_experts(xd, w1p, w2p, self.intermediate_size, w, ids, act)
+            out = self._experts(xd, w, ids, act, w1p, w2p)
         if out.dtype != x2.dtype:
             out = out.to(x2.dtype)
         return out.reshape(x.shape[:1] + (self.hidden_size,)) if x.dim() > 1 else out
@@ -271,28 +357,31 @@ class FusedMoE(BaseOP):
                                         forward_ms=self._since_last_step_ms())
         w1p = [t.data_ptr() for t in w1s]
         w2p = [t.data_ptr() for t in w2s]
-        if not w1p:
+        if not w1p and not len(self.shared_w1):
             return torch.zeros_like(xd)
-        return run_experts(xd, w1p, w2p, self.intermediate_size, w, ids, act,
-                           expert_map=expert_map)
+        return self._experts(xd, w, ids, act, w1p, w2p, expert_map=expert_map)
 
     def _forward_streaming(self, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
                            act: int) -> torch.Tensor:
         """Every routed expert, ``RE_CHUNK_SIZE`` experts at a time, summed in
-        fp32 and cast once at the end (moe_layer.py:354-420)."""
+        fp32 and cast once at the end (moe_layer.py:354-420); the shared
+        experts join the first chunk."""
         cache = self._cache
         chunk_size = env.get_chunk_size(8)
         uniq = sorted({i for i in ids.reshape(-1).tolist() if i >= 0})
         acc = torch.zeros((xd.shape[0], self.hidden_size), dtype=torch.float32, device=xd.device)
-        for start in range(0, len(uniq), chunk_size):
+        starts = list(range(0, len(uniq), chunk_size)) or [0]
+        for n, start in enumerate(starts):
             chunk = uniq[start:start + chunk_size]
             w1s, w2s, local_index = cache.prefetch_slots(chunk)
             expert_map = [-1] * self.num_experts
             for g, loc in local_index.items():
                 expert_map[g] = loc
-            run_experts(xd, [t.data_ptr() for t in w1s], [t.data_ptr() for t in w2s],
-                        self.intermediate_size, w, ids, act, out=acc, expert_map=expert_map,
-                        accumulate_f32=True)
+            if not w1s and (n > 0 or not len(self.shared_w1)):
+                continue
+            self._experts(xd, w, ids, act, [t.data_ptr() for t in w1s],
+                          [t.data_ptr() for t in w2s], expert_map=expert_map, out=acc,
+                          accumulate_f32=True, with_shared=(n == 0))
         out = torch.empty((xd.shape[0], self.hidden_size), dtype=xd.dtype, device=xd.device)
         _capi.cast_f32(acc, out)
         return out
@@ -308,6 +397,13 @@ class FusedMoE(BaseOP):
             result[f"{p}.gate_proj.weight"] = self.experts_w1[e][:I]
             result[f"{p}.up_proj.weight"] = self.experts_w1[e][I:]
             result[f"{p}.down_proj.weight"] = self.experts_w2[e]
+        if len(self.shared_w1):
+            p = f"{prefix}.shared_experts" if prefix else "shared_experts"
+            P = self._shared_piece
+            with torch.no_grad():
+                result[f"{p}.gate_proj.weight"] = torch.cat([t[:P] for t in self.shared_w1])
+                result[f"{p}.up_proj.weight"] = torch.cat([t[P:] for t in self.shared_w1])
+                result[f"{p}.down_proj.weight"] = torch.cat(list(self.shared_w2), dim=1)
         return result
 
     def load_state_dict(self, state_dict: Dict[str, torch.Tensor], *, prefix: str = "",
@@ -325,6 +421,20 @@ class FusedMoE(BaseOP):
                     key = f"{p}.{name}.weight"
                     if key in state_dict:
                         param.copy_(state_dict[key].detach().to(dtype=self.dtype))
+            if len(self.shared_w1):
+                p = f"{prefix}.shared_experts" if prefix else "shared_experts"
+                P = self._shared_piece
+                for j in range(len(self.shared_w1)):
+                    cols = slice(j * P, (j + 1) * P)
+                    for name, dst, src_slice in (("gate_proj", self.shared_w1[j][:P], cols),
+                                                 ("up_proj", self.shared_w1[j][P:], cols)):
+                        key = f"{p}.{name}.weight"
+                        if key in state_dict:
+                            dst.copy_(state_dict[key].detach()[src_slice].to(dtype=self.dtype))
+                    key = f"{p}.down_proj.weight"
+                    if key in state_dict:
+                        self.shared_w2[j].copy_(
+                            state_dict[key].detach()[:, cols].to(dtype=self.dtype))
 
 
 __all__ = ["FusedMoE", "CpuShuttle"]

@@ -90,6 +90,21 @@ def make_layer(shape: MoEShape, dtype: torch.dtype, seed: int = 0, sigma_w: floa
     return {"gate": gate, "w1": w1, "w2": w2, "H": H, "I": I, "E": E}
 
 
+def make_shared(n: int, H: int, I: int, dtype: torch.dtype, seed: int = 0,
+                sigma_w: float = 0.02) -> Dict[str, object]:
+    """``n`` shared experts of width ``I`` (stream 300+j), as pieces w1[j]
+    [2I,H] (gate rows first) / w2[j] [H,I], and as the merged HF tensors
+    ``gate_proj``/``up_proj`` [n*I,H] and ``down_proj`` [H,n*I]."""
+    w1 = [to_dtype(normal(2 * I * H, STREAM_SHARED + j, seed, sigma_w).reshape(2 * I, H), dtype)
+          for j in range(n)]
+    w2 = [to_dtype(normal(H * I, STREAM_SHARED + 64 + j, seed, sigma_w).reshape(H, I), dtype)
+          for j in range(n)]
+    return {"w1": w1, "w2": w2,
+            "gate_proj": torch.cat([w[:I] for w in w1]) if n else None,
+            "up_proj": torch.cat([w[I:] for w in w1]) if n else None,
+            "down_proj": torch.cat(w2, dim=1) if n else None}
+
+
 def make_tokens(T: int, H: int, dtype: torch.dtype, seed: int = 0) -> torch.Tensor:
     return to_dtype(normal(T * H, STREAM_X, seed, 1.0).reshape(T, H), dtype)
 
@@ -110,5 +125,6 @@ def zipf_router_bias(E: int, s: float, seed: int = 0) -> torch.Tensor:
 
 __all__ = [
     "splitmix64", "uniform", "normal", "to_dtype", "MoEShape", "SHAPES", "make_layer",
+    "make_shared",
     "make_tokens", "mixtral_router_bias", "zipf_router_bias",
 ]

@@ -208,3 +208,71 @@ def test_offload_slot_reuse_keeps_results_correct(dev, monkeypatch):
     for o, w in zip(outs, wants):
         assert torch.allclose(o.float(), w.float(), rtol=0, atol=1e-3 * w.float().abs().max().item())
     assert cache.stats.evictions > 0 and cache._n_slots <= 4
+
+
+def _build_shared(E, K, H, I, dtype, n_shared=0, shared_I=None, seed=0):
+    """A layer with shared experts loaded from the merged HF tensors."""
+    moe = FusedMoE(num_experts=E, top_k=K, hidden_size=H, intermediate_size=I, dtype=dtype,
+                   n_shared_experts=n_shared, shared_intermediate_size=shared_I)
+    layer = synth.make_layer(synth.MoEShape("t", H, E, K, I), dtype, seed=seed, sigma_w=0.02)
+    Is = shared_I or n_shared * I
+    sh = synth.make_shared(1, H, Is, dtype, seed=seed)
+    sd = {"gate.weight": layer["gate"]}
+    for e in range(E):
+        sd[f"experts.{e}.gate_proj.weight"] = layer["w1"][e][:I]
+        sd[f"experts.{e}.up_proj.weight"] = layer["w1"][e][I:]
+        sd[f"experts.{e}.down_proj.weight"] = layer["w2"][e]
+    sd["shared_experts.gate_proj.weight"] = sh["gate_proj"]
+    sd["shared_experts.up_proj.weight"] = sh["up_proj"]
+    sd["shared_experts.down_proj.weight"] = sh["down_proj"]
+    moe.load_state_dict(sd)
+    return moe, layer, sh
+
+
+@pytest.mark.parametrize("n_shared,shared_I,T", [(2, None, 100), (0, 384, 100), (2, None, 3)])
+def test_shared_experts_add_dense_swiglu(n_shared, shared_I, T, dev):
+    """out = routed sum + down(silu(x gate^T) * (x up^T)) over every token
+    (litemoe/src/litemoe/model/model.py:192-195): folded as extra experts when
+    the shared width is a multiple of the expert width (2 x 256), as a second
+    fp32-accumulated call otherwise (384)."""
+    banner(f"shared experts n={n_shared} Is={shared_I} T={T}")
+    E, K, H, I = 16, 4, 512, 256
+    moe, layer, sh = _build_shared(E, K, H, I, torch.bfloat16, n_shared, shared_I)
+    assert moe._shared_folded == (shared_I is None)
+    moe = moe.to(dev)
+    x = synth.make_tokens(T, H, torch.bfloat16, seed=5)
+    out = moe(x.to(dev))
+    rw, rids = moe.route(x.to(dev))
+    torch.cuda.synchronize()
+    wn, idn = rw.cpu().numpy(), rids.cpu().numpy()
+    routed = oracle.fused_experts(x, layer["w1"], layer["w2"], wn, idn, inter_round=ROUND[torch.bfloat16])
+    shared = oracle.fused_experts(x, sh["w1"], sh["w2"], np.ones((T, 1), np.float32),
+                                  np.zeros((T, 1), np.int64), inter_round=ROUND[torch.bfloat16])
+    err = oracle.max_rel(out.float().cpu().numpy(), routed + shared)
+    print(f"  max_rel {err:.2e}", flush=True)
+    assert err <= 2e-2
+    # the shared part is really there: without it the output is far off
+    assert oracle.max_rel(out.float().cpu().numpy(), routed) > 0.1
+
+
+def test_shared_experts_with_streaming_offload(dev, monkeypatch):
+    banner("shared experts + streaming offload")
+    E, K, H, I, T = 8, 2, 512, 256, 24
+    ref_moe, _, _ = _build_shared(E, K, H, I, torch.bfloat16, n_shared=2)
+    ref_moe = ref_moe.to(dev)
+    x = synth.make_tokens(T, H, torch.bfloat16, seed=2).to(dev)
+    want = ref_moe(x).float()
+    moe, _, _ = _build_shared(E, K, H, I, torch.bfloat16, n_shared=2)
+    moe.gate.data = moe.gate.data.to(dev)
+    for p in list(moe.shared_w1) + list(moe.shared_w2):
+        p.data = p.data.to(dev)
+    moe.build_offload_cache(dev, lru_capacity=3)
+    monkeypatch.setenv("RE_CHUNK_SIZE", "3")
+    got = moe(x).float()
+    monkeypatch.delenv("RE_CHUNK_SIZE")
+    monkeypatch.setenv("RE_MAX_PACK", "8")
+    got_pack = moe(x).float()
+    torch.cuda.synchronize()
+    for g in (got, got_pack):
+        err = (g - want).abs().max().item() / want.abs().max().item()
+        assert err <= 1e-2
