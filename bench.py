@@ -39,6 +39,10 @@ def parse():
     ap.add_argument("--tokens", type=int, default=4096)
     ap.add_argument("--decode", type=str, default="1,16,256",
                     help="comma-separated token counts reported beside the headline ('' = none)")
+    ap.add_argument("--configs", type=str, default="phi35moe,finegrained,offload",
+                    help="other workloads reported beside the headline ('' = none)")
+    ap.add_argument("--offload-layers", type=int, default=4)
+    ap.add_argument("--offload-steps", type=int, default=48)
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--profile", type=int, default=0,
@@ -50,21 +54,24 @@ def parse():
 
 
 class Layer:
-    """Mixtral-shape layer weights and the libmoe355 stage calls of one forward."""
+    """One MoE layer's weights (bf16, N(0, 0.02), generated on the GPU) and
+    the libmoe355 stage calls of its forward. Default: the Mixtral shape with
+    a fixed per-expert router bias N(0, 0.5^2)."""
 
-    def __init__(self, dev, seed=0):
+    def __init__(self, dev, seed=0, hidden=H, experts=E, top_k=K, ffn=I, bias=None):
         import torch
 
         from reframework_amd import synth
 
+        self.H, self.E, self.K, self.I = hidden, experts, top_k, ffn
         g = torch.Generator(device=dev).manual_seed(seed)
         self.dev = dev
-        self.gate = (torch.randn(E, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-        self.w1 = [(torch.randn(2 * I, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-                   for _ in range(E)]
-        self.w2 = [(torch.randn(H, I, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-                   for _ in range(E)]
-        self.bias = synth.mixtral_router_bias(E, seed).to(dev)
+        self.gate = (torch.randn(experts, hidden, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        self.w1 = [(torch.randn(2 * ffn, hidden, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+                   for _ in range(experts)]
+        self.w2 = [(torch.randn(hidden, ffn, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+                   for _ in range(experts)]
+        self.bias = (synth.mixtral_router_bias(experts, seed) if bias is None else bias).to(dev)
         self.w1p = [w.data_ptr() for w in self.w1]
         self.w2p = [w.data_ptr() for w in self.w2]
 
@@ -72,7 +79,7 @@ class Layer:
         import torch
 
         g = torch.Generator(device=self.dev).manual_seed(seed)
-        return torch.randn(T, H, generator=g, device=self.dev).to(torch.bfloat16)
+        return torch.randn(T, self.H, generator=g, device=self.dev).to(torch.bfloat16)
 
 
 def run_layer(layer, x, bufs, events=None):
@@ -81,7 +88,7 @@ def run_layer(layer, x, bufs, events=None):
 
     plan, ws, w, ids, out = bufs
     s = _capi.stream_handle(x.device)
-    _capi.router_topk(x, layer.gate, layer.bias, K, True, True, 0, w, ids, stream=s)
+    _capi.router_topk(x, layer.gate, layer.bias, layer.K, True, True, 0, w, ids, stream=s)
     _capi.permute(plan, ids, ws, stream=s)
     if events:
         events[0].record()
@@ -99,11 +106,11 @@ def make_bufs(layer, T):
 
     from reframework_amd import _capi
 
-    plan = _capi.make_plan(T, H, I, E, K, _capi.BF16)
+    plan = _capi.make_plan(T, layer.H, layer.I, layer.E, layer.K, _capi.BF16)
     ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=layer.dev)
-    w = torch.empty(T, K, dtype=torch.float32, device=layer.dev)
-    ids = torch.empty(T, K, dtype=torch.int32, device=layer.dev)
-    out = torch.empty(T, H, dtype=torch.bfloat16, device=layer.dev)
+    w = torch.empty(T, layer.K, dtype=torch.float32, device=layer.dev)
+    ids = torch.empty(T, layer.K, dtype=torch.int32, device=layer.dev)
+    out = torch.empty(T, layer.H, dtype=torch.bfloat16, device=layer.dev)
     return plan, ws, w, ids, out
 
 
@@ -178,6 +185,158 @@ def cpu_baseline(layer, T):
                       f"{len(times)} run(s) of {med:.2f} s on {model or 'host CPU'}"}
 
 
+def _rates(flops, alg_bytes, ms):
+    sec = ms / 1000.0
+    return {"tflops": round(flops / sec / 1e12, 2),
+            "mfma_frac": round(flops / sec / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "hbm_gb_s": round(alg_bytes / sec / 1e9, 1),
+            "hbm_frac": round(alg_bytes / sec / 1e9 / PEAK_HBM_GBS, 4)}
+
+
+def config_phi35moe(dev, steps, warmup, T=2048):
+    """Phi-3.5-MoE shape: hidden 4096, 16 experts, top-2, ffn 6400, 2048
+    tokens, router bias log Zipf(1.1) over a seeded expert ranking."""
+    import torch
+
+    from reframework_amd import synth
+
+    h, e, k, i = 4096, 16, 2, 6400
+    layer = Layer(dev, hidden=h, experts=e, top_k=k, ffn=i, bias=synth.zipf_router_bias(e, 1.1))
+    m = measure(layer, T, steps, warmup)
+    flops = 6.0 * T * k * h * i + 2.0 * T * h * e
+    alg = m["routed_experts"] * 3 * h * i * 2 + e * h * 2 + 2 * T * h * 2
+    res = {"workload": "phi-3.5-moe-shape layer forward", "tokens": T, "hidden": h, "experts": e,
+           "top_k": k, "ffn": i, "ms": round(m["ms"], 4),
+           "tokens_per_s": round(T / (m["ms"] / 1000.0), 1), "routed_experts": m["routed_experts"],
+           "gate_up_ms": round(m["gate_up_ms"], 4), "down_ms": round(m["down_ms"], 4),
+           "flops": flops, "alg_bytes": alg, **_rates(flops, alg, m["ms"])}
+    del layer
+    torch.cuda.empty_cache()
+    return res
+
+
+def _time_forward(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1000.0 / steps
+
+
+def config_finegrained(dev, steps, warmup, tokens=(8, 4096)):
+    """Fine-grained shape: hidden 2048, 64 experts, top-6 (renormalised), ffn
+    1408, plus 2 shared experts of 1408, through FusedMoE.forward."""
+    import torch
+
+    from reframework_amd.moe import FusedMoE
+
+    h, e, k, i, ns = 2048, 64, 6, 1408, 2
+    moe = FusedMoE(e, k, h, i, dtype=torch.bfloat16, n_shared_experts=ns).to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    with torch.no_grad():
+        for prm in moe.parameters():
+            prm.copy_(torch.randn(prm.shape, generator=g, device=dev) * 0.02)
+    out = {}
+    for T in tokens:
+        x = (torch.randn(T, h, generator=g, device=dev)).to(torch.bfloat16)
+        ms = _time_forward(lambda: moe(x), max(steps, 20), warmup)
+        _, ids = moe.route(x)
+        n_routed = int(torch.unique(ids).numel())
+        flops = 6.0 * T * k * h * i + 2.0 * T * h * e + 6.0 * T * h * i * ns
+        alg = (n_routed + ns) * 3 * h * i * 2 + e * h * 2 + 2 * T * h * 2
+        out[str(T)] = {"ms": round(ms, 4), "tokens_per_s": round(T / (ms / 1000.0), 1),
+                       "routed_experts": n_routed, "flops": flops, "alg_bytes": alg,
+                       **_rates(flops, alg, ms)}
+    del moe
+    torch.cuda.empty_cache()
+    return {"workload": "fine-grained moe layer forward (64 routed + 2 shared experts)",
+            "hidden": h, "experts": e, "top_k": k, "ffn": i, "shared_experts": ns, "tokens": out}
+
+
+def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
+    """Decode through per-layer expert offload caches (the reference's
+    semantics: lru_capacity 2 per layer, RE_MAX_PACK=2 truncation): Mixtral-
+    shape layers whose experts live in one pinned host pool per layer;
+    routing is the synthetic trace (p=0.7 repeat, Zipf(1.2)); misses stream
+    host->HBM on the cache's copy stream."""
+    import torch
+
+    from reframework_amd import _capi, synth
+    from reframework_amd.moe import FusedMoE
+
+    h, e, k, i = 4096, 8, 2, 14336
+    g = torch.Generator(device=dev).manual_seed(0)
+    layers = []
+    for _ in range(n_layers):
+        moe = FusedMoE(e, k, h, i, dtype=torch.bfloat16).to(dev)
+        with torch.no_grad():
+            for prm in moe.parameters():
+                prm.copy_(torch.randn(prm.shape, generator=g, device=dev) * 0.02)
+        cache = moe.build_offload_cache(dev, lru_capacity=2)
+        cache.log_copies(True)
+        layers.append(moe)
+    torch.cuda.synchronize()
+    # peak pinned H2D on this host: one 1 GiB copy through the same entry point
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+    cs = torch.cuda.Stream(dev)
+    _capi.h2d_async(dst.data_ptr(), src.data_ptr(), n >> 4, cs.cuda_stream)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(cs)
+    _capi.h2d_async(dst.data_ptr(), src.data_ptr(), n, cs.cuda_stream)
+    b.record(cs)
+    b.synchronize()
+    peak_h2d = n / (a.elapsed_time(b) / 1000.0) / 1e9
+    del src, dst
+
+    ids_all, w_all = synth.offload_trace(n_layers, warmup_steps + steps, T, e)
+    ids_d = torch.from_numpy(ids_all).to(dev)
+    w_d = torch.from_numpy(w_all).to(dev)
+    x = (torch.randn(T, h, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    act = 0
+
+    def step(st):
+        y = x
+        for li, moe in enumerate(layers):
+            y = moe._forward_offload(T, y, w_d[st, li], ids_d[st, li], act)
+        return y
+
+    for st in range(warmup_steps):
+        step(st)
+    torch.cuda.synchronize()
+    for moe in layers:
+        moe._cache.stats.reset()
+        moe._cache.log_copies(True)
+    t0 = time.perf_counter()
+    for st in range(warmup_steps, warmup_steps + steps):
+        step(st)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    hits = sum(m._cache.stats.hits for m in layers)
+    misses = sum(m._cache.stats.misses for m in layers)
+    nbytes, copy_ms = 0, 0.0
+    for m in layers:
+        b_, ms_ = m._cache.copy_summary()
+        nbytes += b_
+        copy_ms += ms_
+    res = {"workload": "offload decode, mixtral-shape layers, per-layer lru 2, RE_MAX_PACK 2",
+           "layers": n_layers, "tokens": T, "steps": steps,
+           "tokens_per_s": round(T * steps / sec, 2), "ms_per_step": round(sec * 1000.0 / steps, 3),
+           "hit_rate": round(hits / max(1, hits + misses), 4), "hits": hits, "misses": misses,
+           "h2d_gb_s": round(nbytes / (copy_ms / 1000.0) / 1e9, 2) if copy_ms > 0 else None,
+           "h2d_bytes": nbytes, "peak_pinned_h2d_gb_s": round(peak_h2d, 2),
+           "copy_time_frac": round(copy_ms / 1000.0 / sec, 4)}
+    del layers
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -228,6 +387,16 @@ def main():
             "gate_up_ms": round(m["gate_up_ms"], 4), "down_ms": round(m["down_ms"], 4),
             "path": m["plan_path"], "down_splits": m["down_splits"]}
 
+    configs = {}
+    names = [v.strip() for v in args.configs.split(",") if v.strip()]
+    if "phi35moe" in names:
+        configs["phi35moe"] = config_phi35moe(dev, max(args.steps // 2, 5), args.warmup)
+    if "finegrained" in names:
+        configs["finegrained"] = config_finegrained(dev, args.steps, args.warmup)
+    if "offload" in names:
+        configs["offload_decode"] = config_offload_decode(dev, args.offload_layers,
+                                                          args.offload_steps)
+
     cpu = None
     if not args.skip_cpu:
         cpu = cpu_baseline(layer, args.cpu_sample_tokens)
@@ -254,6 +423,7 @@ def main():
                          "gate_up_ms": round(head["gate_up_ms"], 4),
                          "down_ms": round(head["down_ms"], 4)},
         "decode": decode,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 

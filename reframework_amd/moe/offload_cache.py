@@ -196,6 +196,7 @@ class ExpertOffloadCache:
         self._free_slots: List[_Slot] = []
         self._n_slots = 0
         self._copy_stream: Optional[torch.cuda.Stream] = None
+        self._copy_log: Optional[List[Tuple[torch.cuda.Event, torch.cuda.Event, int]]] = None
         self._n1 = 0
         self._n2 = 0
 
@@ -328,6 +329,20 @@ class ExpertOffloadCache:
         except Exception as exc:  # best effort, like the reference's probe
             logger.warning("host->HBM bandwidth measure failed: %s", exc)
             return None
+
+    def log_copies(self, on: bool = True) -> None:
+        """Time every miss copy with HIP events on the copy stream (off by
+        default; costs two events per miss)."""
+        self._copy_log = [] if on else None
+
+    def copy_summary(self) -> Tuple[int, float]:
+        """(bytes, milliseconds) summed over the logged miss copies; waits for
+        them to finish."""
+        if not self._copy_log:
+            return 0, 0.0
+        self._copy_log[-1][1].synchronize()
+        return (sum(n for _, _, n in self._copy_log),
+                sum(a.elapsed_time(b) for a, b, _ in self._copy_log))
 
     def reset_lru(self) -> None:
         self._release_all()
@@ -490,9 +505,15 @@ class ExpertOffloadCache:
             if slot.free_after is not None:
                 cs.wait_event(slot.free_after)
             src = self._host_buf.data_ptr() + self._host_off[idx] * self._host_buf.element_size()
+            t0 = None
+            if self._copy_log is not None:
+                t0 = torch.cuda.Event(enable_timing=True)
+                t0.record(cs)
             _capi.h2d_async(slot.buf.data_ptr(), src, nbytes, cs.cuda_stream)
-            ev = torch.cuda.Event()
+            ev = torch.cuda.Event(enable_timing=t0 is not None)
             ev.record(cs)
+            if t0 is not None:
+                self._copy_log.append((t0, ev, nbytes))
             slot.ready = ev
             slot.refs = 1
             self._slot_of[idx] = slot

@@ -105,6 +105,39 @@ def make_shared(n: int, H: int, I: int, dtype: torch.dtype, seed: int = 0,
             "down_proj": torch.cat(w2, dim=1) if n else None}
 
 
+def offload_trace(n_layers: int, steps: int, T: int, E: int, seed: int = 0,
+                  p_repeat: float = 0.7, zipf_s: float = 1.2):
+    """Synthetic decode routing for offload runs (bypasses the router).
+
+    Per layer and token: with probability ``p_repeat`` the previous step's
+    expert pair again, else two distinct experts drawn from Zipf(``zipf_s``)
+    popularity over a seeded per-layer rank permutation. Weights are the
+    softmax of two N(0,1) logits, largest first. Returns (ids int32, w fp32),
+    both [steps, n_layers, T, 2].
+    """
+    rng = np.random.Generator(np.random.PCG64([seed, STREAM_TRACE]))
+    pops = []
+    for _ in range(n_layers):
+        ranks = np.empty(E, dtype=np.int64)
+        ranks[rng.permutation(E)] = np.arange(1, E + 1)
+        pop = ranks.astype(np.float64) ** (-zipf_s)
+        pops.append(pop / pop.sum())
+    ids = np.zeros((steps, n_layers, T, 2), dtype=np.int32)
+    w = np.zeros((steps, n_layers, T, 2), dtype=np.float32)
+    for st in range(steps):
+        for li in range(n_layers):
+            for t in range(T):
+                if st > 0 and rng.random() < p_repeat:
+                    ids[st, li, t] = ids[st - 1, li, t]
+                else:
+                    ids[st, li, t] = rng.choice(E, size=2, replace=False, p=pops[li])
+                lg = rng.standard_normal(2)
+                pr = np.exp(lg - lg.max())
+                pr = np.sort(pr / pr.sum())[::-1]
+                w[st, li, t] = pr
+    return ids, w
+
+
 def make_tokens(T: int, H: int, dtype: torch.dtype, seed: int = 0) -> torch.Tensor:
     return to_dtype(normal(T * H, STREAM_X, seed, 1.0).reshape(T, H), dtype)
 
@@ -125,6 +158,6 @@ def zipf_router_bias(E: int, s: float, seed: int = 0) -> torch.Tensor:
 
 __all__ = [
     "splitmix64", "uniform", "normal", "to_dtype", "MoEShape", "SHAPES", "make_layer",
-    "make_shared",
+    "make_shared", "offload_trace",
     "make_tokens", "mixtral_router_bias", "zipf_router_bias",
 ]
