@@ -185,6 +185,18 @@ def cpu_baseline(layer, T):
                       f"{len(times)} run(s) of {med:.2f} s on {model or 'host CPU'}"}
 
 
+def measured_traffic(T):
+    """HBM-side bytes per gate_up launch at this workload from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE profile (copy-calibrated), or None when
+    no profile covers it. Counters cannot be read from inside the timed run."""
+    path = os.path.join(ROOT, "profiles", "traffic_gate_up_mixtral_t4096.json")
+    if T != 4096 or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    return rec.get("traffic_bytes_per_launch")
+
+
 def _rates(flops, alg_bytes, ms):
     sec = ms / 1000.0
     return {"tflops": round(flops / sec / 1e12, 2),
@@ -370,7 +382,8 @@ def main():
     achieved = gemm1_flops / (head["gate_up_ms"] / 1000.0) / 1e12
     grouped = (gemm1_flops + gemm2_flops) / ((head["gate_up_ms"] + head["down_ms"]) / 1000.0) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": measured_traffic(T),
                 "kernel": "ffn_tiled_kernel<bf16, gate_up>",
                 "flops_per_launch": gemm1_flops, "avg_launch_ms": round(head["gate_up_ms"], 4)}
 
