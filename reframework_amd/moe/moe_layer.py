@@ -134,6 +134,8 @@ class FusedMoE(BaseOP):
             torch.nn.Parameter(torch.empty(hidden_size, piece, dtype=dtype))
             for _ in range(n_pieces)
         ])
+        self._checked_tables: set = set()
+        self._shared_cols = None  # cached (key, shared expert ids [T,n], unit weights [T,n])
         self._cache: Optional[ExpertOffloadCache] = None
         self._cpu_split_enabled: bool = False
         self._predictor: Optional[Prediction] = None
@@ -253,16 +255,25 @@ class FusedMoE(BaseOP):
         return self._pointers(self.experts_w1, self.experts_w2)
 
     def _pointers(self, w1s, w2s) -> Tuple[List[int], List[int]]:
-        w1p, w2p = [], []
-        for p1, p2 in zip(w1s, w2s):
-            if p1.device.type != "cuda" or p2.device.type != "cuda":
-                raise RuntimeError("expert parameters must be on the GPU")
-            if p1.dtype != self.dtype or p2.dtype != self.dtype:
-                raise RuntimeError("expert parameters must be in the layer dtype")
-            if not (p1.is_contiguous() and p2.is_contiguous()):
-                raise RuntimeError("expert parameters must be contiguous")
-            w1p.append(p1.data_ptr())
-            w2p.append(p2.data_ptr())
+        """Device pointers of per-expert matrices. The checks (GPU, layer dtype,
+        contiguous) run once per distinct pointer table; at decode sizes the
+        per-parameter checks would otherwise cost more than the kernels."""
+        p1 = list(w1s._parameters.values()) if isinstance(w1s, torch.nn.ParameterList) else list(w1s)
+        p2 = list(w2s._parameters.values()) if isinstance(w2s, torch.nn.ParameterList) else list(w2s)
+        w1p = [t.data_ptr() for t in p1]
+        w2p = [t.data_ptr() for t in p2]
+        key = (tuple(w1p), tuple(w2p))
+        if key not in self._checked_tables:
+            for t1, t2 in zip(p1, p2):
+                if t1.device.type != "cuda" or t2.device.type != "cuda":
+                    raise RuntimeError("expert parameters must be on the GPU")
+                if t1.dtype != self.dtype or t2.dtype != self.dtype:
+                    raise RuntimeError("expert parameters must be in the layer dtype")
+                if not (t1.is_contiguous() and t2.is_contiguous()):
+                    raise RuntimeError("expert parameters must be contiguous")
+            if len(self._checked_tables) >= 16:
+                self._checked_tables.clear()
+            self._checked_tables.add(key)
         return w1p, w2p
 
     @property
@@ -284,10 +295,15 @@ class FusedMoE(BaseOP):
         s1, s2 = self._pointers(self.shared_w1, self.shared_w2)
         T, n = xd.shape[0], len(s1)
         if self._shared_folded:
-            ids_x = torch.arange(self.num_experts, self.num_experts + n, dtype=ids.dtype,
-                                 device=ids.device).expand(T, n)
-            ids2 = torch.cat([ids, ids_x], dim=1).contiguous()
-            w2_ = torch.cat([w, torch.ones((T, n), dtype=w.dtype, device=w.device)], dim=1)
+            key = (T, n, ids.dtype, ids.device)
+            if self._shared_cols is None or self._shared_cols[0] != key:
+                ids_x = torch.arange(self.num_experts, self.num_experts + n, dtype=ids.dtype,
+                                     device=ids.device).expand(T, n)
+                self._shared_cols = (key, ids_x, torch.ones((T, n), dtype=torch.float32,
+                                                            device=ids.device))
+            _, ids_x, ones = self._shared_cols
+            ids2 = torch.cat([ids, ids_x], dim=1)
+            w2_ = torch.cat([w, ones], dim=1)
             base = len(w1p)
             if expert_map is None:
                 emap = None if base == self.num_experts else \
