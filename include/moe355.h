@@ -55,6 +55,7 @@ extern "C" {
 #define MOE355_PATH_MFMA_TILED 0 /* 256x256 bf16/f16 MFMA tiles, prefill-sized groups */
 #define MOE355_PATH_MFMA_SKINNY 1 /* weight-streaming 16x16x32 MFMA, decode-sized groups */
 #define MOE355_PATH_SIMT 2        /* fp32 FMA tiles: fp32 layers and unaligned shapes */
+#define MOE355_PATH_MFMA_MEDIUM 3 /* 256x64 bf16/f16 MFMA tiles, medium groups */
 
 /* Execution plan of one fused_experts call. Filled by moe355_make_plan() from
  * the shape alone (no device data), so every stage sees the same layout. */
@@ -109,8 +110,17 @@ int moe355_router_topk(const void* x, const void* gate, const float* bias, int T
 int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renormalize,
                             float* topk_w, int32_t* topk_ids, void* stream);
 
-/* Fill `plan` for a fused_experts call of this shape. Host-only, no HIP calls. */
+/* Fill `plan` for a fused_experts call of this shape. Host-side; reads the
+ * current device's CU count (256 without a device) to choose the down
+ * projection's K-split, and launches nothing. */
 int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* plan);
+
+/* moe355_make_plan with the kernel family forced (`path` = MOE355_PATH_*, or -1
+ * for the automatic choice); MOE355_EUNSUPPORTED if that family cannot run the
+ * shape. No counterpart in the reference: for tests and tuning, so that every
+ * family can be checked at any shape. */
+int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path,
+                          moe355_plan* plan);
 
 /*
  * Stable counting sort of the routed slots by expert.

@@ -24,7 +24,7 @@ HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__fil
 
 F32, BF16, F16 = 0, 1, 2
 ACT_CODES = {"silu": 0, "gelu": 1, "gelu_tanh": 2}
-PATH_MFMA_TILED, PATH_MFMA_SKINNY, PATH_SIMT = 0, 1, 2
+PATH_MFMA_TILED, PATH_MFMA_SKINNY, PATH_SIMT, PATH_MFMA_MEDIUM = 0, 1, 2, 3
 MAX_EXPERTS = 256
 
 _DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -73,6 +73,7 @@ _SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "moe355_router_topk": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "moe355_topk_from_logits": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "moe355_make_plan": (_I, [_I, _I, _I, _I, _I, _I, _PPLAN]),
+    "moe355_make_plan_path": (_I, [_I, _I, _I, _I, _I, _I, _I, _PPLAN]),
     "moe355_permute": (_I, [_PPLAN, _P, _I, _PI32, _I, _P, _P]),
     "moe355_gate_up": (_I, [_PPLAN, _P, _PP, _I, _P, _P]),
     "moe355_down": (_I, [_PPLAN, _PP, _P, _P]),
@@ -155,9 +156,15 @@ def version() -> int:
     return int(lib().moe355_version())
 
 
-def make_plan(T: int, H: int, I: int, E: int, K: int, dtype: int) -> Plan:
+def make_plan(T: int, H: int, I: int, E: int, K: int, dtype: int, path: int = -1) -> Plan:
+    """Execution plan of a fused_experts call; ``path`` forces a kernel family
+    (PATH_*), -1 lets the library choose."""
     plan = Plan()
-    _check("moe355_make_plan", lib().moe355_make_plan(T, H, I, E, K, dtype, ctypes.byref(plan)))
+    if path < 0:
+        _check("moe355_make_plan", lib().moe355_make_plan(T, H, I, E, K, dtype, ctypes.byref(plan)))
+    else:
+        _check("moe355_make_plan_path",
+               lib().moe355_make_plan_path(T, H, I, E, K, dtype, path, ctypes.byref(plan)))
     return plan
 
 
@@ -219,11 +226,21 @@ def combine(plan: Plan, topk_w: torch.Tensor, out: torch.Tensor, accumulate_f32:
 def fused_experts(x: torch.Tensor, w1_ptrs: Sequence[int], w2_ptrs: Sequence[int], I: int,
                   topk_w: torch.Tensor, topk_ids: torch.Tensor, act: int, out: torch.Tensor,
                   workspace: torch.Tensor, expert_map: Optional[Sequence[int]] = None,
-                  accumulate_f32: bool = False, stream: Optional[int] = None) -> None:
+                  accumulate_f32: bool = False, stream: Optional[int] = None,
+                  plan: Optional[Plan] = None) -> None:
+    """The whole routed-expert computation. With a ``plan`` whose kernel family
+    was forced (make_plan(..., path)), the four stages run one by one on that
+    plan; otherwise one moe355_fused_experts call plans for itself."""
     T, H = x.shape
     K = topk_ids.shape[1]
     E = len(w1_ptrs)
     s = stream if stream is not None else stream_handle(x.device)
+    if plan is not None and plan.path != make_plan(T, H, I, E, K, dtype_code(x.dtype)).path:
+        permute(plan, topk_ids, workspace, expert_map=expert_map, stream=s)
+        gate_up(plan, x, w1_ptrs, act, workspace, stream=s)
+        down(plan, w2_ptrs, workspace, stream=s)
+        combine(plan, topk_w, out, accumulate_f32, workspace, stream=s)
+        return
     t1, _k1 = _ptr_table(w1_ptrs)
     t2, _k2 = _ptr_table(w2_ptrs)
     if expert_map:

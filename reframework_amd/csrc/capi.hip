@@ -45,7 +45,7 @@ T* at(void* ws, size_t off) {
 int check_plan(const moe355_plan* p) {
   if (!p) return fail(MOE355_EINVAL, "plan is NULL");
   if (p->E < 1 || p->E > MOE355_MAX_EXPERTS || p->K < 1 || p->K > p->E || !valid_dtype(p->dtype) ||
-      p->path < 0 || p->path > MOE355_PATH_SIMT || p->rows != p->T * p->K)
+      p->path < 0 || p->path > MOE355_PATH_MFMA_MEDIUM || p->rows != p->T * p->K)
     return fail(MOE355_EINVAL, "plan is not one filled by moe355_make_plan");
   return MOE355_OK;
 }
@@ -91,7 +91,13 @@ int moe355_version(void) { return 100; }
 const char* moe355_last_error(void) { return g_err; }
 
 int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* p) {
+  return moe355_make_plan_path(T, H, I, E, K, dtype, -1, p);
+}
+
+int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path,
+                          moe355_plan* p) {
   if (!p) return fail(MOE355_EINVAL, "plan is NULL");
+  if (path < -1 || path > MOE355_PATH_MFMA_MEDIUM) return fail(MOE355_EINVAL, "unknown path %d", path);
   if (T < 0 || H <= 0 || I <= 0) return fail(MOE355_EINVAL, "bad sizes T=%d H=%d I=%d", T, H, I);
   if (E < 1 || E > MOE355_MAX_EXPERTS)
     return fail(MOE355_EUNSUPPORTED, "E=%d outside [1, %d]", E, MOE355_MAX_EXPERTS);
@@ -116,22 +122,30 @@ int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* 
                         static_cast<long long>(T) * H * esz < (1ll << 32) &&
                         2ll * I * H * esz < (1ll << 32);
   const bool skinny_ok = mfma && H % 128 == 0 && I % 128 == 0;
-  if (tiled_ok && avg > 32) {
-    p->path = MOE355_PATH_MFMA_TILED;
-    p->tile_rows = 256;
-  } else if (skinny_ok) {
-    p->path = MOE355_PATH_MFMA_SKINNY;
-    p->tile_rows = 16;
-  } else {
-    p->path = MOE355_PATH_SIMT;
-    p->tile_rows = 64;
+  if (path < 0) {
+    // Average rows per active expert decide: weight streaming with 16-token
+    // tiles up to 32, 64-token tiles up to 96, 256-token tiles above (the
+    // 64-row kernel wins only where a 256-row tile would be three-quarters
+    // padding; from ~128 rows the bigger tile's reuse pays more).
+    path = tiled_ok && avg > 96   ? MOE355_PATH_MFMA_TILED
+           : tiled_ok && avg > 32 ? MOE355_PATH_MFMA_MEDIUM
+           : skinny_ok            ? MOE355_PATH_MFMA_SKINNY
+                                  : MOE355_PATH_SIMT;
+  } else if (((path == MOE355_PATH_MFMA_TILED || path == MOE355_PATH_MFMA_MEDIUM) && !tiled_ok) ||
+             (path == MOE355_PATH_MFMA_SKINNY && !skinny_ok)) {
+    return fail(MOE355_EUNSUPPORTED, "path %d cannot run dtype %d with H=%d I=%d T=%d", path,
+                dtype, H, I, T);
   }
+  p->path = path;
+  p->tile_rows = path == MOE355_PATH_MFMA_TILED    ? 256
+                 : path == MOE355_PATH_MFMA_SKINNY ? 16
+                                                   : 64;
   p->max_tiles = R > 0 ? static_cast<int>((R + static_cast<long long>(act_e) * (p->tile_rows - 1)) /
                                           p->tile_rows)
                        : 0;
   p->down_splits = 1;
-  if (p->path == MOE355_PATH_MFMA_TILED) {
-    // The persistent down kernel runs (H/256 weight tiles x token tiles x
+  if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_MEDIUM) {
+    // The persistent down kernels run (H/256 weight tiles x token tiles x
     // splits) work items of I/(32*splits) k-steps on one workgroup per CU.
     // Pick the split that minimises the busiest CU's step count, charging each
     // extra split its fp32 partial plane (written once, read by the combine)
@@ -254,6 +268,9 @@ int moe355_gate_up(const moe355_plan* p, const void* x, const void* const* w1, i
   if (p->path == MOE355_PATH_MFMA_TILED) {
     a.n_wtiles = p->I / 128;
     err = launch_gate_up_tiled(a, p->dtype, as_stream(stream));
+  } else if (p->path == MOE355_PATH_MFMA_MEDIUM) {
+    a.n_wtiles = p->I / 128;
+    err = launch_gate_up_medium(a, p->dtype, as_stream(stream));
   } else if (p->path == MOE355_PATH_MFMA_SKINNY) {
     a.n_wtiles = p->I / 16;
     err = launch_gate_up_skinny(a, p->dtype, as_stream(stream));
@@ -283,6 +300,9 @@ int moe355_down(const moe355_plan* p, const void* const* w2, void* workspace, vo
   if (p->path == MOE355_PATH_MFMA_TILED) {
     a.n_wtiles = p->H / 256;
     err = launch_down_tiled(a, p->dtype, as_stream(stream));
+  } else if (p->path == MOE355_PATH_MFMA_MEDIUM) {
+    a.n_wtiles = p->H / 256;
+    err = launch_down_medium(a, p->dtype, as_stream(stream));
   } else if (p->path == MOE355_PATH_MFMA_SKINNY) {
     a.n_wtiles = p->H / 16;
     err = launch_down_skinny(a, p->dtype, as_stream(stream));

@@ -24,81 +24,21 @@
 // free. The kernel is persistent (one workgroup per CU) and streams its K-steps
 // across tile boundaries, so each tile's pipeline fill overlaps the previous
 // tile's epilogue.
-#include "common.h"
+#include "dma_pipe.h"
 
 namespace moe355 {
 namespace {
 
+using namespace pipe;
+
 constexpr int kThreads = 256;
 constexpr int kTileW = 256;
 constexpr int kTileT = 256;
-constexpr int kBK = 32;
-constexpr int kRowBytes = kBK * 2;                    // 64 B: 4 chunks of 16 B
 constexpr int kRegionBytes = kTileW * kRowBytes;      // 16 KB
 constexpr int kStageBytes = 2 * kRegionBytes;         // weights + tokens
 constexpr int kStages = 5;
 constexpr int kLdsBytes = kStages * kStageBytes;      // 160 KB: the whole LDS
 constexpr int kLoadsPerWave = kStageBytes / 1024 / (kThreads / kWave);  // 8 x 1 KB
-
-// Physical 16-byte chunk of logical chunk c (0..3) in LDS row r (64 B). Four
-// consecutive rows fill one 256-byte span of a 64-bank LDS; XOR with
-// (r >> 2) & 3 gives the four such spans of any 16 consecutive rows different
-// chunk columns, so 16 rows read at one logical chunk hit 16 distinct 16-byte
-// bank groups.
-__device__ __forceinline__ uint32_t swz(int c, int r) {
-  return static_cast<uint32_t>(c ^ ((r >> 2) & 3));
-}
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-// s_waitcnt that waits until at most n vector-memory operations are
-// outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
-// left at their maxima, i.e. not waited on).
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Workgroup barrier after which the direct-to-LDS loads older than the newest
-// n of every wave are visible to all waves. __syncthreads() would wait for all
-// vector-memory operations (vmcnt(0)), draining the load pipeline; the signal
-// fences only stop the compiler from moving memory accesses across.
-template <int n>
-__device__ __forceinline__ void dma_barrier() {
-  wait_vmcnt<n>();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// One 1 KB direct-to-LDS load per wave: lane i's 16 bytes land at dst + 16 i.
-__device__ __forceinline__ void dma16(const void* src, uint8_t* dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void*)(dst), 16, 0, 0);
-}
-
-template <typename T>
-struct Mfma32;
-
-template <>
-struct Mfma32<bf16> {
-  __device__ __forceinline__ static f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-};
-
-template <>
-struct Mfma32<f16> {
-  __device__ __forceinline__ static f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-};
-
-struct Tile {
-  int split, wtile, e, row0, row_end;
-};
 
 // Persistent: one workgroup per CU walks work items L = L0, L0 + G, ... (G =
 // grid size) of the (split, weight tile, token tile) space. Its K-steps form
@@ -126,17 +66,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
   const uint32_t pitch = static_cast<uint32_t>(ld * 2);
   const int nk = a.k_per_split / kBK;
 
-  auto decode = [&](int L) {
-    Tile t;
-    t.split = L / per_split;
-    const int rem = L - t.split * per_split;
-    t.wtile = rem / n_t;
-    const int tt = rem - t.wtile * n_t;
-    t.e = a.tile_map[2 + 2 * tt];
-    t.row0 = a.tile_map[3 + 2 * tt];
-    t.row_end = min(t.row0 + kTileT, a.offsets[t.e + 1]);
-    return t;
-  };
+  auto decode = [&](int L) { return decode_tile(a, L, per_split, n_t, kTileT); };
 
   // Stage = 32 loads of 1 KB (16 rows x 64 B each). Waves 0-1 fill the weight
   // region, waves 2-3 the token region, 8 loads each: load q of wave w covers
@@ -268,7 +198,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
 
   u32x4 fa[2][4], fb[2][4];
   read_frags(lds, 0, fa[0], fb[0]);
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  wait_lgkm0();
 
   // Each half: wait for its operands (read during the previous half), then 16
   // MFMAs. The next half's 8 operand reads and half of the next stage's loads
@@ -277,7 +207,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
   // the last read still has 4 MFMAs to land.
   auto half = [&](const u32x4* af, const u32x4* bf, const uint8_t* src, int ks, u32x4* na,
                   u32x4* nb, uint8_t* lb, int q0) {
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    wait_lgkm0();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -316,7 +246,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
       half(fa[0], fb[0], st, 1, fa[1], fb[1], lb, 0);
       // Step g+1 landed (everything but steps g+2, g+3 and the first half of
       // g+4 is done) and every wave finished reading step g-1's buffer.
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      wait_lgkm0();
       dma_barrier<(kStages - 3) * kLoadsPerWave + kLoadsPerWave / 2>();
       half(fa[1], fb[1], nx, 0, fa[0], fb[0], lb, kLoadsPerWave / 2);
       advance_load();

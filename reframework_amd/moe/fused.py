@@ -93,12 +93,15 @@ def run_experts(
     out: Optional[torch.Tensor] = None,
     expert_map: Optional[Sequence[int]] = None,
     accumulate_f32: bool = False,
+    path: int = -1,
 ) -> torch.Tensor:
     """One libmoe355 fused_experts call on the current stream.
 
     x [T,H] contiguous in the bank dtype; topk_weights [T,K] fp32; topk_ids
     [T,K] int32/int64; ids are local bank rows unless ``expert_map`` renames
     them. With ``accumulate_f32`` the result is added to the fp32 ``out``.
+    ``path`` forces a kernel family (``_capi.PATH_*``); -1 lets the library
+    choose from the shape.
     """
     T, H = x.shape
     if out is None:
@@ -108,10 +111,11 @@ def run_experts(
         return out
     stream = _capi.stream_handle(x.device)
     plan = _capi.make_plan(T, H, intermediate_size, len(w1_ptrs), topk_ids.shape[1],
-                           _capi.dtype_code(x.dtype))
+                           _capi.dtype_code(x.dtype), path)
     ws = _capi.workspaces.get(x.device, stream, plan.workspace_bytes)
     _capi.fused_experts(x, w1_ptrs, w2_ptrs, intermediate_size, topk_weights, topk_ids, act, out,
-                        ws, expert_map=expert_map, accumulate_f32=accumulate_f32, stream=stream)
+                        ws, expert_map=expert_map, accumulate_f32=accumulate_f32, stream=stream,
+                        plan=plan)
     return out
 
 

@@ -40,7 +40,8 @@ def skewed_ids(T: int, K: int, E: int, seed: int, skew: float = 1.0) -> np.ndarr
 
 def gpu_fused(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch.Tensor],
               topk_w: np.ndarray, ids: np.ndarray, act: int = 0,
-              expert_map: Optional[List[int]] = None, ids64: bool = False) -> torch.Tensor:
+              expert_map: Optional[List[int]] = None, ids64: bool = False,
+              path: int = -1) -> torch.Tensor:
     """libmoe355 fused_experts on cuda:0 tensors; returns the device output."""
     dev = torch.device("cuda:0")
     xd = x.to(dev).contiguous()
@@ -51,7 +52,7 @@ def gpu_fused(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch.Te
     tw = torch.from_numpy(np.ascontiguousarray(topk_w, dtype=np.float32)).to(dev)
     I = w1[0].shape[0] // 2
     out = run_experts(xd, [w.data_ptr() for w in w1d], [w.data_ptr() for w in w2d], I, tw, idt,
-                      act, expert_map=expert_map)
+                      act, expert_map=expert_map, path=path)
     torch.cuda.synchronize()
     return out
 

@@ -30,13 +30,14 @@ def test_version_and_constants():
 
 @pytest.mark.parametrize("T,H,I,E,K,dtype,path", [
     (4096, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
-    (256, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
+    (256, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_MEDIUM),
     (16, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_SKINNY),
     (1, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_SKINNY),
     (2048, 4096, 6400, 16, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
     (8, 2048, 1408, 64, 6, _capi.BF16, _capi.PATH_MFMA_SKINNY),
     (4096, 2048, 1408, 64, 6, _capi.BF16, _capi.PATH_MFMA_TILED),
     (512, 1024, 2816, 8, 2, _capi.F32, _capi.PATH_SIMT),
+    (256, 1024, 2816, 8, 2, _capi.F16, _capi.PATH_MFMA_MEDIUM),
     (512, 1024, 2816, 8, 2, _capi.F16, _capi.PATH_MFMA_TILED),
 ])
 def test_plan_paths_and_layout(T, H, I, E, K, dtype, path):
@@ -53,12 +54,13 @@ def test_plan_paths_and_layout(T, H, I, E, K, dtype, path):
         assert (I // 128) % p.down_splits == 0
 
 
-@pytest.mark.parametrize("T,K,E,tile", [(4096, 2, 8, 256), (16, 2, 8, 16), (8, 6, 64, 16),
-                                        (333, 3, 7, 64)])
-def test_tile_map_capacity_bounds_every_routing(T, K, E, tile):
-    dtype = _capi.F32 if tile == 64 else _capi.BF16
+@pytest.mark.parametrize("T,K,E,tile,path", [(4096, 2, 8, 256, -1), (16, 2, 8, 16, -1),
+                                             (8, 6, 64, 16, -1), (333, 3, 7, 64, -1),
+                                             (256, 2, 8, 64, -1), (777, 2, 5, 64, 3)])
+def test_tile_map_capacity_bounds_every_routing(T, K, E, tile, path):
+    dtype = _capi.F32 if (tile == 64 and path < 0 and T == 333) else _capi.BF16
     H, I = (256, 256) if tile != 16 else (256, 128)
-    p = _capi.make_plan(T, H, I, E, K, dtype)
+    p = _capi.make_plan(T, H, I, E, K, dtype, path)
     assert p.tile_rows == tile
     rng = np.random.default_rng(0)
     R = T * K
@@ -113,6 +115,28 @@ def test_zero_tokens_is_a_no_op():
                                   None, None) == 0
     assert lib.moe355_fused_experts(None, None, None, None, None, 0, None, 0, 0, 256, 256, 8, 2,
                                     _capi.BF16, 0, None, 0, None, 0, None) == 0
+
+
+@pytest.mark.parametrize("path,tile", [(_capi.PATH_MFMA_TILED, 256), (_capi.PATH_MFMA_MEDIUM, 64),
+                                       (_capi.PATH_MFMA_SKINNY, 16), (_capi.PATH_SIMT, 64)])
+def test_forced_path_plans(path, tile):
+    p = _capi.make_plan(300, 512, 384, 8, 2, _capi.BF16, path)
+    assert p.path == path and p.tile_rows == tile
+    assert p.max_tiles >= -(-600 // tile)
+    if path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_MEDIUM):
+        assert (384 // 32) % p.down_splits == 0
+
+
+def test_forced_path_rejects_shapes_it_cannot_run():
+    lib = _capi.lib()
+    plan = _capi.Plan()
+    # fp32 has no MFMA family; H=384 is not a multiple of the 256-row weight tile
+    assert lib.moe355_make_plan_path(4, 256, 256, 8, 2, _capi.F32, _capi.PATH_MFMA_MEDIUM,
+                                     ctypes.byref(plan)) == -2
+    assert lib.moe355_make_plan_path(4, 384, 256, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED,
+                                     ctypes.byref(plan)) == -2
+    assert lib.moe355_make_plan_path(4, 256, 256, 8, 2, _capi.BF16, 7, ctypes.byref(plan)) == -1
+    assert "unknown path" in lib.moe355_last_error().decode()
 
 
 def test_activation_codes():

@@ -6,9 +6,10 @@ Reference: fused_experts (reframework/moe/fused.py:49-87). Bars:
   * bf16/f16 layers: <= 2e-2 against the fp64 oracle, and <= 4e-3 against
     the oracle that rounds the intermediate to the storage type like the
     kernels do (a tighter check of the GEMMs themselves).
-Every kernel family (tiled MFMA, skinny MFMA with split-K, fp32 SIMT) is
-driven, with ragged and empty expert groups, tile-boundary group sizes,
-dropped slots and int64 ids.
+Every kernel family (256- and 64-token-tile MFMA, skinny MFMA with split-K,
+fp32 SIMT) is driven, with ragged and empty expert groups, tile-boundary group
+sizes, dropped slots and int64 ids; each MFMA family is also forced onto
+shapes the automatic choice would give another one.
 """
 
 from __future__ import annotations
@@ -80,9 +81,12 @@ CASES = [
     ("decode_t16", 16, 2, 8, 1024, 2048, "bf16", _capi.PATH_MFMA_SKINNY),
     ("decode_f16", 8, 2, 8, 512, 512, "f16", _capi.PATH_MFMA_SKINNY),
     ("finegrained_t8", 8, 6, 64, 256, 128, "bf16", _capi.PATH_MFMA_SKINNY),
+    ("medium_ragged", 350, 2, 8, 512, 384, "bf16", _capi.PATH_MFMA_MEDIUM),
+    ("medium_f16", 150, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_MEDIUM),
+    ("medium_e16", 600, 2, 16, 512, 256, "bf16", _capi.PATH_MFMA_MEDIUM),
     ("prefill_ragged", 700, 2, 8, 512, 384, "bf16", _capi.PATH_MFMA_TILED),
-    ("prefill_f16", 300, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_TILED),
-    ("prefill_e16", 1024, 2, 16, 512, 256, "bf16", _capi.PATH_MFMA_TILED),
+    ("prefill_tiled", 1200, 2, 4, 512, 384, "bf16", _capi.PATH_MFMA_TILED),
+    ("prefill_f16", 1000, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_TILED),
     ("fp32_tiny", 96, 2, 8, 256, 352, "f32", _capi.PATH_SIMT),
     ("fp32_decode", 3, 2, 8, 128, 96, "f32", _capi.PATH_SIMT),
     ("bf16_unaligned", 40, 2, 4, 136, 200, "bf16", _capi.PATH_SIMT),
@@ -125,10 +129,26 @@ def test_gelu_activations(act, T, dev):
     _check(gpu_fused(x, w1, w2, w, ids, act=act), x, w1, w2, w, ids, act=act)
 
 
-@pytest.mark.parametrize("m", [255, 256, 257, 512, 513])
-def test_tile_boundary_group_sizes(m, dev):
+@pytest.mark.parametrize("T,K,E,H,I,seed", [(700, 2, 8, 512, 384, 1), (333, 6, 18, 512, 256, 2),
+                                            (1, 2, 8, 256, 256, 3), (2048, 2, 16, 512, 512, 4),
+                                            (64, 1, 1, 256, 256, 5)])
+@pytest.mark.parametrize("path", [_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_MEDIUM,
+                                  _capi.PATH_MFMA_SKINNY])
+def test_every_mfma_family_on_every_shape(path, T, K, E, H, I, seed, dev):
+    banner(f"forced path={path} T={T} K={K} E={E} H={H} I={I}")
+    w1, w2 = make_bank(E, H, I, torch.bfloat16, seed=seed)
+    x = (torch.randn(T, H, generator=torch.Generator().manual_seed(seed))).to(torch.bfloat16)
+    ids = skewed_ids(T, K, E, seed=seed, skew=1.1)
+    w = np.random.default_rng(seed).random((T, K)).astype(np.float32)
+    out = gpu_fused(x, w1, w2, w, ids, path=path)
+    _check(out, x, w1, w2, w, ids)
+
+
+@pytest.mark.parametrize("path", [-1, _capi.PATH_MFMA_TILED])
+@pytest.mark.parametrize("m", [63, 64, 65, 255, 256, 257, 512, 513])
+def test_tile_boundary_group_sizes(m, path, dev):
     # all m tokens to expert 0 (K=1) plus one token on expert 3
-    banner(f"tile boundary m={m}")
+    banner(f"tile boundary m={m} path={path}")
     E, H, I = 4, 256, 256
     T = m + 1
     ids = np.zeros((T, 1), np.int64)
@@ -136,7 +156,7 @@ def test_tile_boundary_group_sizes(m, dev):
     w1, w2 = make_bank(E, H, I, torch.bfloat16, seed=m)
     x = torch.randn(T, H).to(torch.bfloat16)
     w = np.ones((T, 1), np.float32)
-    _check(gpu_fused(x, w1, w2, w, ids), x, w1, w2, w, ids)
+    _check(gpu_fused(x, w1, w2, w, ids, path=path), x, w1, w2, w, ids)
 
 
 def test_dropped_slots_and_expert_map(dev):
