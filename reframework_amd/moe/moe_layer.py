@@ -170,12 +170,19 @@ class FusedMoE(BaseOP):
         return moe
 
     # ----------------------------------------------------------- offload setup
-    def build_offload_cache(self, device: torch.device, lru_capacity: int) -> ExpertOffloadCache:
+    def build_offload_cache(self, device: torch.device, lru_capacity: int,
+                            source=None) -> ExpertOffloadCache:
         """Stage this layer's experts into a pinned-host cache on ``device``
-        and drop the per-expert parameters."""
+        and drop the per-expert parameters. ``source(e) -> (gate [I,H], up
+        [I,H], down [H,I])``, when given, supplies the experts instead of the
+        parameters (e.g. straight from a checkpoint)."""
         self._cache = ExpertOffloadCache(device=device, lru_capacity=lru_capacity, dtype=self.dtype)
-        self._cache.load([{"w1": self.experts_w1[e], "w2": self.experts_w2[e]}
-                          for e in range(self.num_experts)])
+        if source is None:
+            self._cache.load([{"w1": self.experts_w1[e], "w2": self.experts_w2[e]}
+                              for e in range(self.num_experts)])
+        else:
+            self._cache.load_from(self.num_experts, self.hidden_size, self.intermediate_size,
+                                  source)
         self.experts_w1 = torch.nn.ParameterList()
         self.experts_w2 = torch.nn.ParameterList()
         if torch.cuda.is_available():

@@ -218,7 +218,36 @@ class ExpertOffloadCache:
         """
         w1s = [e["w1"].detach().to(dtype=self.dtype).contiguous() for e in experts]
         w2s = [e["w2"].detach().to(dtype=self.dtype).contiguous() for e in experts]
-        total = sum(w.numel() for w in w1s) + sum(w.numel() for w in w2s)
+        buf = self._alloc_pool([(tuple(a.shape), tuple(b.shape)) for a, b in zip(w1s, w2s)])
+        for (v1, v2), w1, w2 in zip(self._host, w1s, w2s):
+            v1.copy_(w1)
+            v2.copy_(w2)
+        del w1s, w2s, buf
+        self._loaded()
+
+    def load_from(self, num_experts: int, hidden: int, inter: int, fetch) -> None:
+        """Stage experts one at a time from ``fetch(e) -> (gate [I,H], up
+        [I,H], down [H,I])`` (host tensors of any float dtype, e.g. lazily read
+        checkpoint slices) straight into the host pool, without first
+        building per-expert tensors."""
+        self._alloc_pool([((2 * inter, hidden), (hidden, inter))] * num_experts)
+        for e, (v1, v2) in enumerate(self._host):
+            g, u, d = fetch(e)
+            if tuple(g.shape) != (inter, hidden) or tuple(u.shape) != (inter, hidden) or \
+                    tuple(d.shape) != (hidden, inter):
+                raise ValueError(f"expert {e}: shapes {tuple(g.shape)}, {tuple(u.shape)}, "
+                                 f"{tuple(d.shape)} do not match hidden={hidden} inter={inter}")
+            v1[:inter].copy_(g)
+            v1[inter:].copy_(u)
+            v2.copy_(d)
+        self._loaded()
+
+    def _alloc_pool(self, shapes) -> torch.Tensor:
+        """One host buffer holding every expert's w1 then w2; pinned
+        (hipHostMalloc through torch) when a GPU is present, else pageable."""
+        total = 0
+        for s1, s2 in shapes:
+            total += s1[0] * s1[1] + s2[0] * s2[1]
         try:
             buf = torch.empty(total, dtype=self.dtype, pin_memory=True)
             self._pinned = True
@@ -228,16 +257,16 @@ class ExpertOffloadCache:
         self._host_buf = buf
         self._host, self._host_off = [], []
         off = 0
-        for w1, w2 in zip(w1s, w2s):
+        for s1, s2 in shapes:
             self._host_off.append(off)
-            v1 = buf[off:off + w1.numel()].view_as(w1)
-            v1.copy_(w1)
-            off += w1.numel()
-            v2 = buf[off:off + w2.numel()].view_as(w2)
-            v2.copy_(w2)
-            off += w2.numel()
+            n1, n2 = s1[0] * s1[1], s2[0] * s2[1]
+            v1 = buf[off:off + n1].view(s1)
+            v2 = buf[off + n1:off + n1 + n2].view(s2)
+            off += n1 + n2
             self._host.append((v1, v2))
-        del w1s, w2s
+        return buf
+
+    def _loaded(self) -> None:
         if self._host:
             self._n1 = self._host[0][0].numel()
             self._n2 = self._host[0][1].numel()

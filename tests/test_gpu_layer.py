@@ -276,3 +276,40 @@ def test_shared_experts_with_streaming_offload(dev, monkeypatch):
     for g in (got, got_pack):
         err = (g - want).abs().max().item() / want.abs().max().item()
         assert err <= 1e-2
+
+
+def test_checkpoint_loaded_layer_matches_resident_and_offload(dev, tmp_path, monkeypatch):
+    """Mixtral-named safetensors -> FusedMoE (resident) and -> pinned pool
+    (offload, streamed per expert); both forwards agree with the oracle."""
+    from safetensors.torch import save_file
+
+    from reframework_amd.checkpoint import SafetensorsIndex, load_moe_layer, load_moe_layer_offload
+
+    banner("checkpoint adapter on the GPU")
+    E, K, H, I, T = 8, 2, 512, 256, 32
+    layer = synth.make_layer(synth.MoEShape("t", H, E, K, I), torch.bfloat16, seed=7)
+    p = "model.layers.5.block_sparse_moe"
+    sd = {f"{p}.gate.weight": layer["gate"]}
+    for e in range(E):
+        sd[f"{p}.experts.{e}.w1.weight"] = layer["w1"][e][:I].contiguous()
+        sd[f"{p}.experts.{e}.w3.weight"] = layer["w1"][e][I:].contiguous()
+        sd[f"{p}.experts.{e}.w2.weight"] = layer["w2"][e]
+    save_file(sd, str(tmp_path / "model.safetensors"))
+    idx = SafetensorsIndex(tmp_path)
+    res = FusedMoE(E, K, H, I, dtype=torch.bfloat16)
+    assert not load_moe_layer(idx, res, "model.layers.5.mlp").missing
+    res = res.to(dev)
+    off = FusedMoE(E, K, H, I, dtype=torch.bfloat16)
+    off.gate.data = off.gate.data.to(dev)
+    cache, rep = load_moe_layer_offload(idx, off, "model.layers.5.mlp", dev, lru_capacity=8)
+    assert not rep.missing and cache._pinned
+    off.gate.data = off.gate.data.to(dev)
+    x = synth.make_tokens(T, H, torch.bfloat16, seed=3).to(dev)
+    monkeypatch.setenv("RE_CHUNK_SIZE", "4")
+    a, b = res(x), off(x)
+    rw, rids = res.route(x)
+    torch.cuda.synchronize()
+    ref = oracle.fused_experts(x.cpu(), layer["w1"], layer["w2"], rw.cpu().numpy(),
+                               rids.cpu().numpy())
+    assert oracle.max_rel(a.float().cpu().numpy(), ref) <= 2e-2
+    assert oracle.max_rel(b.float().cpu().numpy(), ref) <= 2e-2
