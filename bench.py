@@ -271,15 +271,17 @@ def config_finegrained(dev, steps, warmup, tokens=(8, 4096)):
 
 
 def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
-    """Decode through per-layer expert offload caches (the reference's
-    semantics: lru_capacity 2 per layer, RE_MAX_PACK=2 truncation): Mixtral-
-    shape layers whose experts live in one pinned host pool per layer;
-    routing is the synthetic trace (p=0.7 repeat, Zipf(1.2)); misses stream
-    host->HBM on the cache's copy stream."""
+    """Decode through expert offload: Mixtral-shape layers whose experts live
+    in one pinned host pool per layer, synthetic routing (p=0.7 repeat,
+    Zipf(1.2)); misses stream host->HBM on the caches' copy streams. Forwards:
+    the reference's default truncation to RE_MAX_PACK=2 experts, and the exact
+    streaming forward (every routed expert). Residency, same HBM budget of 2
+    experts per layer: (i) the reference's per-layer LRU of 2, (ii) one LRU
+    over (layer, expert) shared by all layers."""
     import torch
 
     from reframework_amd import _capi, synth
-    from reframework_amd.moe import FusedMoE
+    from reframework_amd.moe import ExpertPool, FusedMoE
 
     h, e, k, i = 4096, 8, 2, 14336
     g = torch.Generator(device=dev).manual_seed(0)
@@ -289,8 +291,7 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
         with torch.no_grad():
             for prm in moe.parameters():
                 prm.copy_(torch.randn(prm.shape, generator=g, device=dev) * 0.02)
-        cache = moe.build_offload_cache(dev, lru_capacity=2)
-        cache.log_copies(True)
+        moe.build_offload_cache(dev, lru_capacity=2)
         layers.append(moe)
     torch.cuda.synchronize()
     # peak pinned H2D on this host: one 1 GiB copy through the same entry point
@@ -311,39 +312,51 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
     ids_d = torch.from_numpy(ids_all).to(dev)
     w_d = torch.from_numpy(w_all).to(dev)
     x = (torch.randn(T, h, generator=g, device=dev) * 0.5).to(torch.bfloat16)
-    act = 0
 
-    def step(st):
-        y = x
-        for li, moe in enumerate(layers):
-            y = moe._forward_offload(T, y, w_d[st, li], ids_d[st, li], act)
-        return y
+    def run_mode(pool, exact):
+        def fwd(moe, y, st, li):
+            if exact:  # every routed expert (the streaming forward with one chunk)
+                return moe._forward_streaming(y, w_d[st, li], ids_d[st, li], 0)
+            return moe._forward_offload(T, y, w_d[st, li], ids_d[st, li], 0)
 
-    for st in range(warmup_steps):
-        step(st)
-    torch.cuda.synchronize()
-    for moe in layers:
-        moe._cache.stats.reset()
-        moe._cache.log_copies(True)
-    t0 = time.perf_counter()
-    for st in range(warmup_steps, warmup_steps + steps):
-        step(st)
-    torch.cuda.synchronize()
-    sec = time.perf_counter() - t0
-    hits = sum(m._cache.stats.hits for m in layers)
-    misses = sum(m._cache.stats.misses for m in layers)
-    nbytes, copy_ms = 0, 0.0
-    for m in layers:
-        b_, ms_ = m._cache.copy_summary()
-        nbytes += b_
-        copy_ms += ms_
-    res = {"workload": "offload decode, mixtral-shape layers, per-layer lru 2, RE_MAX_PACK 2",
-           "layers": n_layers, "tokens": T, "steps": steps,
-           "tokens_per_s": round(T * steps / sec, 2), "ms_per_step": round(sec * 1000.0 / steps, 3),
-           "hit_rate": round(hits / max(1, hits + misses), 4), "hits": hits, "misses": misses,
-           "h2d_gb_s": round(nbytes / (copy_ms / 1000.0) / 1e9, 2) if copy_ms > 0 else None,
-           "h2d_bytes": nbytes, "peak_pinned_h2d_gb_s": round(peak_h2d, 2),
-           "copy_time_frac": round(copy_ms / 1000.0 / sec, 4)}
+        for moe in layers:
+            moe._cache.use_pool(pool)
+            moe._cache.log_copies(False)
+        for st in range(warmup_steps):
+            y = x
+            for li, moe in enumerate(layers):
+                y = fwd(moe, y, st, li)
+        torch.cuda.synchronize()
+        for moe in layers:
+            moe._cache.stats.reset()
+            moe._cache.log_copies(True)
+        t0 = time.perf_counter()
+        for st in range(warmup_steps, warmup_steps + steps):
+            y = x
+            for li, moe in enumerate(layers):
+                y = fwd(moe, y, st, li)
+        torch.cuda.synchronize()
+        sec = time.perf_counter() - t0
+        hits = sum(m._cache.stats.hits for m in layers)
+        misses = sum(m._cache.stats.misses for m in layers)
+        nbytes, copy_ms = 0, 0.0
+        for m in layers:
+            b_, ms_ = m._cache.copy_summary()
+            nbytes += b_
+            copy_ms += ms_
+        slots = pool.n_slots if pool is not None else sum(m._cache._n_slots for m in layers)
+        return {"tokens_per_s": round(T * steps / sec, 2), "ms_per_step": round(sec * 1000.0 / steps, 3),
+                "hbm_expert_slots": slots,
+                "hit_rate": round(hits / max(1, hits + misses), 4), "hits": hits, "misses": misses,
+                "h2d_gb_s": round(nbytes / (copy_ms / 1000.0) / 1e9, 2) if copy_ms > 0 else None,
+                "h2d_bytes": nbytes, "copy_time_frac": round(copy_ms / 1000.0 / sec, 4)}
+
+    res = {"workload": "offload decode, mixtral-shape layers, 2 HBM experts per layer",
+           "layers": n_layers, "tokens": T, "steps": steps, "peak_pinned_h2d_gb_s": round(peak_h2d, 2)}
+    for exact in (False, True):
+        tag = "exact" if exact else "max_pack_2"
+        res[f"{tag}_per_layer_lru"] = run_mode(None, exact)
+        res[f"{tag}_shared_pool"] = run_mode(ExpertPool(capacity=2 * n_layers), exact)
     del layers
     torch.cuda.empty_cache()
     return res

@@ -6,7 +6,8 @@ __init__.py:8-18).
 
 from reframework_amd.moe.fused import fused_experts, torch_fused_topk
 from reframework_amd.moe.moe_layer import CpuShuttle, FusedMoE
-from reframework_amd.moe.offload_cache import ExpertOffloadCache, OffloadStats, Prediction
+from reframework_amd.moe.offload_cache import (ExpertOffloadCache, ExpertPool, OffloadStats,
+                                               Prediction)
 
 __all__ = [
     "torch_fused_topk",
@@ -14,6 +15,7 @@ __all__ = [
     "FusedMoE",
     "CpuShuttle",
     "ExpertOffloadCache",
+    "ExpertPool",
     "OffloadStats",
     "Prediction",
 ]

@@ -171,12 +171,15 @@ class FusedMoE(BaseOP):
 
     # ----------------------------------------------------------- offload setup
     def build_offload_cache(self, device: torch.device, lru_capacity: int,
-                            source=None) -> ExpertOffloadCache:
+                            source=None, pool=None) -> ExpertOffloadCache:
         """Stage this layer's experts into a pinned-host cache on ``device``
         and drop the per-expert parameters. ``source(e) -> (gate [I,H], up
         [I,H], down [H,I])``, when given, supplies the experts instead of the
-        parameters (e.g. straight from a checkpoint)."""
-        self._cache = ExpertOffloadCache(device=device, lru_capacity=lru_capacity, dtype=self.dtype)
+        parameters (e.g. straight from a checkpoint). ``pool`` (an
+        ExpertPool) shares one HBM slot pool and LRU with other layers
+        instead of a per-layer window of ``lru_capacity`` experts."""
+        self._cache = ExpertOffloadCache(device=device, lru_capacity=lru_capacity, dtype=self.dtype,
+                                         pool=pool)
         if source is None:
             self._cache.load([{"w1": self.experts_w1[e], "w2": self.experts_w2[e]}
                               for e in range(self.num_experts)])

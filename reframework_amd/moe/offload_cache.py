@@ -164,6 +164,57 @@ class _Slot:
         self.refs = 0
 
 
+class ExpertPool:
+    """One HBM slot pool and one LRU shared by the offload caches of several
+    layers (no counterpart in the reference, whose caches are per layer).
+
+    Recency is global over (layer cache, expert), as in litemoe's global LRU
+    (litemoe/src/litemoe/cache/lru.py:66-102): a hit moves the entry to the
+    back, a miss is appended, and the oldest entries are evicted while the
+    pool is over ``capacity``. Unlike that cache, the experts of the request
+    being served are never evicted by it (their slots are about to be read),
+    so a request larger than the pool overflows it, as the per-layer cache
+    does. Freed slots go to a free list shared by all member caches (experts
+    of one model have one size).
+    """
+
+    def __init__(self, capacity: int) -> None:
+        self.capacity = int(capacity)
+        self._order: "OrderedDict[Tuple[int, int], ExpertOffloadCache]" = OrderedDict()
+        self._free: List[_Slot] = []
+        self.n_slots = 0
+
+    def __len__(self) -> int:
+        return len(self._order)
+
+    def touch(self, cache: "ExpertOffloadCache", idx: int) -> None:
+        key = (id(cache), int(idx))
+        self._order[key] = cache
+        self._order.move_to_end(key)
+
+    def forget(self, cache: "ExpertOffloadCache", idx: int) -> None:
+        self._order.pop((id(cache), int(idx)), None)
+
+    def evict(self, cache: "ExpertOffloadCache", hard: Sequence[int]) -> None:
+        """Evict oldest-first down to capacity, sparing ``cache``'s ``hard``."""
+        spare = {(id(cache), int(i)) for i in hard}
+        while len(self._order) > self.capacity:
+            victim = next((k for k in self._order if k not in spare), None)
+            if victim is None:
+                return
+            owner = self._order.pop(victim)
+            owner._drop(victim[1])
+
+    def acquire(self, make) -> _Slot:
+        if self._free:
+            return self._free.pop()
+        self.n_slots += 1
+        return make()
+
+    def release(self, slot: _Slot) -> None:
+        self._free.append(slot)
+
+
 class ExpertOffloadCache:
     """Pinned-host expert pool + an HBM LRU window of expert slots.
 
@@ -174,9 +225,13 @@ class ExpertOffloadCache:
     dtype: storage dtype of the experts.
     """
 
-    def __init__(self, device, lru_capacity: int, dtype: torch.dtype = torch.float16) -> None:
+    def __init__(self, device, lru_capacity: int, dtype: torch.dtype = torch.float16,
+                 pool: Optional[ExpertPool] = None) -> None:
         self.device = torch.device(device)
         self.lru_capacity = int(lru_capacity)
+        # With a shared pool, residency and eviction are global across the
+        # member caches and lru_capacity is not used.
+        self._pool = pool
         self.dtype = dtype
         self._host: List[Tuple[torch.Tensor, torch.Tensor]] = []
         self._host_buf: Optional[torch.Tensor] = None
@@ -359,6 +414,14 @@ class ExpertOffloadCache:
             logger.warning("host->HBM bandwidth measure failed: %s", exc)
             return None
 
+    def use_pool(self, pool: Optional["ExpertPool"]) -> None:
+        """Switch between a per-layer LRU window (None) and a shared pool;
+        the resident set starts empty."""
+        self.reset_lru()
+        self._free_slots = []
+        self._n_slots = 0
+        self._pool = pool
+
     def log_copies(self, on: bool = True) -> None:
         """Time every miss copy with HIP events on the copy stream (off by
         default; costs two events per miss)."""
@@ -374,6 +437,9 @@ class ExpertOffloadCache:
                 sum(a.elapsed_time(b) for a, b, _ in self._copy_log))
 
     def reset_lru(self) -> None:
+        if self._pool is not None:
+            for idx in list(self._lru):
+                self._pool.forget(self, idx)
         self._release_all()
         self._lru = OrderedDict()
         self._next_reserve = frozenset()
@@ -394,7 +460,12 @@ class ExpertOffloadCache:
             elif self._substitute(idx) is None:
                 self._fill(idx)
             self._lru.move_to_end(idx)
-        self._evict(uniq, self._next_reserve - set(uniq))
+            if self._pool is not None:
+                self._pool.touch(self, idx)
+        if self._pool is not None:
+            self._pool.evict(self, uniq)
+        else:
+            self._evict(uniq, self._next_reserve - set(uniq))
         return uniq
 
     def prefetch(self, indices: Sequence[int]) -> Tuple[torch.Tensor, torch.Tensor, Dict[int, int]]:
@@ -436,7 +507,12 @@ class ExpertOffloadCache:
         for i in uniq:
             if i not in self._lru:
                 self._fill(i)
-        self._evict(uniq, self._next_reserve - set(uniq))
+            if self._pool is not None:
+                self._pool.touch(self, i)
+        if self._pool is not None:
+            self._pool.evict(self, uniq)
+        else:
+            self._evict(uniq, self._next_reserve - set(uniq))
 
     def reserve(
         self,
@@ -456,7 +532,7 @@ class ExpertOffloadCache:
         ``predicted`` are evicted, and loading stops once the LRU is over
         capacity with nothing stale left.
         """
-        if not predicted or self.lru_capacity <= 0:
+        if not predicted or (self._pool is None and self.lru_capacity <= 0):
             return 0
         protect = {int(i) for i in protect_current} | {int(i) for i in predicted}
         bw = bandwidth_gb_s if bandwidth_gb_s is not None else self._bw_gb_s
@@ -479,6 +555,12 @@ class ExpertOffloadCache:
             self._fill(idx)
             self.stats.predicts += 1
             loaded.append(idx)
+            if self._pool is not None:
+                self._pool.touch(self, idx)
+                self._pool.evict(self, protect)
+                if len(self._pool) > self._pool.capacity:
+                    break
+                continue
             self._evict(protect)
             if len(self._lru) > self.lru_capacity:
                 break
@@ -492,12 +574,25 @@ class ExpertOffloadCache:
         return self._copy_stream
 
     def _acquire_slot(self) -> _Slot:
+        w1r, w2r = self._host[0]
+
+        def make() -> _Slot:
+            buf = torch.empty(self._n1 + self._n2, dtype=self.dtype, device=self.device)
+            return _Slot(buf, buf[:self._n1].view(w1r.shape), buf[self._n1:].view(w2r.shape))
+
+        if self._pool is not None:
+            slot = self._pool.acquire(make)
+            if slot.buf.numel() < self._n1 + self._n2:  # freed by a layer with smaller experts
+                slot = make()
+                self._pool.n_slots += 1
+            # a slot from another layer's cache holds that layer's layout
+            slot.w1 = slot.buf[:self._n1].view(w1r.shape)
+            slot.w2 = slot.buf[self._n1:].view(w2r.shape)
+            return slot
         if self._free_slots:
             return self._free_slots.pop()
-        w1r, w2r = self._host[0]
-        buf = torch.empty(self._n1 + self._n2, dtype=self.dtype, device=self.device)
         self._n_slots += 1
-        return _Slot(buf, buf[:self._n1].view(w1r.shape), buf[self._n1:].view(w2r.shape))
+        return make()
 
     def _release(self, slot: _Slot) -> None:
         slot.refs -= 1
@@ -507,7 +602,10 @@ class ExpertOffloadCache:
         ev.record(torch.cuda.current_stream(self.device))
         slot.free_after = ev
         slot.ready = None
-        self._free_slots.append(slot)
+        if self._pool is not None:
+            self._pool.release(slot)
+        else:
+            self._free_slots.append(slot)
 
     def _release_all(self) -> None:
         for slot in set(self._slot_of.values()):
@@ -551,6 +649,15 @@ class ExpertOffloadCache:
             self._lru[idx] = (w1.to(device=self.device), w2.to(device=self.device))
         self.stats.transfers_bytes += nbytes
         self.stats.misses += 1
+
+    def _drop(self, idx: int) -> None:
+        """Evict ``idx`` on the shared pool's decision."""
+        if self._lru.pop(idx, None) is None:
+            return
+        slot = self._slot_of.pop(idx, None)
+        if slot is not None:
+            self._release(slot)
+        self.stats.evictions += 1
 
     def _evict(self, hard_protect: Sequence[int], soft_protect: Sequence[int] = ()) -> None:
         """Evict down to ``lru_capacity``: stale entries first, then soft ones,
@@ -619,4 +726,4 @@ class ExpertOffloadCache:
                 f"pred={s['predicts']} evict={s['evictions']} transfer={s['transfer_mb']:.1f}MB")
 
 
-__all__ = ["ExpertOffloadCache", "OffloadStats", "Prediction"]
+__all__ = ["ExpertOffloadCache", "ExpertPool", "OffloadStats", "Prediction"]

@@ -313,3 +313,36 @@ def test_checkpoint_loaded_layer_matches_resident_and_offload(dev, tmp_path, mon
                                rids.cpu().numpy())
     assert oracle.max_rel(a.float().cpu().numpy(), ref) <= 2e-2
     assert oracle.max_rel(b.float().cpu().numpy(), ref) <= 2e-2
+
+
+def test_shared_pool_across_layers_matches_resident(dev, monkeypatch):
+    """Three layers share a 3-slot HBM pool; every step of a chained decode
+    must equal the resident layers while slots move between layers."""
+    from reframework_amd.moe import ExpertPool
+
+    monkeypatch.delenv("RE_CHUNK_SIZE", raising=False)
+    monkeypatch.setenv("RE_MAX_PACK", "8")
+    banner("shared expert pool across layers")
+    E, K, H, I = 8, 2, 256, 256
+    pool = ExpertPool(capacity=3)
+    refs, layers = [], []
+    for li in range(3):
+        refs.append(_build(E, K, H, I, torch.bfloat16, seed=10 + li, gate_sigma=0.2).to(dev))
+        m = _build(E, K, H, I, torch.bfloat16, seed=10 + li, gate_sigma=0.2)
+        m.gate.data = m.gate.data.to(dev)
+        m.build_offload_cache(dev, lru_capacity=2, pool=pool)
+        layers.append(m)
+    outs, wants = [], []
+    for step in range(8):
+        x = synth.make_tokens(1, H, torch.bfloat16, seed=100 + step).to(dev)
+        y, z = x, x
+        for m, r in zip(layers, refs):
+            y = m(y)
+            z = r(z)
+        outs.append(y)
+        wants.append(z)
+    torch.cuda.synchronize()
+    for o, w in zip(outs, wants):
+        assert torch.allclose(o.float(), w.float(), rtol=0, atol=2e-3 * w.float().abs().max().item())
+    ev = sum(m._cache.stats.evictions for m in layers)
+    assert ev > 0 and pool.n_slots <= 3 + 2 and len(pool) <= 3 + 2
