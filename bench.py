@@ -39,7 +39,7 @@ def parse():
     ap.add_argument("--tokens", type=int, default=4096)
     ap.add_argument("--decode", type=str, default="1,16,256",
                     help="comma-separated token counts reported beside the headline ('' = none)")
-    ap.add_argument("--configs", type=str, default="phi35moe,finegrained,offload",
+    ap.add_argument("--configs", type=str, default="phi35moe,finegrained,offload,norm_router",
                     help="other workloads reported beside the headline ('' = none)")
     ap.add_argument("--offload-layers", type=int, default=4)
     ap.add_argument("--offload-steps", type=int, default=48)
@@ -362,6 +362,40 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
     return res
 
 
+def config_norm_router(dev, steps, warmup, tokens=(1, 16, 4096)):
+    """The decoder step before the MoE (residual add + RMSNorm + router, one
+    library call) on the Mixtral shape: HBM bound, 4*T*H*2 bytes of rows plus
+    the 64 KB gate."""
+    import torch
+
+    from reframework_amd import _capi, synth
+
+    h, e, k = 4096, 8, 2
+    g = torch.Generator(device=dev).manual_seed(0)
+    gate = (torch.randn(e, h, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    nw = (torch.rand(h, generator=g, device=dev) + 0.5).to(torch.bfloat16)
+    bias = synth.mixtral_router_bias(e).to(dev)
+    out = {}
+    for T in tokens:
+        x = torch.randn(T, h, generator=g, device=dev).to(torch.bfloat16)
+        r = torch.randn(T, h, generator=g, device=dev).to(torch.bfloat16)
+        nr, normed = torch.empty_like(x), torch.empty_like(x)
+        w = torch.empty(T, k, dtype=torch.float32, device=dev)
+        ids = torch.empty(T, k, dtype=torch.int32, device=dev)
+
+        def step():
+            _capi.add_rmsnorm_router_topk(x, r, nr, nw, None, 1e-5, gate, bias, k, True, True,
+                                          normed, w, ids)
+
+        ms = _time_forward(step, max(steps, 50), warmup)
+        alg = 4 * T * h * 2 + e * h * 2
+        out[str(T)] = {"us": round(ms * 1000.0, 2), "alg_bytes": alg,
+                       "hbm_gb_s": round(alg / (ms / 1000.0) / 1e9, 1),
+                       "hbm_frac": round(alg / (ms / 1000.0) / 1e9 / PEAK_HBM_GBS, 4)}
+    return {"workload": "residual add + RMSNorm + router top-2, hidden 4096, 8 experts",
+            "tokens": out}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -419,6 +453,8 @@ def main():
         configs["phi35moe"] = config_phi35moe(dev, max(args.steps // 2, 5), args.warmup)
     if "finegrained" in names:
         configs["finegrained"] = config_finegrained(dev, args.steps, args.warmup)
+    if "norm_router" in names:
+        configs["norm_router"] = config_norm_router(dev, args.steps, args.warmup)
     if "offload" in names:
         configs["offload_decode"] = config_offload_decode(dev, args.offload_layers,
                                                           args.offload_steps)

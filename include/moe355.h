@@ -103,6 +103,33 @@ int moe355_router_topk(const void* x, const void* gate, const float* bias, int T
                        float* logits_out, float* topk_w, int32_t* topk_ids, void* stream);
 
 /*
+ * residual_out = x + residual (rounded to `dtype`; residual_out may alias x or
+ * residual), then normed = residual_out / sqrt(mean(residual_out^2) + eps) *
+ * weight (+ bias), in fp32, rounded once. With residual == NULL: normed =
+ * rmsnorm(x) and residual_out is unused (x may alias normed_out). weight/bias
+ * are [H] in weight_dtype; bias may be NULL.
+ * Replaces RMSNorm._forward / forward_add_residual
+ * (reframework/layers/norm.py:27-53), the step before the MoE block at
+ * reframework/models/base.py:135.
+ */
+int moe355_add_rmsnorm(const void* x, const void* residual, void* residual_out,
+                       const void* weight, const void* bias, int weight_dtype, float eps, int T,
+                       int H, int dtype, void* normed_out, void* stream);
+
+/*
+ * moe355_add_rmsnorm followed by moe355_router_topk on the normed rows, in one
+ * call on one stream: post_attention_layernorm.forward_add_residual + route
+ * (reframework/models/base.py:135-136, moe/moe_layer.py:320-344).
+ */
+int moe355_add_rmsnorm_router_topk(const void* x, const void* residual, void* residual_out,
+                                   const void* norm_weight, const void* norm_bias,
+                                   int weight_dtype, float eps,
+                                   const void* gate, const float* router_bias, int T, int H, int E,
+                                   int K, int dtype, int renormalize, int round_logits,
+                                   void* normed_out, float* topk_w, int32_t* topk_ids,
+                                   void* stream);
+
+/*
  * softmax -> top-k -> renormalise on given fp32 logits.
  * Replaces torch_fused_topk (reframework/moe/fused.py:32-46). Selection is on
  * the logits (monotone with the softmax), ties -> lower expert id.

@@ -12,6 +12,7 @@
  *   oracle_topk           reframework/moe/fused.py:32-46 (+ moe_layer.py:326-342 entropy branch)
  *   oracle_permute        reframework/moe/fused.py:70-80, moe_layer.py:477-511 (remap/drop)
  *   oracle_fused_experts  reframework/moe/fused.py:49-87, reframework/layers/activation.py:15-59
+ *   oracle_add_rmsnorm    reframework/layers/norm.py:27-53 (RMSNorm._forward, forward_add_residual)
  *
  * Inputs are given in their storage type (fp32, or raw bf16/f16 bits) and are
  * widened exactly. Results are fp64 (outputs) or fp32 rounded once (weights).
@@ -288,6 +289,34 @@ int oracle_fused_experts(const void* x, int x_type, const void* const* w1, const
     free(inter);
   }
   return 0;
+}
+
+/* ---------------------------------------------------------------- rmsnorm */
+/* residual_out = storage(fp32(x) + fp32(residual)) when residual != NULL (the
+ * reference adds in the storage dtype: torch widens to fp32, adds, rounds
+ * once), else residual_out = x; normed = storage(r * 1/sqrt(mean(r^2) + eps)
+ * * w + b) with the scaling in double. w and b are doubles ([H]; b may be
+ * NULL). Tensors x/residual are in storage type `type`; outputs are doubles
+ * holding values representable in that type. */
+void oracle_add_rmsnorm(const void* x, const void* residual, int type, const double* w,
+                        const double* b, double eps, int T, int H, double* residual_out,
+                        double* normed) {
+  const int mode = type == ORACLE_F32 ? 3 : type;
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < T; ++t) {
+    double* r = residual_out + (size_t)t * H;
+    double ss = 0.0;
+    for (int h = 0; h < H; ++h) {
+      const size_t i = (size_t)t * H + h;
+      double v = load_elem(x, i, type);
+      if (residual) v = round_to((double)((float)v + (float)load_elem(residual, i, type)), mode);
+      r[h] = v;
+      ss += v * v;
+    }
+    const double inv = 1.0 / sqrt(ss / (double)H + eps);
+    for (int h = 0; h < H; ++h)
+      normed[(size_t)t * H + h] = round_to(r[h] * inv * w[h] + (b ? b[h] : 0.0), mode);
+  }
 }
 
 /* Round n doubles to `mode` (1 bf16, 2 f16, 3 f32) in place; exposes the

@@ -47,6 +47,8 @@ def lib() -> ctypes.CDLL:
         h.oracle_fused_experts.restype = I
         h.oracle_round.argtypes = [P, ctypes.c_size_t, I]
         h.oracle_round.restype = None
+        h.oracle_add_rmsnorm.argtypes = [P, P, I, P, P, ctypes.c_double, I, I, P, P]
+        h.oracle_add_rmsnorm.restype = None
         _lib = h
     return _lib
 
@@ -136,6 +138,26 @@ def fused_experts(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torc
                                None if tok is None else tok.ctypes.data,
                                0 if tok is None else len(tok), out.ctypes.data)
     return out
+
+
+def add_rmsnorm(x: torch.Tensor, residual: Optional[torch.Tensor], weight, bias, eps: float):
+    """(new residual, normed), both fp64 [T,H] holding storage-dtype values,
+    of reframework/layers/norm.py:27-53 (x and residual in one storage dtype;
+    weight and bias any float arrays of length H)."""
+    xt, tx = _raw(x)
+    T, H = xt.shape
+    rt = None
+    if residual is not None:
+        rt, tr = _raw(residual)
+        assert tr == tx
+    w = np.ascontiguousarray(_cpu(torch.as_tensor(weight)).double().numpy())
+    b = None if bias is None else np.ascontiguousarray(_cpu(torch.as_tensor(bias)).double().numpy())
+    r_out = np.empty((T, H), dtype=np.float64)
+    n_out = np.empty((T, H), dtype=np.float64)
+    lib().oracle_add_rmsnorm(xt.data_ptr(), None if rt is None else rt.data_ptr(), tx,
+                             w.ctypes.data, None if b is None else b.ctypes.data, float(eps), T, H,
+                             r_out.ctypes.data, n_out.ctypes.data)
+    return r_out, n_out
 
 
 def max_rel(out: np.ndarray, ref: np.ndarray) -> float:

@@ -207,6 +207,44 @@ int moe355_router_topk(const void* x, const void* gate, const float* bias, int T
   return check_hip(launch_router(a, dtype, as_stream(stream)), "router_topk launch");
 }
 
+int moe355_add_rmsnorm(const void* x, const void* residual, void* residual_out,
+                       const void* weight, const void* bias, int weight_dtype, float eps, int T,
+                       int H, int dtype, void* normed_out, void* stream) {
+  if (T < 0 || H <= 0) return fail(MOE355_EINVAL, "bad sizes T=%d H=%d", T, H);
+  if (!valid_dtype(dtype) || !valid_dtype(weight_dtype))
+    return fail(MOE355_EINVAL, "unknown dtype %d / weight dtype %d", dtype, weight_dtype);
+  const int vec = 16 / elem_size(dtype);
+  if (H % vec || H > norm_max_hidden(dtype))
+    return fail(MOE355_EUNSUPPORTED, "norm needs H %% %d == 0 and H <= %d", vec,
+                norm_max_hidden(dtype));
+  if (!(eps >= 0.0f)) return fail(MOE355_EINVAL, "eps must be >= 0");
+  if (T == 0) return MOE355_OK;
+  if (!x || !weight || !normed_out) return fail(MOE355_EINVAL, "NULL tensor argument");
+  if (residual && !residual_out) return fail(MOE355_EINVAL, "residual given without residual_out");
+  if (!aligned16(x) || !aligned16(normed_out) || (residual && !aligned16(residual)) ||
+      (residual && !aligned16(residual_out)))
+    return fail(MOE355_EINVAL, "x/residual/out not 16-byte aligned");
+  NormArgs a{};
+  a.x = x; a.residual = residual; a.residual_out = residual_out; a.weight = weight;
+  a.bias = bias; a.out = normed_out;
+  a.T = T; a.H = H; a.weight_dtype = weight_dtype; a.eps = eps;
+  return check_hip(launch_add_rmsnorm(a, dtype, as_stream(stream)), "add_rmsnorm launch");
+}
+
+int moe355_add_rmsnorm_router_topk(const void* x, const void* residual, void* residual_out,
+                                   const void* norm_weight, const void* norm_bias,
+                                   int weight_dtype, float eps,
+                                   const void* gate, const float* router_bias, int T, int H, int E,
+                                   int K, int dtype, int renormalize, int round_logits,
+                                   void* normed_out, float* topk_w, int32_t* topk_ids,
+                                   void* stream) {
+  int rc = moe355_add_rmsnorm(x, residual, residual_out, norm_weight, norm_bias, weight_dtype, eps,
+                              T, H, dtype, normed_out, stream);
+  if (rc) return rc;
+  return moe355_router_topk(normed_out, gate, router_bias, T, H, E, K, dtype, renormalize,
+                            round_logits, 0, nullptr, topk_w, topk_ids, stream);
+}
+
 int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renormalize,
                             float* topk_w, int32_t* topk_ids, void* stream) {
   if (T < 0) return fail(MOE355_EINVAL, "bad T=%d", T);

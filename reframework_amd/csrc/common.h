@@ -175,6 +175,17 @@ struct FfnArgs {
   const void* w[kMaxExperts];  // w1[e] ([2I,H]) or w2[e] ([H,I])
 };
 
+struct NormArgs {
+  const void* x;        // [T,H]
+  const void* residual; // [T,H] added to x, or nullptr for a plain norm of x
+  void* residual_out;   // [T,H] x + residual (may alias residual or x)
+  const void* weight;   // [H] (weight_dtype)
+  const void* bias;     // [H] (weight_dtype) or nullptr
+  void* out;            // [T,H] normed
+  int T, H, weight_dtype;
+  float eps;
+};
+
 struct CombineArgs {
   const float* y;            // [S,R,H]
   const float* topk_w;       // [T,K]
@@ -191,6 +202,8 @@ int device_cu_count();
 // ---------------------------------------------------------------- launchers
 // Each returns the hipError_t of the launch (hipSuccess when nothing to do).
 hipError_t launch_router(const RouterArgs& a, int dtype, hipStream_t s);
+hipError_t launch_add_rmsnorm(const NormArgs& a, int dtype, hipStream_t s);
+int norm_max_hidden(int dtype);
 hipError_t launch_topk_from_logits(const RouterArgs& a, hipStream_t s);
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
 hipError_t launch_gate_up_tiled(const FfnArgs& a, int dtype, hipStream_t s);

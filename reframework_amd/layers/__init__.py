@@ -1,7 +1,8 @@
-"""Layer primitives the MoE path needs: the parameter-owning base class and the
-gated-activation registry."""
+"""Layer primitives the MoE path needs: the parameter-owning base class, the
+gated-activation registry and the RMSNorm that precedes the MoE block."""
 
 from .activation import GATED_ACTIVATIONS, activation_code
 from .base import BaseOP
+from .norm import RMSNorm
 
-__all__ = ["BaseOP", "GATED_ACTIVATIONS", "activation_code"]
+__all__ = ["BaseOP", "GATED_ACTIVATIONS", "activation_code", "RMSNorm"]

@@ -357,6 +357,46 @@ class FusedMoE(BaseOP):
             out = out.to(x2.dtype)
         return out.reshape(x.shape[:1] + (self.hidden_size,)) if x.dim() > 1 else out
 
+    def forward_with_norm(self, x: torch.Tensor, residual: torch.Tensor,
+                          norm) -> Tuple[torch.Tensor, torch.Tensor]:
+        """``f, residual = norm.forward_add_residual(x, residual); f = self(f)``
+        (reframework/models/base.py:135-136) with the residual add, the
+        RMSNorm and the router in one library call; returns (output, new
+        residual). ``norm`` is an RMSNorm (its weight, optional bias and eps)."""
+        shape = x.shape
+        x2 = x.reshape(-1, self.hidden_size)
+        require_gpu(x2)
+        xd = x2.to(self.dtype).contiguous()
+        res = residual.reshape(-1, self.hidden_size).to(self.dtype).contiguous()
+        T = xd.shape[0]
+        normed = torch.empty_like(xd)
+        new_res = torch.empty_like(xd)
+        w = torch.empty((T, self.top_k), dtype=torch.float32, device=xd.device)
+        ids = torch.empty((T, self.top_k), dtype=torch.int32, device=xd.device)
+        gate = self.gate.detach()
+        if gate.device != xd.device:
+            gate = gate.to(xd.device)
+        nw, nb = norm._params(xd)
+        if self.entropy_adaptive_k:
+            # the entropy-adaptive router is not fused: norm, then the router
+            _capi.add_rmsnorm(xd, res, new_res, nw, nb, norm.eps, normed)
+            w, ids = self._route32(normed)
+        else:
+            _capi.add_rmsnorm_router_topk(xd, res, new_res, nw, nb, norm.eps,
+                                          gate.to(self.dtype).contiguous(), None, self.top_k,
+                                          self.renormalize, True, normed, w, ids)
+        act = activation_code(self.activation)
+        if self.uses_offload and env.get_chunk_size(0) > 0:
+            out = self._forward_streaming(normed, w, ids, act)
+        elif self.uses_offload:
+            out = self._forward_offload(T, normed, w, ids, act)
+        else:
+            w1p, w2p = self._resident_banks()
+            out = self._experts(normed, w, ids, act, w1p, w2p)
+        if out.dtype != x.dtype:
+            out = out.to(x.dtype)
+        return out.reshape(shape), new_res.reshape(shape).to(residual.dtype)
+
     def _forward_offload(self, M: int, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
                          act: int) -> torch.Tensor:
         cache = self._cache
