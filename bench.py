@@ -140,9 +140,11 @@ def measure(layer, T, steps, warmup):
     total_ev = sum(e[3].elapsed_time(e[4]) for e in ev) / steps
     ids = bufs[3].cpu().numpy()
     routed = sorted(set(int(v) for v in ids.reshape(-1)))
+    plan, ws = bufs[0], bufs[1]
+    tiles = int(ws[plan.off_tile_map:plan.off_tile_map + 4].cpu().view(torch.int32)[0])
     return {"ms": ms, "gate_up_ms": gate_up, "down_ms": down, "layer_ev_ms": total_ev,
-            "routed_experts": len(routed), "plan_path": bufs[0].path,
-            "down_splits": bufs[0].down_splits}
+            "routed_experts": len(routed), "plan_path": plan.path,
+            "down_splits": plan.down_splits, "token_tiles": tiles}
 
 
 def cpu_baseline(layer, T):

@@ -1,6 +1,7 @@
 // The extern "C" boundary of libmoe355.so: argument checks, the execution
 // plan, and dispatch to the kernel launchers. Declarations and their reference
 // counterparts are in include/moe355.h.
+#include <algorithm>
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
@@ -305,6 +306,11 @@ int moe355_gate_up(const moe355_plan* p, const void* x, const void* const* w1, i
   hipError_t err;
   if (p->path == MOE355_PATH_MFMA_TILED) {
     a.n_wtiles = p->I / 128;
+    // The y region is free until the down projection: it holds the partial
+    // tiles of the K-split tail items (256x256 fp32 each).
+    const size_t y_bytes = static_cast<size_t>(p->down_splits) * p->rows * p->H * 4;
+    a.part = at<float>(workspace, p->off_y);
+    a.part_units = static_cast<int>(std::min<size_t>(y_bytes / (256 * 256 * 4), 4096));
     err = launch_gate_up_tiled(a, p->dtype, as_stream(stream));
   } else if (p->path == MOE355_PATH_MFMA_MEDIUM) {
     a.n_wtiles = p->I / 128;

@@ -172,6 +172,9 @@ struct FfnArgs {
   int H, I, R;
   int max_tiles, n_wtiles, splits, k_per_split;
   int act;
+  float* part;             // tiled gate_up: tail-split partial tiles, part_units x 256 KB
+  int part_units;          // capacity of part in 256x256 fp32 tiles (0: no tail split)
+  int grid;                // workgroups of the tiled launch (the fix-up recomputes its split)
   const void* w[kMaxExperts];  // w1[e] ([2I,H]) or w2[e] ([H,I])
 };
 

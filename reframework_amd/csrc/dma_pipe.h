@@ -21,6 +21,7 @@ __device__ __forceinline__ uint32_t swz(int c, int r) {
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(4))) int32_t const_i32;
 
 // s_waitcnt that waits until at most n vector-memory operations are
 // outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
@@ -43,6 +44,15 @@ __device__ __forceinline__ void dma_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// v unchanged, but opaque to the optimiser: per-lane indices derived from it
+// are recomputed where they are used instead of being hoisted out of the
+// persistent loop and kept live (or spilled to scratch, whose reloads wait on
+// vmcnt and so drain the load pipeline) across the MFMA stream.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
 }
 
 // One 1 KB direct-to-LDS load per wave: lane i's 16 bytes land at dst + 16 i.
@@ -78,15 +88,57 @@ struct Tile {
 // rows from the permute's tile map.
 __device__ __forceinline__ Tile decode_tile(const FfnArgs& a, int L, int per_split, int n_t,
                                             int tile_rows) {
+  // L is wave-uniform; saying so keeps the tile-map reads on the scalar unit
+  // (vector loads here would be waited for with vmcnt and drain the
+  // direct-to-LDS pipeline at every item boundary).
+  // The tables are read through the constant address space (they do not
+  // change during the kernel), so the compiler may use scalar loads although
+  // the kernel stores to memory it cannot tell apart from them.
+  L = __builtin_amdgcn_readfirstlane(L);
+  const const_i32* tile_map = (const const_i32*)(a.tile_map);
+  const const_i32* offsets = (const const_i32*)(a.offsets);
   Tile t;
   t.split = L / per_split;
   const int rem = L - t.split * per_split;
   t.wtile = rem / n_t;
   const int tt = rem - t.wtile * n_t;
-  t.e = a.tile_map[2 + 2 * tt];
-  t.row0 = a.tile_map[3 + 2 * tt];
-  t.row_end = min(t.row0 + tile_rows, a.offsets[t.e + 1]);
+  t.e = tile_map[2 + 2 * tt];
+  t.row0 = tile_map[3 + 2 * tt];
+  t.row_end = min(t.row0 + tile_rows, offsets[t.e + 1]);
   return t;
+}
+
+// Tail split of a persistent grouped GEMM. With n_work items on G workgroups
+// the last n_work % G items (the tail) would run alone while the other CUs
+// idle for a whole item. Instead each tail item is cut along K into S parts
+// (S a power of two, S | nk, S * tail <= cap), one unit per idle workgroup,
+// whose fp32 partial tiles a fix-up pass sums. Items [0, n_full) run whole;
+// unit u < n_units is k-part u % S of item n_full + u / S. S minimises
+// 7 * nk / S + S * tail: a K-step of a 256x256 tile costs about seven times
+// what one unit's partial tile costs to write and read back through HBM (so a
+// short K or a wide tail keeps the item whole). cap = 0 disables the split.
+struct WorkSplit {
+  int n_full, n_units, S;
+};
+
+__device__ __forceinline__ WorkSplit work_split(int n_work, int G, int nk, int cap) {
+  WorkSplit w{n_work, 0, 1};
+  const int R = G > 0 ? n_work / G : 0, tail = n_work - R * G;
+  if (cap <= 0 || tail == 0) return w;
+  cap = min(cap, G);
+  int best = 7 * nk;
+  for (int s = 2; s <= 16 && s * tail <= cap && nk % s == 0; s *= 2) {
+    const int c = 7 * nk / s + s * tail;
+    if (c < best) {
+      best = c;
+      w.S = s;
+    }
+  }
+  if (w.S > 1) {
+    w.n_full = R * G;
+    w.n_units = tail * w.S;
+  }
+  return w;
 }
 
 }  // namespace pipe

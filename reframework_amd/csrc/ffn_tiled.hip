@@ -23,7 +23,9 @@
 // XOR-swizzled in 16-byte chunks (swz) so the operand reads are bank-conflict
 // free. The kernel is persistent (one workgroup per CU) and streams its K-steps
 // across tile boundaries, so each tile's pipeline fill overlaps the previous
-// tile's epilogue.
+// tile's epilogue. The gate_up items left for a last, mostly idle round are
+// split along K over the idle CUs (work_split); their fp32 partial tiles are
+// summed and activated by gate_up_tail_fixup.
 #include "dma_pipe.h"
 
 namespace moe355 {
@@ -39,6 +41,34 @@ constexpr int kStageBytes = 2 * kRegionBytes;         // weights + tokens
 constexpr int kStages = 5;
 constexpr int kLdsBytes = kStages * kStageBytes;      // 160 KB: the whole LDS
 constexpr int kLoadsPerWave = kStageBytes / 1024 / (kThreads / kWave);  // 8 x 1 KB
+// One tail-split unit's partial tile: 4 waves x 16 (i, j) MFMA blocks x 4 x 64
+// lanes of f32x4, stored in register order so every store is 1 KB contiguous.
+constexpr int kPartVecsPerWave = 4 * 4 * 4 * kWave;
+
+// A work item or a K-part of a split tail item: its tile, K-step range and
+// partial-tile slot (-1 for a whole item).
+struct Work {
+  Tile t;
+  int kb, ke, unit;
+};
+
+__device__ __forceinline__ Work decode_work(const FfnArgs& a, const WorkSplit& ws, int L,
+                                            int per_split, int n_t, int nk) {
+  Work w;
+  if (L < ws.n_full) {
+    w.t = decode_tile(a, L, per_split, n_t, kTileT);
+    w.kb = 0;
+    w.ke = nk;
+    w.unit = -1;
+  } else {
+    const int u = L - ws.n_full, len = nk / ws.S;
+    w.t = decode_tile(a, ws.n_full + u / ws.S, per_split, n_t, kTileT);
+    w.kb = (u % ws.S) * len;
+    w.ke = w.kb + len;
+    w.unit = u;
+  }
+  return w;
+}
 
 // Persistent: one workgroup per CU walks work items L = L0, L0 + G, ... (G =
 // grid size) of the (split, weight tile, token tile) space. Its K-steps form
@@ -59,14 +89,18 @@ void ffn_tiled_kernel(const FfnArgs a) {
   const int per_split = a.n_wtiles * n_t;
   const int n_work = a.splits * per_split;
   const int G = gridDim.x;
+  const int nk = a.k_per_split / kBK;
+  // Work sequence L0, L0 + G, ...: whole items below ws.n_full, then (gate_up
+  // only) at most one tail unit per workgroup.
+  const WorkSplit ws = work_split(n_work, G, nk, kGateUp ? a.part_units : 0);
+  const int n_seq = ws.n_full + ws.n_units;
   int Lc = xcd_remap(blockIdx.x, G);  // work item being multiplied
-  if (Lc >= n_work) return;
+  if (Lc >= n_seq) return;
 
   const int ld = kGateUp ? a.H : a.I;  // elements per weight row and per token row
   const uint32_t pitch = static_cast<uint32_t>(ld * 2);
-  const int nk = a.k_per_split / kBK;
 
-  auto decode = [&](int L) { return decode_tile(a, L, per_split, n_t, kTileT); };
+  auto decode = [&](int L) { return decode_work(a, ws, L, per_split, n_t, nk); };
 
   // Stage = 32 loads of 1 KB (16 rows x 64 B each). Waves 0-1 fill the weight
   // region, waves 2-3 the token region, 8 loads each: load q of wave w covers
@@ -74,63 +108,68 @@ void ffn_tiled_kernel(const FfnArgs a) {
   // 16 * (...) + i / 4, physical chunk i % 4, so it fetches that row's logical
   // chunk swz(i % 4, row) (the swizzle is an involution) from global memory.
   const bool wload = wave < 2;
-  auto region_row = [&](int q) { return ((wave & 1) * kLoadsPerWave + q) * 16 + (lane >> 2); };
+  auto region_row = [&](int q, int ln) { return ((wave & 1) * kLoadsPerWave + q) * 16 + (ln >> 2); };
 
   // gate_up token rows come through row_src; they are fetched one tile ahead.
   int grow[kLoadsPerWave];
   auto fetch_rows = [&](const Tile& t) {
+    const int ln = opaque(lane);
 #pragma unroll
     for (int q = 0; q < kLoadsPerWave; ++q)
-      grow[q] = a.row_src[min(t.row0 + region_row(q), t.row_end - 1)];
+      grow[q] = a.row_src[min(t.row0 + region_row(q, ln), t.row_end - 1)];
   };
 
-  // Load cursor: work item Ll, step lkt; source base and per-load offsets.
-  int Ll = Lc, lkt = 0;
+  // Load cursor: work item Ll, step lkt of [.., lke); source base and per-load
+  // offsets.
+  int Ll = Lc, lkt = 0, lke = 0;
   const char* lsrc;
   uint32_t lgoff[kLoadsPerWave];
-  auto setup_load = [&](const Tile& t) {
+  auto setup_load = [&](const Work& w) {
+    const Tile& t = w.t;
+    lkt = w.kb;
+    lke = w.ke;
+    const int ln = opaque(lane);
     const size_t kbeg = static_cast<size_t>(t.split) * a.k_per_split;
     if (wload) {
       lsrc = static_cast<const char*>(a.w[t.e]) + kbeg * 2;
 #pragma unroll
       for (int q = 0; q < kLoadsPerWave; ++q) {
-        const int r = region_row(q);
+        const int r = region_row(q, ln);
         const int wr = kGateUp ? (r < kTileW / 2 ? t.wtile * (kTileW / 2) + r
                                                  : a.I + t.wtile * (kTileW / 2) + (r - kTileW / 2))
                                : t.wtile * kTileW + r;
-        lgoff[q] = static_cast<uint32_t>(wr) * pitch + swz(lane & 3, r) * 16;
+        lgoff[q] = static_cast<uint32_t>(wr) * pitch + swz(ln & 3, r) * 16;
       }
     } else if (kGateUp) {
       lsrc = static_cast<const char*>(a.x) + kbeg * 2;
 #pragma unroll
       for (int q = 0; q < kLoadsPerWave; ++q)
-        lgoff[q] = static_cast<uint32_t>(grow[q]) * pitch + swz(lane & 3, region_row(q)) * 16;
+        lgoff[q] = static_cast<uint32_t>(grow[q]) * pitch + swz(ln & 3, region_row(q, ln)) * 16;
     } else {
       lsrc = static_cast<const char*>(a.x) + (static_cast<size_t>(t.row0) * ld + kbeg) * 2;
 #pragma unroll
       for (int q = 0; q < kLoadsPerWave; ++q) {
-        const int r = region_row(q);
+        const int r = region_row(q, ln);
         const int xr = min(t.row0 + r, t.row_end - 1) - t.row0;
-        lgoff[q] = static_cast<uint32_t>(xr) * pitch + swz(lane & 3, r) * 16;
+        lgoff[q] = static_cast<uint32_t>(xr) * pitch + swz(ln & 3, r) * 16;
       }
     }
   };
   auto prefetch_next_rows = [&]() {
-    if (kGateUp && !wload && Ll + G < n_work) fetch_rows(decode(Ll + G));
+    if (kGateUp && !wload && Ll + G < n_seq) fetch_rows(decode(Ll + G).t);
   };
   // Step to the next K-step of the load stream; past the last work item the
   // cursor stays on its final step, so the tail keeps issuing (harmless,
   // in-bounds) loads into buffers nobody reads and the vmcnt accounting of
   // the pipeline stays fixed.
   auto advance_load = [&]() {
-    if (++lkt < nk) return;
-    if (Ll + G < n_work) {
+    if (++lkt < lke) return;
+    if (Ll + G < n_seq) {
       Ll += G;
-      lkt = 0;
       setup_load(decode(Ll));
       prefetch_next_rows();
     } else {
-      lkt = nk - 1;
+      lkt = lke - 1;
     }
   };
   // Loads q0 .. q0+n-1 of the current load step into LDS buffer lb.
@@ -160,10 +199,21 @@ void ffn_tiled_kernel(const FfnArgs a) {
   for (int ks = 0; ks < kBK / 16; ++ks) coff[ks] = swz(ks * 2 + kh, lr) << 4;
 
   f32x16 acc[4][4];
+
+  // Accumulator element to a VGPR at the point of use. Read all at once at
+  // the loop exit, the 256 accumulators would need 256 VGPRs next to the
+  // AGPRs that hold them and spill.
+  auto acc_read = [](float x) {
+    float r;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(r) : "a"(x));
+    return r;
+  };
+  auto zero_acc = [&]() {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  };
 
   auto read_frags = [&](const uint8_t* st, int ks, u32x4* af, u32x4* bf) {
 #pragma unroll
@@ -184,9 +234,9 @@ void ffn_tiled_kernel(const FfnArgs a) {
   // operations issued in between (row_src prefetch, epilogue stores) only make
   // the waits stricter.
   {
-    const Tile t0 = decode(Ll);
-    if (kGateUp && !wload) fetch_rows(t0);
-    setup_load(t0);
+    const Work w0 = decode(Ll);
+    if (kGateUp && !wload) fetch_rows(w0.t);
+    setup_load(w0);
     prefetch_next_rows();
   }
 #pragma unroll
@@ -196,6 +246,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
   }
   dma_barrier<(kStages - 2) * kLoadsPerWave>();  // step 0 landed
 
+  zero_acc();
   u32x4 fa[2][4], fb[2][4];
   read_frags(lds, 0, fa[0], fb[0]);
   wait_lgkm0();
@@ -235,9 +286,10 @@ void ffn_tiled_kernel(const FfnArgs a) {
   };
 
   int cb = 0;  // LDS buffer of the step being multiplied
-  Tile ct = decode(Lc);
+  Work cw = decode(Lc);
   while (true) {
-    for (int kt = 0; kt < nk; ++kt) {
+    const Tile& ct = cw.t;
+    for (int kt = cw.kb; kt < cw.ke; ++kt) {
       const int nb_ = cb == kStages - 1 ? 0 : cb + 1;
       const int lb_ = cb == 0 ? kStages - 1 : cb - 1;  // (cb + kStages - 1) % kStages
       uint8_t* st = lds + cb * kStageBytes;
@@ -255,24 +307,45 @@ void ffn_tiled_kernel(const FfnArgs a) {
 
     // Epilogue. Lane (lr, kh) of block (i, j) holds, for q = 0..3, features
     // 8q + 4kh + 0..3 of the 32-row weight block and token lr of the token block.
-    if (kGateUp) {
+    const int eln = opaque(lane), elr = eln & 31, ekh = eln >> 5;
+    if (kGateUp && cw.unit >= 0) {
+      // K-part of a split tail item: raw fp32 accumulators to its partial slot.
+      f32x4* pp = reinterpret_cast<f32x4*>(a.part) +
+                  static_cast<size_t>(cw.unit * 4 + wave) * kPartVecsPerWave + eln;
+  #pragma unroll
+      for (int i = 0; i < 4; ++i)
+  #pragma unroll
+        for (int j = 0; j < 4; ++j)
+  #pragma unroll
+          for (int q = 0; q < 4; ++q)
+            pp[((i * 4 + j) * 4 + q) * kWave] =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                      acc[i][j][4 * q + 3]};
+      zero_acc();
+    } else if (kGateUp) {
       T* inter = static_cast<T*>(a.out);
   #pragma unroll
       for (int b = 0; b < 2; ++b) {
   #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int prow = ct.row0 + wave_t * 128 + j * 32 + lr;
+          const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
           if (prow < ct.row_end) {
   #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              const int col = ct.wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * kh;
+              const int col = ct.wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * ekh;
               float v[4];
   #pragma unroll
               for (int r = 0; r < 4; ++r)
-                v[r] = gate_act(a.act, acc[b][j][4 * q + r]) * acc[b + 2][j][4 * q + r];
+                v[r] = gate_act(a.act, acc_read(acc[b][j][4 * q + r])) *
+                       acc_read(acc[b + 2][j][4 * q + r]);
               store4<T>(inter + static_cast<size_t>(prow) * a.I + col, v[0], v[1], v[2], v[3]);
             }
           }
+          // One (b, j) pair at a time, its accumulators cleared in place:
+          // keeps the epilogue's temporaries within the register file.
+          acc[b][j] = f32x16{};
+          acc[b + 2][j] = f32x16{};
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     } else {
@@ -281,41 +354,87 @@ void ffn_tiled_kernel(const FfnArgs a) {
       for (int b = 0; b < 4; ++b) {
   #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int prow = ct.row0 + wave_t * 128 + j * 32 + lr;
+          const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
           if (prow < ct.row_end) {
   #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              const int h = ct.wtile * kTileW + wave_w * 128 + b * 32 + 8 * q + 4 * kh;
+              const int h = ct.wtile * kTileW + wave_w * 128 + b * 32 + 8 * q + 4 * ekh;
               store4<float>(y + static_cast<size_t>(prow) * a.H + h, acc[b][j][4 * q],
                             acc[b][j][4 * q + 1], acc[b][j][4 * q + 2], acc[b][j][4 * q + 3]);
             }
           }
+          acc[b][j] = f32x16{};
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
-
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
     Lc += G;
-    if (Lc >= n_work) break;
-    ct = decode(Lc);
+    if (Lc >= n_seq) break;
+    cw = decode(Lc);
   }
   // No direct-to-LDS write may still be in flight when the workgroup's LDS is
   // released.
   wait_vmcnt<0>();
 }
 
+// Sums the S partial tiles of each split tail item of the tiled gate_up and
+// writes act(gate) * up to inter, with the epilogue's lane mapping. Task
+// (item, b, j) covers gate block b and up block b + 2 against token block j of
+// every wave: 16 KB read per part, 4 KB of inter written at most.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void gate_up_tail_fixup(const FfnArgs a) {
+  const int n_t = a.tile_map[0];
+  const int per_split = a.n_wtiles * n_t;
+  const int nk = a.k_per_split / kBK;
+  const WorkSplit ws = work_split(a.splits * per_split, a.grid, nk, a.part_units);
+  const int tasks = ws.n_units / ws.S * 8;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int wave_w = wave >> 1, wave_t = wave & 1, lr = lane & 31, kh = lane >> 5;
+  T* inter = static_cast<T*>(a.out);
+  for (int task = blockIdx.x; task < tasks; task += gridDim.x) {
+    const int it = task >> 3, b = (task >> 2) & 1, j = task & 3;
+    const Tile t = decode_tile(a, ws.n_full + it, per_split, n_t, kTileT);
+    const int prow = t.row0 + wave_t * 128 + j * 32 + lr;
+    if (prow >= t.row_end) continue;
+    f32x4 g[4] = {}, u[4] = {};
+    for (int p = 0; p < ws.S; ++p) {
+      const f32x4* pp = reinterpret_cast<const f32x4*>(a.part) +
+                        static_cast<size_t>((it * ws.S + p) * 4 + wave) * kPartVecsPerWave + lane;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        g[q] += pp[((b * 4 + j) * 4 + q) * kWave];
+        u[q] += pp[(((b + 2) * 4 + j) * 4 + q) * kWave];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int col = t.wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * kh;
+      store4<T>(inter + static_cast<size_t>(prow) * a.I + col, gate_act(a.act, g[q][0]) * u[q][0],
+                gate_act(a.act, g[q][1]) * u[q][1], gate_act(a.act, g[q][2]) * u[q][2],
+                gate_act(a.act, g[q][3]) * u[q][3]);
+    }
+  }
+}
+
 template <bool kGateUp>
-hipError_t launch_tiled(const FfnArgs& a, int dtype, hipStream_t s) {
-  const long work = static_cast<long>(a.n_wtiles) * a.max_tiles * a.splits;
+hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
+  const long work = static_cast<long>(args.n_wtiles) * args.max_tiles * args.splits;
   if (work == 0) return hipSuccess;
-  const int nwg = static_cast<int>(work < device_cu_count() ? work : device_cu_count());
+  FfnArgs a = args;
+  a.grid = static_cast<int>(work < device_cu_count() ? work : device_cu_count());
+  if (!kGateUp || !a.part) a.part_units = 0;
   if (dtype == MOE355_BF16)
-    ffn_tiled_kernel<bf16, kGateUp><<<dim3(nwg), dim3(kThreads), 0, s>>>(a);
+    ffn_tiled_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else
-    ffn_tiled_kernel<f16, kGateUp><<<dim3(nwg), dim3(kThreads), 0, s>>>(a);
+    ffn_tiled_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || a.part_units == 0) return err;
+  // The split depends on the device-side tile count; without a tail the
+  // fix-up finds no task and exits.
+  if (dtype == MOE355_BF16)
+    gate_up_tail_fixup<bf16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+  else
+    gate_up_tail_fixup<f16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   return hipGetLastError();
 }
 

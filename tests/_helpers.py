@@ -60,3 +60,31 @@ def gpu_fused(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch.Te
 def read_ws(plan: _capi.Plan, ws: torch.Tensor, off: int, n: int) -> np.ndarray:
     """int32 array of n entries at byte offset `off` of the workspace."""
     return ws[off:off + 4 * n].cpu().view(torch.int32).numpy().copy()
+
+
+def tail_split(n_work: int, G: int, nk: int, cap: int) -> Tuple[int, int, int]:
+    """(n_full, n_units, S) of the tiled gate_up's tail split, as the kernel
+    derives it (reframework_amd/csrc/dma_pipe.h, work_split): lets a test
+    state which shapes run the K-split tail and its fix-up."""
+    R = n_work // G if G > 0 else 0
+    tail = n_work - R * G
+    if cap <= 0 or tail == 0:
+        return n_work, 0, 1
+    cap = min(cap, G)
+    best, S, s = 7 * nk, 1, 2
+    while s <= 16 and s * tail <= cap and nk % s == 0:
+        c = 7 * nk // s + s * tail
+        if c < best:
+            best, S = c, s
+        s *= 2
+    return (R * G, tail * S, S) if S > 1 else (n_work, 0, 1)
+
+
+def tiled_gate_up_split(plan: _capi.Plan, counts: Sequence[int], cus: int) -> int:
+    """S of the tiled gate_up for per-expert row counts `counts` on `cus` CUs
+    (1: no split)."""
+    n_t = sum(-(-int(c) // plan.tile_rows) for c in counts)
+    n_wtiles = plan.I // 128
+    G = min(n_wtiles * plan.max_tiles, cus)
+    cap = plan.down_splits * plan.rows * plan.H * 4 // (256 * 256 * 4)
+    return tail_split(n_wtiles * n_t, G, plan.H // 32, min(cap, 4096))[2]
