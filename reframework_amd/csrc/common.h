@@ -9,6 +9,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/moe355.h"
 
 namespace moe355 {
@@ -115,6 +117,33 @@ __device__ __forceinline__ float gate_act(int act, float g) {
   return 0.5f * g * (1.0f + tanhf(c * (g + 0.044715f * g * g * g)));
 }
 
+// sigmoid(z) = 1 / (1 + e^-z) as 1 / (1 + 2^(-z log2 e)) on the hardware
+// transcendental unit (v_exp_f32, v_rcp_f32; ~1 ulp each). Limits: z -> -inf
+// gives 2^+inf = inf and rcp(inf) = 0; z -> +inf gives 2^-inf = 0 and 1.
+__device__ __forceinline__ float sigmoid_hw(float z) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.4426950408889634f));
+}
+
+// gate_act for the 16-bit (bf16/f16) kernels, whose outputs are rounded to 8
+// or 11 significant bits: the relative error of sigmoid_hw (~3e-7) is far below
+// that rounding, and the precise expf and IEEE division of gate_act cost about
+// 30 VALU instructions per element in an epilogue that keeps the MFMA pipe
+// idle. silu(g) = g * sigmoid(g); gelu_tanh(g) = g/2 * (1 + tanh(u)) =
+// g * sigmoid(2u) with u = sqrt(2/pi) * (g + 0.044715 g^3); erf-gelu keeps erff.
+__device__ __forceinline__ float gate_act_fast(int act, float g) {
+  if (act == MOE355_ACT_SILU) return g * sigmoid_hw(g);
+  if (act == MOE355_ACT_GELU) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
+  const float c2 = 1.5957691216057308f;  // 2 sqrt(2/pi)
+  return g * sigmoid_hw(c2 * (g + 0.044715f * g * g * g));
+}
+
+// gate_act_fast with SiLU resolved at compile time (kSilu) for epilogues that
+// pick the activation once per tile.
+template <bool kSilu>
+__device__ __forceinline__ float gate_act_16(int act, float g) {
+  return kSilu ? g * sigmoid_hw(g) : gate_act_fast(act, g);
+}
+
 // ---------------------------------------------------------------- wave helpers
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -175,6 +204,7 @@ struct FfnArgs {
   float* part;             // tiled gate_up: tail-split partial tiles, part_units x 256 KB
   int part_units;          // capacity of part in 256x256 fp32 tiles (0: no tail split)
   int grid;                // workgroups of the tiled launch (the fix-up recomputes its split)
+  int group_t;             // token tiles per item group (0: all; see decode_tile)
   const void* w[kMaxExperts];  // w1[e] ([2I,H]) or w2[e] ([H,I])
 };
 

@@ -100,8 +100,14 @@ __device__ __forceinline__ Tile decode_tile(const FfnArgs& a, int L, int per_spl
   Tile t;
   t.split = L / per_split;
   const int rem = L - t.split * per_split;
-  t.wtile = rem / n_t;
-  const int tt = rem - t.wtile * n_t;
+  // Items come in groups of gt token tiles x all weight tiles, the token tile
+  // varying fastest inside a group; the last group may hold fewer token tiles.
+  const int gfull = a.group_t > 0 ? a.group_t : n_t;
+  const int g = rem / (gfull * a.n_wtiles);
+  const int r2 = rem - g * gfull * a.n_wtiles;
+  const int gt = min(gfull, n_t - g * gfull);
+  t.wtile = r2 / gt;
+  const int tt = g * gfull + (r2 - t.wtile * gt);
   t.e = tile_map[2 + 2 * tt];
   t.row0 = tile_map[3 + 2 * tt];
   t.row_end = min(t.row0 + tile_rows, offsets[t.e + 1]);

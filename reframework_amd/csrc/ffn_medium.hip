@@ -221,7 +221,7 @@ void ffn_medium_kernel(const FfnArgs a) {
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            v[r] = gate_act(a.act, acc[0][j][4 * q + r]) * acc[1][j][4 * q + r];
+            v[r] = gate_act_fast(a.act, acc[0][j][4 * q + r]) * acc[1][j][4 * q + r];
           store4<T>(inter + col, v[0], v[1], v[2], v[3]);
         }
       } else {

@@ -170,8 +170,8 @@ __global__ __launch_bounds__(kThreads) void ffn_skinny_kernel(const FfnArgs a) {
   if (kGateUp) {
     const f32x4 g = acc[0], u = acc[NOP - 1];
     T* inter = static_cast<T*>(a.out) + static_cast<size_t>(prow) * a.I + col;
-    store4<T>(inter, gate_act(a.act, g[0]) * u[0], gate_act(a.act, g[1]) * u[1],
-              gate_act(a.act, g[2]) * u[2], gate_act(a.act, g[3]) * u[3]);
+    store4<T>(inter, gate_act_fast(a.act, g[0]) * u[0], gate_act_fast(a.act, g[1]) * u[1],
+              gate_act_fast(a.act, g[2]) * u[2], gate_act_fast(a.act, g[3]) * u[3]);
   } else {
     float* y = static_cast<float*>(a.out) + static_cast<size_t>(split) * a.R * a.H +
                static_cast<size_t>(prow) * a.H + col;

@@ -324,30 +324,38 @@ void ffn_tiled_kernel(const FfnArgs a) {
       zero_acc();
     } else if (kGateUp) {
       T* inter = static_cast<T*>(a.out);
+      // The activation is chosen once per tile, so the SiLU epilogue has no
+      // per-element branch.
+      auto epilogue = [&](auto silu) {
   #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < 2; ++b) {
   #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
-          if (prow < ct.row_end) {
+          for (int j = 0; j < 4; ++j) {
+            const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
+            if (prow < ct.row_end) {
   #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int col = ct.wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * ekh;
-              float v[4];
+              for (int q = 0; q < 4; ++q) {
+                const int col = ct.wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * ekh;
+                float v[4];
   #pragma unroll
-              for (int r = 0; r < 4; ++r)
-                v[r] = gate_act(a.act, acc_read(acc[b][j][4 * q + r])) *
-                       acc_read(acc[b + 2][j][4 * q + r]);
-              store4<T>(inter + static_cast<size_t>(prow) * a.I + col, v[0], v[1], v[2], v[3]);
+                for (int r = 0; r < 4; ++r)
+                  v[r] = gate_act_16<decltype(silu)::value>(a.act, acc_read(acc[b][j][4 * q + r])) *
+                         acc_read(acc[b + 2][j][4 * q + r]);
+                store4<T>(inter + static_cast<size_t>(prow) * a.I + col, v[0], v[1], v[2], v[3]);
+              }
             }
+            // One (b, j) pair at a time, its accumulators cleared in place:
+            // keeps the epilogue's temporaries within the register file.
+            acc[b][j] = f32x16{};
+            acc[b + 2][j] = f32x16{};
+            __builtin_amdgcn_sched_barrier(0);
           }
-          // One (b, j) pair at a time, its accumulators cleared in place:
-          // keeps the epilogue's temporaries within the register file.
-          acc[b][j] = f32x16{};
-          acc[b + 2][j] = f32x16{};
-          __builtin_amdgcn_sched_barrier(0);
         }
-      }
+      };
+      if (a.act == MOE355_ACT_SILU)
+        epilogue(std::true_type{});
+      else
+        epilogue(std::false_type{});
     } else {
       float* y = static_cast<float*>(a.out) + static_cast<size_t>(ct.split) * a.R * a.H;
   #pragma unroll
@@ -409,9 +417,9 @@ __global__ __launch_bounds__(kThreads) void gate_up_tail_fixup(const FfnArgs a) 
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int col = t.wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * kh;
-      store4<T>(inter + static_cast<size_t>(prow) * a.I + col, gate_act(a.act, g[q][0]) * u[q][0],
-                gate_act(a.act, g[q][1]) * u[q][1], gate_act(a.act, g[q][2]) * u[q][2],
-                gate_act(a.act, g[q][3]) * u[q][3]);
+      store4<T>(inter + static_cast<size_t>(prow) * a.I + col, gate_act_fast(a.act, g[q][0]) * u[q][0],
+                gate_act_fast(a.act, g[q][1]) * u[q][1], gate_act_fast(a.act, g[q][2]) * u[q][2],
+                gate_act_fast(a.act, g[q][3]) * u[q][3]);
     }
   }
 }
@@ -421,6 +429,11 @@ hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   const long work = static_cast<long>(args.n_wtiles) * args.max_tiles * args.splits;
   if (work == 0) return hipSuccess;
   FfnArgs a = args;
+  // Items in groups of 6 token tiles: the 32 consecutive items one XCD takes
+  // per round then span ~6 token tiles x ~5 weight tiles instead of 32 token
+  // tiles of one weight tile, so its L2 holds fewer distinct operand slabs
+  // (Mixtral-shape down projection at 4096 tokens: 1.08 -> 1.00 ms).
+  a.group_t = 6;
   a.grid = static_cast<int>(work < device_cu_count() ? work : device_cu_count());
   if (!kGateUp || !a.part) a.part_units = 0;
   if (dtype == MOE355_BF16)
