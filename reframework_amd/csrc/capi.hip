@@ -151,10 +151,13 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
     // Pick the split that minimises the busiest CU's step count, charging each
     // extra split its fp32 partial plane (written once, read by the combine)
     // at ~1.8e-6 steps per element; ties keep fewer splits.
+    // Each split must be a whole number of pipeline steps: 64 k for the
+    // 256-row kernel, 32 k for the 64-row one.
     const long long items = static_cast<long long>(H / 256) * p->max_tiles;
     const int cus = moe355::device_cu_count();
+    const int step_k = p->path == MOE355_PATH_MFMA_TILED ? 64 : 32;
     double best = 0.0;
-    for (int s = 1; s <= 8 && (I / 32) % s == 0; s *= 2) {
+    for (int s = 1; s <= 8 && (I / step_k) % s == 0; s *= 2) {
       const long long rounds = (items * s + cus - 1) / cus;
       const double cost = static_cast<double>(rounds) * (I / 32 / s) +
                           (s - 1) * static_cast<double>(R) * H * 1.8e-6;

@@ -17,15 +17,20 @@
 //            gathered straight from x through row_src (no permuted copy of x).
 //   down:    256 rows of w2 against the permuted inter rows, fp32 partials
 //            per K-split into y.
-// Operands move global -> LDS with direct-to-LDS loads (no register staging),
-// 32 k per step in five 32 KB LDS buffers (the whole 160 KB LDS), issued three
-// steps ahead of the MFMAs and interleaved with them. LDS rows are 64 B,
-// XOR-swizzled in 16-byte chunks (swz) so the operand reads are bank-conflict
-// free. The kernel is persistent (one workgroup per CU) and streams its K-steps
-// across tile boundaries, so each tile's pipeline fill overlaps the previous
-// tile's epilogue. The gate_up items left for a last, mostly idle round are
-// split along K over the idle CUs (work_split); their fp32 partial tiles are
-// summed and activated by gate_up_tail_fixup.
+// Operands move global -> LDS with direct-to-LDS loads (no register staging)
+// in steps of 64 k. One operand of one step is a 32 KB buffer of 256 rows of
+// 128 B, so every load instruction fetches whole 128-byte lines (8 rows x
+// 128 B): the L1 then tracks half as many outstanding requests per byte as with
+// 64-byte rows, which is what bounds the load stream. Five such buffers (the
+// whole 160 KB LDS) form a ring over the operand stream W0 X0 W1 X1 ...;
+// weights are issued two steps ahead of their use, tokens (mostly L2 hits)
+// one step ahead. Rows are XOR-swizzled in 16-byte chunks (swz8) so the MFMA
+// operand reads are bank-conflict free. The kernel is persistent (one
+// workgroup per CU) and streams its steps across tile boundaries, so each
+// tile's pipeline fill overlaps the previous tile's epilogue. The gate_up
+// items left for a last, mostly idle round are split along K over the idle
+// CUs (work_split); their fp32 partial tiles are summed and activated by
+// gate_up_tail_fixup.
 #include "dma_pipe.h"
 
 namespace moe355 {
@@ -36,16 +41,30 @@ using namespace pipe;
 constexpr int kThreads = 256;
 constexpr int kTileW = 256;
 constexpr int kTileT = 256;
-constexpr int kRegionBytes = kTileW * kRowBytes;      // 16 KB
-constexpr int kStageBytes = 2 * kRegionBytes;         // weights + tokens
-constexpr int kStages = 5;
-constexpr int kLdsBytes = kStages * kStageBytes;      // 160 KB: the whole LDS
-constexpr int kLoadsPerWave = kStageBytes / 1024 / (kThreads / kWave);  // 8 x 1 KB
+constexpr int kSK = 64;                         // k per pipeline step
+constexpr int kSRowBytes = kSK * 2;             // 128 B: 8 chunks of 16 B
+constexpr int kBufBytes = kTileW * kSRowBytes;  // 32 KB: one operand of one step
+constexpr int kBufs = 5;                        // 160 KB: the whole LDS
+constexpr int kLoadsPerOp = kBufBytes / 1024 / (kThreads / kWave);  // 8 x 1 KB per wave
 // One tail-split unit's partial tile: 4 waves x 16 (i, j) MFMA blocks x 4 x 64
 // lanes of f32x4, stored in register order so every store is 1 KB contiguous.
 constexpr int kPartVecsPerWave = 4 * 4 * 4 * kWave;
 
-// A work item or a K-part of a split tail item: its tile, K-step range and
+// Physical 16-byte chunk of logical chunk c (0..7) in the 128-byte LDS row r.
+// Two consecutive rows fill one 256-byte span of the 64-bank LDS; XOR with
+// (r >> 1) & 7 gives the eight row pairs of any 16 consecutive rows different
+// chunk columns, so 16 rows read at one logical chunk hit 16 distinct 16-byte
+// bank groups. The map is an involution.
+__device__ __forceinline__ uint32_t swz8(int c, int r) {
+  return static_cast<uint32_t>(c ^ ((r >> 1) & 7));
+}
+
+__device__ __forceinline__ int ring_add(int b, int n) {  // (b + n) % kBufs, 0 <= n < kBufs
+  b += n;
+  return b >= kBufs ? b - kBufs : b;
+}
+
+// A work item or a K-part of a split tail item: its tile, step range and
 // partial-tile slot (-1 for a whole item).
 struct Work {
   Tile t;
@@ -71,15 +90,30 @@ __device__ __forceinline__ Work decode_work(const FfnArgs& a, const WorkSplit& w
 }
 
 // Persistent: one workgroup per CU walks work items L = L0, L0 + G, ... (G =
-// grid size) of the (split, weight tile, token tile) space. Its K-steps form
-// one continuous stream: the direct-to-LDS loads run kStages-1 steps ahead of
-// the MFMAs and cross into the next tile while the current one is still being
-// multiplied, so the next tile's first stages are in flight during the
-// epilogue and no workgroup launch or pipeline fill is paid per tile.
+// grid size) of the (split, weight tile, token tile) space. Its steps form one
+// continuous stream; two load cursors (weights, tokens) walk it ahead of the
+// MFMAs and cross into the next item while the current one is still being
+// multiplied, so no workgroup launch or pipeline fill is paid per tile.
+//
+// Pipeline, step s (64 k = four 16-k sub-steps of 16 MFMAs per wave). Operand
+// W_s (weights) sits in LDS buffer (2s) % 5, X_s (tokens) in (2s + 1) % 5.
+//   sub-step 0: MFMAs of (s, 0); read operands (s, 1); issue X_{s+1} loads 4-7
+//   sub-step 1: MFMAs of (s, 1); read operands (s, 2); issue W_{s+2} loads 0-3
+//   sub-step 2: MFMAs of (s, 2); read operands (s, 3); issue W_{s+2} loads 4-7
+//   barrier B_s: each wave waits until at most its 8 W_{s+2} loads are in
+//                flight, so W_{s+1} and X_{s+1} have landed; after it no wave
+//                reads the buffers of step s again (the operands of (s, 3) are
+//                in registers).
+//   sub-step 3: MFMAs of (s, 3); read operands (s+1, 0); issue X_{s+2} loads
+//               0-3 into the buffer of W_s, freed by B_s.
+// W_{s+2} goes to buffer (2s + 4) % 5, which held X_{s-1} (freed by B_{s-1}),
+// and X_{s+1} to (2s + 3) % 5, which held W_{s-1}. Weights thus have about
+// two steps to land and tokens one. Other vector-memory operations issued in
+// between (row_src prefetch, epilogue stores) only make the waits stricter.
 template <typename T, bool kGateUp>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void ffn_tiled_kernel(const FfnArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kBufs * kBufBytes];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -89,7 +123,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
   const int per_split = a.n_wtiles * n_t;
   const int n_work = a.splits * per_split;
   const int G = gridDim.x;
-  const int nk = a.k_per_split / kBK;
+  const int nk = a.k_per_split / kSK;
   // Work sequence L0, L0 + G, ...: whole items below ws.n_full, then (gate_up
   // only) at most one tail unit per workgroup.
   const WorkSplit ws = work_split(n_work, G, nk, kGateUp ? a.part_units : 0);
@@ -102,85 +136,104 @@ void ffn_tiled_kernel(const FfnArgs a) {
 
   auto decode = [&](int L) { return decode_work(a, ws, L, per_split, n_t, nk); };
 
-  // Stage = 32 loads of 1 KB (16 rows x 64 B each). Waves 0-1 fill the weight
-  // region, waves 2-3 the token region, 8 loads each: load q of wave w covers
-  // region rows 16 * (8 * (w & 1) + q) .. +15. Lane i of a load fills row
-  // 16 * (...) + i / 4, physical chunk i % 4, so it fetches that row's logical
-  // chunk swz(i % 4, row) (the swizzle is an involution) from global memory.
-  const bool wload = wave < 2;
-  auto region_row = [&](int q, int ln) { return ((wave & 1) * kLoadsPerWave + q) * 16 + (ln >> 2); };
+  // An operand buffer is 32 loads of 1 KB, 8 rows x 128 B each; wave w issues
+  // loads q = 0..7, covering rows 8 (8 w + q) + i / 8 for lane i. Lane i writes
+  // physical chunk i % 8 of its row, so it fetches that row's logical chunk
+  // swz8(i % 8, row) (the swizzle is an involution) from global memory.
+  auto op_row = [&](int q, int ln) { return (wave * kLoadsPerOp + q) * 8 + (ln >> 3); };
 
-  // gate_up token rows come through row_src; they are fetched one tile ahead.
-  int grow[kLoadsPerWave];
+  // Weight cursor: work item wL, step wkt of [.., wke); source base and
+  // per-load offsets.
+  int wL = Lc, wkt = 0, wke = 0;
+  const char* wsrc;
+  uint32_t woff[kLoadsPerOp];
+  auto setup_w = [&](const Work& w) {
+    const Tile& t = w.t;
+    wkt = w.kb;
+    wke = w.ke;
+    const int ln = opaque(lane);
+    wsrc = static_cast<const char*>(a.w[t.e]) + static_cast<size_t>(t.split) * a.k_per_split * 2;
+#pragma unroll
+    for (int q = 0; q < kLoadsPerOp; ++q) {
+      const int r = op_row(q, ln);
+      const int wr = kGateUp ? (r < kTileW / 2 ? t.wtile * (kTileW / 2) + r
+                                               : a.I + t.wtile * (kTileW / 2) + (r - kTileW / 2))
+                             : t.wtile * kTileW + r;
+      woff[q] = static_cast<uint32_t>(wr) * pitch + swz8(ln & 7, r) * 16;
+    }
+  };
+
+  // Token cursor: work item xL, step xkt of [.., xke). gate_up token rows come
+  // through row_src; they are fetched one item ahead.
+  int xL = Lc, xkt = 0, xke = 0;
+  const char* xsrc;
+  uint32_t xoff[kLoadsPerOp];
+  int grow[kLoadsPerOp];
   auto fetch_rows = [&](const Tile& t) {
     const int ln = opaque(lane);
 #pragma unroll
-    for (int q = 0; q < kLoadsPerWave; ++q)
-      grow[q] = a.row_src[min(t.row0 + region_row(q, ln), t.row_end - 1)];
+    for (int q = 0; q < kLoadsPerOp; ++q)
+      grow[q] = a.row_src[min(t.row0 + op_row(q, ln), t.row_end - 1)];
   };
-
-  // Load cursor: work item Ll, step lkt of [.., lke); source base and per-load
-  // offsets.
-  int Ll = Lc, lkt = 0, lke = 0;
-  const char* lsrc;
-  uint32_t lgoff[kLoadsPerWave];
-  auto setup_load = [&](const Work& w) {
+  auto setup_x = [&](const Work& w) {
     const Tile& t = w.t;
-    lkt = w.kb;
-    lke = w.ke;
+    xkt = w.kb;
+    xke = w.ke;
     const int ln = opaque(lane);
     const size_t kbeg = static_cast<size_t>(t.split) * a.k_per_split;
-    if (wload) {
-      lsrc = static_cast<const char*>(a.w[t.e]) + kbeg * 2;
+    if (kGateUp) {
+      xsrc = static_cast<const char*>(a.x) + kbeg * 2;
 #pragma unroll
-      for (int q = 0; q < kLoadsPerWave; ++q) {
-        const int r = region_row(q, ln);
-        const int wr = kGateUp ? (r < kTileW / 2 ? t.wtile * (kTileW / 2) + r
-                                                 : a.I + t.wtile * (kTileW / 2) + (r - kTileW / 2))
-                               : t.wtile * kTileW + r;
-        lgoff[q] = static_cast<uint32_t>(wr) * pitch + swz(ln & 3, r) * 16;
-      }
-    } else if (kGateUp) {
-      lsrc = static_cast<const char*>(a.x) + kbeg * 2;
-#pragma unroll
-      for (int q = 0; q < kLoadsPerWave; ++q)
-        lgoff[q] = static_cast<uint32_t>(grow[q]) * pitch + swz(ln & 3, region_row(q, ln)) * 16;
+      for (int q = 0; q < kLoadsPerOp; ++q)
+        xoff[q] = static_cast<uint32_t>(grow[q]) * pitch + swz8(ln & 7, op_row(q, ln)) * 16;
     } else {
-      lsrc = static_cast<const char*>(a.x) + (static_cast<size_t>(t.row0) * ld + kbeg) * 2;
+      xsrc = static_cast<const char*>(a.x) + (static_cast<size_t>(t.row0) * ld + kbeg) * 2;
 #pragma unroll
-      for (int q = 0; q < kLoadsPerWave; ++q) {
-        const int r = region_row(q, ln);
+      for (int q = 0; q < kLoadsPerOp; ++q) {
+        const int r = op_row(q, ln);
         const int xr = min(t.row0 + r, t.row_end - 1) - t.row0;
-        lgoff[q] = static_cast<uint32_t>(xr) * pitch + swz(ln & 3, r) * 16;
+        xoff[q] = static_cast<uint32_t>(xr) * pitch + swz8(ln & 7, r) * 16;
       }
     }
   };
   auto prefetch_next_rows = [&]() {
-    if (kGateUp && !wload && Ll + G < n_seq) fetch_rows(decode(Ll + G).t);
+    if (kGateUp && xL + G < n_seq) fetch_rows(decode(xL + G).t);
   };
-  // Step to the next K-step of the load stream; past the last work item the
-  // cursor stays on its final step, so the tail keeps issuing (harmless,
-  // in-bounds) loads into buffers nobody reads and the vmcnt accounting of
-  // the pipeline stays fixed.
-  auto advance_load = [&]() {
-    if (++lkt < lke) return;
-    if (Ll + G < n_seq) {
-      Ll += G;
-      setup_load(decode(Ll));
-      prefetch_next_rows();
+  // Step a cursor to its next step; past the last work item it stays on its
+  // final step, so the tail keeps issuing (harmless, in-bounds) loads into
+  // buffers nobody reads and the vmcnt accounting of the pipeline stays fixed.
+  auto advance_w = [&]() {
+    if (++wkt < wke) return;
+    if (wL + G < n_seq) {
+      wL += G;
+      setup_w(decode(wL));
     } else {
-      lkt = lke - 1;
+      wkt = wke - 1;
     }
   };
-  // Loads q0 .. q0+n-1 of the current load step into LDS buffer lb.
-  auto issue = [&](uint8_t* lb, int q0, int n) {
-    uint8_t* dst = lb + wave * kLoadsPerWave * 1024;
+  auto advance_x = [&]() {
+    if (++xkt < xke) return;
+    if (xL + G < n_seq) {
+      xL += G;
+      setup_x(decode(xL));
+      prefetch_next_rows();
+    } else {
+      xkt = xke - 1;
+    }
+  };
+  // Loads q0 .. q0+n-1 of a cursor's current step into LDS buffer b.
+  auto issue_w = [&](int b, int q0, int n) {
+    uint8_t* dst = lds + b * kBufBytes + wave * kLoadsPerOp * 1024;
 #pragma unroll
-    for (int q = q0; q < q0 + n; ++q)
-      dma16(lsrc + lkt * kRowBytes + lgoff[q], dst + q * 1024);
+    for (int q = q0; q < q0 + n; ++q) dma16(wsrc + wkt * kSRowBytes + woff[q], dst + q * 1024);
+  };
+  auto issue_x = [&](int b, int q0, int n) {
+    uint8_t* dst = lds + b * kBufBytes + wave * kLoadsPerOp * 1024;
+#pragma unroll
+    for (int q = q0; q < q0 + n; ++q) dma16(xsrc + xkt * kSRowBytes + xoff[q], dst + q * 1024);
   };
 
-  // MFMA operand rows of this wave inside a stage.
+  // MFMA operand rows of this wave inside a buffer.
   const int lr = lane & 31, kh = lane >> 5;
   uint32_t arow[4], brow[4];
 #pragma unroll
@@ -190,13 +243,13 @@ void ffn_tiled_kernel(const FfnArgs a) {
       rb = b < 2 ? wave_w * 64 + b * 32 : kTileW / 2 + wave_w * 64 + (b - 2) * 32;
     else
       rb = wave_w * 128 + b * 32;
-    arow[b] = (rb + lr) * kRowBytes;
-    brow[b] = kRegionBytes + (wave_t * 128 + b * 32 + lr) * kRowBytes;
+    arow[b] = (rb + lr) * kSRowBytes;
+    brow[b] = (wave_t * 128 + b * 32 + lr) * kSRowBytes;
   }
   // Operand rows start at multiples of 32, so the swizzle bits are lr's.
-  uint32_t coff[kBK / 16];
+  uint32_t coff[kSK / 16];
 #pragma unroll
-  for (int ks = 0; ks < kBK / 16; ++ks) coff[ks] = swz(ks * 2 + kh, lr) << 4;
+  for (int j = 0; j < kSK / 16; ++j) coff[j] = swz8(2 * j + kh, lr) << 4;
 
   f32x16 acc[4][4];
 
@@ -215,62 +268,39 @@ void ffn_tiled_kernel(const FfnArgs a) {
       for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
   };
 
-  auto read_frags = [&](const uint8_t* st, int ks, u32x4* af, u32x4* bf) {
+  auto read_frags = [&](int bw, int bx, int j, u32x4* af, u32x4* bf) {
+    const uint8_t* sw = lds + bw * kBufBytes;
+    const uint8_t* sx = lds + bx * kBufBytes;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      af[b] = *reinterpret_cast<const u32x4*>(st + arow[b] + coff[ks]);
-      bf[b] = *reinterpret_cast<const u32x4*>(st + brow[b] + coff[ks]);
+      af[b] = *reinterpret_cast<const u32x4*>(sw + arow[b] + coff[j]);
+      bf[b] = *reinterpret_cast<const u32x4*>(sx + brow[b] + coff[j]);
     }
   };
 
-  // Pipeline over kStages LDS buffers. Invariant at the top of each step g:
-  // step g is in LDS and visible to every wave, the sub-step 0 operands of
-  // step g are in registers, and the loads of steps g+1 .. g+kStages-2 are in
-  // flight. Step g issues step g+kStages-1 into the buffer of step g-1 (whose
-  // last reads finished before step g-1's mid-step barrier), runs 16 MFMAs
-  // while reading its sub-step 1 operands, then waits at a mid-step barrier
-  // for step g+1 only, and runs 16 more MFMAs while reading step g+1's first
-  // operands. A load thus has about three steps to land. Other vector-memory
-  // operations issued in between (row_src prefetch, epilogue stores) only make
-  // the waits stricter.
-  {
-    const Work w0 = decode(Ll);
-    if (kGateUp && !wload) fetch_rows(w0.t);
-    setup_load(w0);
-    prefetch_next_rows();
-  }
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) {
-    issue(lds + s * kStageBytes, 0, kLoadsPerWave);
-    advance_load();
-  }
-  dma_barrier<(kStages - 2) * kLoadsPerWave>();  // step 0 landed
-
-  zero_acc();
-  u32x4 fa[2][4], fb[2][4];
-  read_frags(lds, 0, fa[0], fb[0]);
-  wait_lgkm0();
-
-  // Each half: wait for its operands (read during the previous half), then 16
-  // MFMAs. The next half's 8 operand reads and half of the next stage's loads
-  // are spread over the first 12 MFMAs (3 MFMA : 2 LDS reads : 1 load), so
-  // neither the LDS nor the texture unit sees a burst from all four waves and
-  // the last read still has 4 MFMAs to land.
-  auto half = [&](const u32x4* af, const u32x4* bf, const uint8_t* src, int ks, u32x4* na,
-                  u32x4* nb, uint8_t* lb, int q0) {
+  // One sub-step: wait for its operands (read during the previous sub-step),
+  // then 16 MFMAs; the next sub-step's 8 operand reads (sub-step j of buffers
+  // bw/bx) and 4 loads (issue(0..3)) are spread over the first 12 MFMAs
+  // (3 MFMA : 2 LDS reads : 1 load), so neither the LDS nor the texture unit
+  // sees a burst from all four waves and the last read still has 4 MFMAs to
+  // land.
+  auto sub = [&](const u32x4* af, const u32x4* bf, int bw, int bx, int j, u32x4* na, u32x4* nb,
+                 auto issue) {
     wait_lgkm0();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = Mfma32<T>::mma(af[i], bf[j], acc[i][j]);
+      for (int jj = 0; jj < 4; ++jj) acc[i][jj] = Mfma32<T>::mma(af[i], bf[jj], acc[i][jj]);
     // Memory operations in the order of the schedule below: the compiler keeps
     // LDS reads and direct-to-LDS loads in program order (it cannot tell that
     // they touch different buffers).
+    const uint8_t* sw = lds + bw * kBufBytes;
+    const uint8_t* sx = lds + bx * kBufBytes;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      na[i] = *reinterpret_cast<const u32x4*>(src + arow[i] + coff[ks]);
-      issue(lb, q0 + i, 1);
-      nb[i] = *reinterpret_cast<const u32x4*>(src + brow[i] + coff[ks]);
+      na[i] = *reinterpret_cast<const u32x4*>(sw + arow[i] + coff[j]);
+      issue(i);
+      nb[i] = *reinterpret_cast<const u32x4*>(sx + brow[i] + coff[j]);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -285,24 +315,52 @@ void ffn_tiled_kernel(const FfnArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  int cb = 0;  // LDS buffer of the step being multiplied
+  // Prologue: W_0, X_0, W_1 and the first half of X_1 (the loads sub-step 3
+  // of step -1 would issue), then wait for W_0 and X_0 and read the operands
+  // of (0, 0).
+  {
+    const Work w0 = decode(Lc);
+    if (kGateUp) fetch_rows(w0.t);
+    setup_w(w0);
+    setup_x(w0);
+    prefetch_next_rows();
+  }
+  issue_w(0, 0, kLoadsPerOp);
+  advance_w();
+  issue_x(1, 0, kLoadsPerOp);
+  advance_x();
+  issue_w(2, 0, kLoadsPerOp);
+  advance_w();
+  issue_x(3, 0, kLoadsPerOp / 2);
+  dma_barrier<kLoadsPerOp + kLoadsPerOp / 2>();  // W_0 and X_0 landed
+
+  zero_acc();
+  u32x4 fa[2][4], fb[2][4];
+  read_frags(0, 1, 0, fa[0], fb[0]);
+
+  int bw = 0;  // buffer of W_s (X_s is in the next one)
   Work cw = decode(Lc);
   while (true) {
     const Tile& ct = cw.t;
     for (int kt = cw.kb; kt < cw.ke; ++kt) {
-      const int nb_ = cb == kStages - 1 ? 0 : cb + 1;
-      const int lb_ = cb == 0 ? kStages - 1 : cb - 1;  // (cb + kStages - 1) % kStages
-      uint8_t* st = lds + cb * kStageBytes;
-      uint8_t* nx = lds + nb_ * kStageBytes;
-      uint8_t* lb = lds + lb_ * kStageBytes;
-      half(fa[0], fb[0], st, 1, fa[1], fb[1], lb, 0);
-      // Step g+1 landed (everything but steps g+2, g+3 and the first half of
-      // g+4 is done) and every wave finished reading step g-1's buffer.
+      const int bx = ring_add(bw, 1);
+      const int nbw = ring_add(bw, 2), nbx = ring_add(bw, 3);  // step s+1
+      const int bw2 = ring_add(bw, 4);                          // W_{s+2}
+      // X_{s+1} loads 4-7 (its buffer is nbx), then its cursor moves to X_{s+2}.
+      sub(fa[0], fb[0], bw, bx, 1, fa[1], fb[1],
+          [&](int i) { issue_x(nbx, kLoadsPerOp / 2 + i, 1); });
+      advance_x();
+      sub(fa[1], fb[1], bw, bx, 2, fa[0], fb[0], [&](int i) { issue_w(bw2, i, 1); });
+      sub(fa[0], fb[0], bw, bx, 3, fa[1], fb[1],
+          [&](int i) { issue_w(bw2, kLoadsPerOp / 2 + i, 1); });
+      advance_w();
+      // W_{s+1} and X_{s+1} landed (only W_{s+2} may be in flight) and every
+      // wave has read its last operands of step s.
       wait_lgkm0();
-      dma_barrier<(kStages - 3) * kLoadsPerWave + kLoadsPerWave / 2>();
-      half(fa[1], fb[1], nx, 0, fa[0], fb[0], lb, kLoadsPerWave / 2);
-      advance_load();
-      cb = nb_;
+      dma_barrier<kLoadsPerOp>();
+      // X_{s+2} loads 0-3 into the buffer of W_s.
+      sub(fa[1], fb[1], nbw, nbx, 0, fa[0], fb[0], [&](int i) { issue_x(bw, i, 1); });
+      bw = nbw;
     }
 
     // Epilogue. Lane (lr, kh) of block (i, j) holds, for q = 0..3, features
@@ -393,7 +451,7 @@ template <typename T>
 __global__ __launch_bounds__(kThreads) void gate_up_tail_fixup(const FfnArgs a) {
   const int n_t = a.tile_map[0];
   const int per_split = a.n_wtiles * n_t;
-  const int nk = a.k_per_split / kBK;
+  const int nk = a.k_per_split / kSK;
   const WorkSplit ws = work_split(a.splits * per_split, a.grid, nk, a.part_units);
   const int tasks = ws.n_units / ws.S * 8;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -428,6 +486,7 @@ template <bool kGateUp>
 hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   const long work = static_cast<long>(args.n_wtiles) * args.max_tiles * args.splits;
   if (work == 0) return hipSuccess;
+  if (args.k_per_split % kSK != 0) return hipErrorInvalidValue;
   FfnArgs a = args;
   // Items in groups of 6 token tiles: the 32 consecutive items one XCD takes
   // per round then span ~6 token tiles x ~5 weight tiles instead of 32 token
