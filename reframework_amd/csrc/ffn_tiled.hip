@@ -196,8 +196,11 @@ void ffn_tiled_kernel(const FfnArgs a) {
       }
     }
   };
+  // Unconditional (past the last item it fetches the current item's rows
+  // again): a conditional load leaves two values of grow to merge, and the
+  // register copies that merge them wait for the loads to land (vmcnt(0)).
   auto prefetch_next_rows = [&]() {
-    if (kGateUp && xL + G < n_seq) fetch_rows(decode(xL + G).t);
+    if (kGateUp) fetch_rows(decode(xL + G < n_seq ? xL + G : xL).t);
   };
   // Step a cursor to its next step; past the last work item it stays on its
   // final step, so the tail keeps issuing (harmless, in-bounds) loads into
