@@ -124,12 +124,14 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
                         2ll * I * H * esz < (1ll << 32);
   const bool skinny_ok = mfma && H % 128 == 0 && I % 128 == 0;
   if (path < 0) {
-    // Average rows per active expert decide: weight streaming with 16-token
-    // tiles up to 32, 64-token tiles up to 96, 256-token tiles above (the
-    // 64-row kernel wins only where a 256-row tile would be three-quarters
-    // padding; from ~128 rows the bigger tile's reuse pays more).
-    path = tiled_ok && avg > 96   ? MOE355_PATH_MFMA_TILED
-           : tiled_ok && avg > 32 ? MOE355_PATH_MFMA_MEDIUM
+    // Average rows per active expert decide (measured layer times, Mixtral,
+    // Phi-3.5 and fine-grained shapes): weight streaming with 16-token tiles up
+    // to 10 rows (beyond that each 16-row tile re-streams the weights),
+    // 64-token tiles up to 48, 256-token tiles above (from ~48 rows the
+    // 256-row kernel's weight stream outruns the 64-row kernel despite its
+    // padding: Mixtral 256 tokens 0.67 vs 0.74 ms).
+    path = tiled_ok && avg > 48   ? MOE355_PATH_MFMA_TILED
+           : tiled_ok && avg > 10 ? MOE355_PATH_MFMA_MEDIUM
            : skinny_ok            ? MOE355_PATH_MFMA_SKINNY
                                   : MOE355_PATH_SIMT;
   } else if (((path == MOE355_PATH_MFMA_TILED || path == MOE355_PATH_MFMA_MEDIUM) && !tiled_ok) ||

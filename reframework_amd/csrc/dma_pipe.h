@@ -120,9 +120,10 @@ __device__ __forceinline__ Tile decode_tile(const FfnArgs& a, int L, int per_spl
 // (S a power of two, S | nk, S * tail <= cap), one unit per idle workgroup,
 // whose fp32 partial tiles a fix-up pass sums. Items [0, n_full) run whole;
 // unit u < n_units is k-part u % S of item n_full + u / S. S minimises
-// 7 * nk / S + S * tail: a K-step of a 256x256 tile costs about seven times
-// what one unit's partial tile costs to write and read back through HBM (so a
-// short K or a wide tail keeps the item whole). cap = 0 disables the split.
+// 14 * nk / S + S * tail: a 64-k step of a 256x256 tile costs about fourteen
+// times what one unit's partial tile costs to write and read back through HBM
+// (so a short K or a wide tail keeps the item whole). cap = 0 disables the
+// split.
 struct WorkSplit {
   int n_full, n_units, S;
 };
@@ -132,9 +133,9 @@ __device__ __forceinline__ WorkSplit work_split(int n_work, int G, int nk, int c
   const int R = G > 0 ? n_work / G : 0, tail = n_work - R * G;
   if (cap <= 0 || tail == 0) return w;
   cap = min(cap, G);
-  int best = 7 * nk;
+  int best = 14 * nk;
   for (int s = 2; s <= 16 && s * tail <= cap && nk % s == 0; s *= 2) {
-    const int c = 7 * nk / s + s * tail;
+    const int c = 14 * nk / s + s * tail;
     if (c < best) {
       best = c;
       w.S = s;

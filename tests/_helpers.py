@@ -71,9 +71,9 @@ def tail_split(n_work: int, G: int, nk: int, cap: int) -> Tuple[int, int, int]:
     if cap <= 0 or tail == 0:
         return n_work, 0, 1
     cap = min(cap, G)
-    best, S, s = 7 * nk, 1, 2
+    best, S, s = 14 * nk, 1, 2
     while s <= 16 and s * tail <= cap and nk % s == 0:
-        c = 7 * nk // s + s * tail
+        c = 14 * nk // s + s * tail
         if c < best:
             best, S = c, s
         s *= 2
@@ -87,4 +87,4 @@ def tiled_gate_up_split(plan: _capi.Plan, counts: Sequence[int], cus: int) -> in
     n_wtiles = plan.I // 128
     G = min(n_wtiles * plan.max_tiles, cus)
     cap = plan.down_splits * plan.rows * plan.H * 4 // (256 * 256 * 4)
-    return tail_split(n_wtiles * n_t, G, plan.H // 32, min(cap, 4096))[2]
+    return tail_split(n_wtiles * n_t, G, plan.H // 64, min(cap, 4096))[2]

@@ -30,14 +30,15 @@ def test_version_and_constants():
 
 @pytest.mark.parametrize("T,H,I,E,K,dtype,path", [
     (4096, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
-    (256, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_MEDIUM),
+    (256, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
+    (128, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_MEDIUM),
     (16, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_SKINNY),
     (1, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_SKINNY),
     (2048, 4096, 6400, 16, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
     (8, 2048, 1408, 64, 6, _capi.BF16, _capi.PATH_MFMA_SKINNY),
     (4096, 2048, 1408, 64, 6, _capi.BF16, _capi.PATH_MFMA_TILED),
     (512, 1024, 2816, 8, 2, _capi.F32, _capi.PATH_SIMT),
-    (256, 1024, 2816, 8, 2, _capi.F16, _capi.PATH_MFMA_MEDIUM),
+    (128, 1024, 2816, 8, 2, _capi.F16, _capi.PATH_MFMA_MEDIUM),
     (512, 1024, 2816, 8, 2, _capi.F16, _capi.PATH_MFMA_TILED),
 ])
 def test_plan_paths_and_layout(T, H, I, E, K, dtype, path):
@@ -56,7 +57,7 @@ def test_plan_paths_and_layout(T, H, I, E, K, dtype, path):
 
 @pytest.mark.parametrize("T,K,E,tile,path", [(4096, 2, 8, 256, -1), (16, 2, 8, 16, -1),
                                              (8, 6, 64, 16, -1), (333, 3, 7, 64, -1),
-                                             (256, 2, 8, 64, -1), (777, 2, 5, 64, 3)])
+                                             (128, 2, 8, 64, -1), (777, 2, 5, 64, 3)])
 def test_tile_map_capacity_bounds_every_routing(T, K, E, tile, path):
     dtype = _capi.F32 if (tile == 64 and path < 0 and T == 333) else _capi.BF16
     H, I = (256, 256) if tile != 16 else (256, 128)

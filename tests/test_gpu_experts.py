@@ -81,9 +81,9 @@ CASES = [
     ("decode_t16", 16, 2, 8, 1024, 2048, "bf16", _capi.PATH_MFMA_SKINNY),
     ("decode_f16", 8, 2, 8, 512, 512, "f16", _capi.PATH_MFMA_SKINNY),
     ("finegrained_t8", 8, 6, 64, 256, 128, "bf16", _capi.PATH_MFMA_SKINNY),
-    ("medium_ragged", 350, 2, 8, 512, 384, "bf16", _capi.PATH_MFMA_MEDIUM),
-    ("medium_f16", 150, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_MEDIUM),
-    ("medium_e16", 600, 2, 16, 512, 256, "bf16", _capi.PATH_MFMA_MEDIUM),
+    ("medium_ragged", 150, 2, 8, 512, 384, "bf16", _capi.PATH_MFMA_MEDIUM),
+    ("medium_f16", 80, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_MEDIUM),
+    ("medium_e16", 300, 2, 16, 512, 256, "bf16", _capi.PATH_MFMA_MEDIUM),
     ("prefill_ragged", 700, 2, 8, 512, 384, "bf16", _capi.PATH_MFMA_TILED),
     ("prefill_tiled", 1200, 2, 4, 512, 384, "bf16", _capi.PATH_MFMA_TILED),
     ("prefill_f16", 1000, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_TILED),
