@@ -118,11 +118,15 @@ __device__ __forceinline__ float transpose_reduce(float (&v)[V], int lane) {
     const int d = 32 >> r;
     const int n = (V >> r) > 1 ? (V >> r) : 1;
     if (n > 1) {
-      const bool up = (lane & d) != 0;
+      // Bitwise select on the values: a lane-dependent `up ? v[i] : v[j]`
+      // can be folded into a per-lane array index, which sends the whole
+      // array to scratch memory.
+      const uint32_t m = (lane & d) != 0 ? 0xffffffffu : 0u;
 #pragma unroll
       for (int i = 0; i < n / 2; ++i) {
-        const float send = up ? v[i] : v[i + n / 2];
-        const float keep = up ? v[i + n / 2] : v[i];
+        const uint32_t lo = __float_as_uint(v[i]), hi = __float_as_uint(v[i + n / 2]);
+        const float send = __uint_as_float((lo & m) | (hi & ~m));
+        const float keep = __uint_as_float((hi & m) | (lo & ~m));
         v[i] = keep + __shfl_xor(send, d, kWave);
       }
     } else {
@@ -159,20 +163,34 @@ __global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
     float acc[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) acc[i] = 0.f;
-    for (int c = tid; c < nch; c += kThreads) {
-      float xf[TB][V];
+    // U chunks per thread per pass (two for the one-token kernel, whose
+    // registers allow it): every load of the pass is issued before any is used
+    // (rows past the last token or expert, and chunks past the row end, are
+    // clamped in bounds and their products dropped), so the U * (TB + 8) loads
+    // are in flight together instead of one HBM round trip each.
+    constexpr int U = TB == 1 ? 2 : 1;
+    for (int c0 = tid; c0 < nch; c0 += U * kThreads) {
+      u32x4 xraw[U][TB], graw[U][kExpGroup];
 #pragma unroll
-      for (int t = 0; t < TB; ++t) {
-        const u32x4 raw = t < ntok ? *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(t) * a.H + c * V)
-                                   : u32x4{0, 0, 0, 0};
-        Vec16<T>::unpack(raw, xf[t]);
+      for (int u = 0; u < U; ++u) {
+        const int c = min(c0 + u * kThreads, nch - 1);
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
+          xraw[u][t] = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(min(t, ntok - 1)) * a.H + c * V);
+#pragma unroll
+        for (int j = 0; j < kExpGroup; ++j)
+          graw[u][j] = *reinterpret_cast<const u32x4*>(gate + static_cast<size_t>(min(e0 + j, a.E - 1)) * a.H + c * V);
       }
 #pragma unroll
-      for (int j = 0; j < kExpGroup; ++j) {
-        const int e = e0 + j;
-        if (e < a.E) {
+      for (int u = 0; u < U; ++u) {
+        if (c0 + u * kThreads >= nch) break;
+        float xf[TB][V];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) Vec16<T>::unpack(xraw[u][t], xf[t]);
+#pragma unroll
+        for (int j = 0; j < kExpGroup; ++j) {
           float gf[V];
-          Vec16<T>::unpack(*reinterpret_cast<const u32x4*>(gate + static_cast<size_t>(e) * a.H + c * V), gf);
+          Vec16<T>::unpack(graw[u][j], gf);
 #pragma unroll
           for (int t = 0; t < TB; ++t)
 #pragma unroll
