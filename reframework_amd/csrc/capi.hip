@@ -230,6 +230,8 @@ int moe355_add_rmsnorm(const void* x, const void* residual, void* residual_out,
   if (!aligned16(x) || !aligned16(normed_out) || (residual && !aligned16(residual)) ||
       (residual && !aligned16(residual_out)))
     return fail(MOE355_EINVAL, "x/residual/out not 16-byte aligned");
+  if (!aligned16(weight) || (bias && !aligned16(bias)))
+    return fail(MOE355_EINVAL, "norm weight/bias not 16-byte aligned");
   NormArgs a{};
   a.x = x; a.residual = residual; a.residual_out = residual_out; a.weight = weight;
   a.bias = bias; a.out = normed_out;
