@@ -89,16 +89,46 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
     }
   }
   __syncthreads();
-  if (tid == 0) {
-    int acc = 0, tacc = 0;
-    for (int e = 0; e < a.E; ++e) {
-      start[e] = acc;
-      tile_start[e] = tacc;
-      acc += total[e];
-      tacc += (total[e] + a.tile_rows - 1) / a.tile_rows;
+  if (wave == 0) {
+    // Exclusive scans of the expert row counts and tile counts by one wave:
+    // lane l owns experts l*per .. l*per+per-1 (per <= 4 for E <= 256).
+    constexpr int kPer = kMaxExperts / kWave;
+    const int per = (a.E + kWave - 1) / kWave;
+    int cnt[kPer], tl[kPer];
+    int sc = 0, st = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = lane * per + i;
+      const bool own = i < per && e < a.E;
+      cnt[i] = own ? total[e] : 0;
+      tl[i] = (cnt[i] + a.tile_rows - 1) / a.tile_rows;
+      sc += cnt[i];
+      st += tl[i];
     }
-    start[a.E] = acc;
-    tile_start[a.E] = tacc < a.max_tiles ? tacc : a.max_tiles;
+    int ic = sc, it = st;  // inclusive scans across lanes
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int vc = __shfl_up(ic, o, kWave), vt = __shfl_up(it, o, kWave);
+      if (lane >= o) {
+        ic += vc;
+        it += vt;
+      }
+    }
+    int ec = ic - sc, et = it - st;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = lane * per + i;
+      if (i < per && e < a.E) {
+        start[e] = ec;
+        tile_start[e] = et;
+      }
+      ec += cnt[i];
+      et += tl[i];
+    }
+    if (lane == kWave - 1) {
+      start[a.E] = ic;
+      tile_start[a.E] = it < a.max_tiles ? it : a.max_tiles;
+    }
   }
   __syncthreads();
   for (int e = tid; e < a.E; e += kThreads) base[e] += start[e];
@@ -122,7 +152,8 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
   }
 
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
-  for (int r = 0; r < kRounds; ++r) {
+  // Rounds past the last routed slot have nothing to rank.
+  for (int r = 0; r < kRounds && b * kPermuteChunk + r * kThreads < a.R; ++r) {
     for (int i = tid; i < kWaves * a.E; i += kThreads) wave_cnt[i / a.E][i % a.E] = 0;
     __syncthreads();
     const int slot = b * kPermuteChunk + r * kThreads + tid;

@@ -14,7 +14,6 @@ namespace moe355 {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kExpGroup = 8;   // experts accumulated per pass over the row
 constexpr int kMaxPerLane = kMaxExperts / kWave;
 
 // Softmax + top-k + renormalisation of one token's logits by one wave.
@@ -139,13 +138,14 @@ __device__ __forceinline__ float transpose_reduce(float (&v)[V], int lane) {
 constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
 
 // TB tokens per workgroup share every gate-row load (the gate matrix is read
-// once per TB tokens from L2). Per thread: TB x 8 partial dot products over its
-// slice of H, folded across the wave by transpose_reduce and across the 4
-// waves through LDS.
-template <typename T, int TB>
+// once per TB tokens from L2). Per thread: TB x EG partial dot products (EG
+// experts per pass over the row) over its slice of H, folded across the wave
+// by transpose_reduce and across the 4 waves through LDS.
+template <typename T, int TB, int EG>
 __global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
   constexpr int V = Vec16<T>::N;
-  constexpr int NV = TB * kExpGroup;     // partial sums per thread (<= 64)
+  constexpr int NV = TB * EG;            // partial sums per thread (<= 64)
+  static_assert(NV <= 64, "one value per lane after the transposed reduction");
   constexpr int SH = 6 - log2i(NV);      // lane bits below the value index
   __shared__ float part[kThreads / kWave][64];
   __shared__ float lg[TB][kMaxExperts];
@@ -159,18 +159,18 @@ __global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
   const T* x = static_cast<const T*>(a.x) + static_cast<size_t>(t0) * a.H;
   const T* gate = static_cast<const T*>(a.gate);
 
-  for (int e0 = 0; e0 < a.E; e0 += kExpGroup) {
+  for (int e0 = 0; e0 < a.E; e0 += EG) {
     float acc[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) acc[i] = 0.f;
-    // U chunks per thread per pass (two for the one-token kernel, whose
+    // U chunks per thread per pass (two for one token and 8 experts, whose
     // registers allow it): every load of the pass is issued before any is used
     // (rows past the last token or expert, and chunks past the row end, are
-    // clamped in bounds and their products dropped), so the U * (TB + 8) loads
-    // are in flight together instead of one HBM round trip each.
-    constexpr int U = TB == 1 ? 2 : 1;
+    // clamped in bounds and their products dropped), so the U * (TB + EG)
+    // loads are in flight together instead of one HBM round trip each.
+    constexpr int U = TB == 1 && EG == 8 ? 2 : 1;
     for (int c0 = tid; c0 < nch; c0 += U * kThreads) {
-      u32x4 xraw[U][TB], graw[U][kExpGroup];
+      u32x4 xraw[U][TB], graw[U][EG];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c = min(c0 + u * kThreads, nch - 1);
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
         for (int t = 0; t < TB; ++t)
           xraw[u][t] = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(min(t, ntok - 1)) * a.H + c * V);
 #pragma unroll
-        for (int j = 0; j < kExpGroup; ++j)
+        for (int j = 0; j < EG; ++j)
           graw[u][j] = *reinterpret_cast<const u32x4*>(gate + static_cast<size_t>(min(e0 + j, a.E - 1)) * a.H + c * V);
       }
 #pragma unroll
@@ -188,13 +188,13 @@ __global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
 #pragma unroll
         for (int t = 0; t < TB; ++t) Vec16<T>::unpack(xraw[u][t], xf[t]);
 #pragma unroll
-        for (int j = 0; j < kExpGroup; ++j) {
+        for (int j = 0; j < EG; ++j) {
           float gf[V];
           Vec16<T>::unpack(graw[u][j], gf);
 #pragma unroll
           for (int t = 0; t < TB; ++t)
 #pragma unroll
-            for (int q = 0; q < V; ++q) acc[t * kExpGroup + j] = fmaf(xf[t][q], gf[q], acc[t * kExpGroup + j]);
+            for (int q = 0; q < V; ++q) acc[t * EG + j] = fmaf(xf[t][q], gf[q], acc[t * EG + j]);
         }
       }
     }
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
     if ((lane & ((1 << SH) - 1)) == 0) part[wave][lane >> SH] = r;
     __syncthreads();
     for (int i = tid; i < NV; i += kThreads) {
-      const int t = i / kExpGroup, e = e0 + i % kExpGroup;
+      const int t = i / EG, e = e0 + i % EG;
       if (t < ntok && e < a.E) {
         float l = (part[0][i] + part[1][i]) + (part[2][i] + part[3][i]);
         if (a.round_logits) l = to_f32(from_f32<T>(l));
@@ -236,13 +236,22 @@ __global__ __launch_bounds__(kThreads) void topk_logits_kernel(const RouterArgs 
 
 template <typename T>
 hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
+  // Experts per pass over the row: as many as the 64 per-thread sums allow
+  // for the workgroup's token count, so E = 64 at one token costs two passes
+  // (two memory round trips) rather than eight.
   const dim3 block(kThreads);
   if (a.T >= 1024)
-    router_kernel<T, 8><<<dim3((a.T + 7) / 8), block, 0, s>>>(a);
+    router_kernel<T, 8, 8><<<dim3((a.T + 7) / 8), block, 0, s>>>(a);
+  else if (a.T >= 256 && a.E > 8)
+    router_kernel<T, 4, 16><<<dim3((a.T + 3) / 4), block, 0, s>>>(a);
   else if (a.T >= 256)
-    router_kernel<T, 4><<<dim3((a.T + 3) / 4), block, 0, s>>>(a);
+    router_kernel<T, 4, 8><<<dim3((a.T + 3) / 4), block, 0, s>>>(a);
+  else if (a.E > 16)
+    router_kernel<T, 1, 32><<<dim3(a.T), block, 0, s>>>(a);
+  else if (a.E > 8)
+    router_kernel<T, 1, 16><<<dim3(a.T), block, 0, s>>>(a);
   else
-    router_kernel<T, 1><<<dim3(a.T), block, 0, s>>>(a);
+    router_kernel<T, 1, 8><<<dim3(a.T), block, 0, s>>>(a);
   return hipGetLastError();
 }
 

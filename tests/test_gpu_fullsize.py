@@ -132,3 +132,25 @@ def test_mixtral_prefill_t4096_sampled_tokens(dev):
     w = rng.random((T, K)).astype(np.float32)
     out = gpu_fused(x, w1, w2, w, ids)
     _check_sampled(out, x, w1, w2, w, ids, _sample_tokens(ids, 6, seed=5))
+
+
+def test_mixtral_t256_sampled_tokens(dev):
+    """Mixtral-8x7B layer, T=256 (~64 rows per expert): the automatic plan
+    takes the 256-row kernel with an 8-way K-split down projection, and the
+    112 x 8 gate_up items leave a 128-item last round that is cut along K."""
+    T, H, I, E, K = 256, 4096, 14336, 8, 2
+    rng = np.random.default_rng(17)
+    ids = np.argsort(rng.random((T, E)), axis=1)[:, :K].astype(np.int64)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    plan = _capi.make_plan(T, H, I, E, K, _capi.BF16)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    S = tiled_gate_up_split(plan, counts, cus)
+    banner(f"mixtral T={T} path={plan.path} down_splits={plan.down_splits} gate_up tail S={S}")
+    assert plan.path == _capi.PATH_MFMA_TILED
+    if cus == 256:
+        assert S == 2 and plan.down_splits == 8
+    w1, w2 = _bank(E, H, I, torch.bfloat16, seed=19, dev=dev, scale=0.02)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    w = rng.random((T, K)).astype(np.float32)
+    out = gpu_fused(x, w1, w2, w, ids)
+    _check_sampled(out, x, w1, w2, w, ids, _sample_tokens(ids, 8, seed=6))
