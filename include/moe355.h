@@ -103,6 +103,18 @@ int moe355_router_topk(const void* x, const void* gate, const float* bias, int T
                        float* logits_out, float* topk_w, int32_t* topk_ids, void* stream);
 
 /*
+ * moe355_router_topk writing token t's K weights and ids at row t of [T, out_ld]
+ * arrays (out_ld >= K; columns K.. are left untouched). The same replacement of
+ * FusedMoE.route (reframework/moe/moe_layer.py:320-344); the stride lets the
+ * routed ids land beside constant columns, e.g. the always-on shared experts
+ * folded in as extra experts with weight 1 (which the reference does not have).
+ */
+int moe355_router_topk_ld(const void* x, const void* gate, const float* bias, int T, int H, int E,
+                          int K, int dtype, int renormalize, int round_logits, int entropy_k_min,
+                          float* logits_out, float* topk_w, int32_t* topk_ids, int out_ld,
+                          void* stream);
+
+/*
  * residual_out = x + residual (rounded to `dtype`; residual_out may alias x or
  * residual), then normed = residual_out / sqrt(mean(residual_out^2) + eps) *
  * weight (+ bias), in fp32, rounded once. With residual == NULL: normed =

@@ -71,6 +71,8 @@ _SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "moe355_version": (_I, []),
     "moe355_last_error": (ctypes.c_char_p, []),
     "moe355_router_topk": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "moe355_router_topk_ld": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _I,
+                                   _P]),
     "moe355_topk_from_logits": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "moe355_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _I, ctypes.c_float, _I, _I, _I, _P, _P]),
     "moe355_add_rmsnorm_router_topk": (_I, [_P, _P, _P, _P, _P, _I, ctypes.c_float, _P, _P, _I,
@@ -175,12 +177,18 @@ def router_topk(x: torch.Tensor, gate: torch.Tensor, bias: Optional[torch.Tensor
                 renormalize: bool, round_logits: bool, entropy_k_min: int,
                 topk_w: torch.Tensor, topk_ids: torch.Tensor,
                 logits_out: Optional[torch.Tensor] = None, stream: Optional[int] = None) -> None:
+    """Routes x into topk_w / topk_ids of shape [T, ld] (ld >= K, row-major):
+    the first K columns of each row; columns K.. are left as they are."""
     T, H = x.shape
     E = gate.shape[0]
+    ld = topk_w.shape[1] if topk_w.dim() == 2 else K
+    if topk_ids.dim() == 2 and topk_ids.shape[1] != ld:
+        raise ValueError(f"topk_w and topk_ids rows differ: {ld} vs {topk_ids.shape[1]}")
     s = stream if stream is not None else stream_handle(x.device)
-    _check("moe355_router_topk", lib().moe355_router_topk(
+    _check("moe355_router_topk_ld", lib().moe355_router_topk_ld(
         _ptr(x), _ptr(gate), _ptr(bias), T, H, E, K, dtype_code(x.dtype), int(renormalize),
-        int(round_logits), int(entropy_k_min), _ptr(logits_out), _ptr(topk_w), _ptr(topk_ids), s))
+        int(round_logits), int(entropy_k_min), _ptr(logits_out), _ptr(topk_w), _ptr(topk_ids), ld,
+        s))
 
 
 def topk_from_logits(logits: torch.Tensor, K: int, renormalize: bool, topk_w: torch.Tensor,

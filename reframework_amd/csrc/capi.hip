@@ -192,6 +192,14 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
 int moe355_router_topk(const void* x, const void* gate, const float* bias, int T, int H, int E,
                        int K, int dtype, int renormalize, int round_logits, int entropy_k_min,
                        float* logits_out, float* topk_w, int32_t* topk_ids, void* stream) {
+  return moe355_router_topk_ld(x, gate, bias, T, H, E, K, dtype, renormalize, round_logits,
+                               entropy_k_min, logits_out, topk_w, topk_ids, K, stream);
+}
+
+int moe355_router_topk_ld(const void* x, const void* gate, const float* bias, int T, int H, int E,
+                          int K, int dtype, int renormalize, int round_logits, int entropy_k_min,
+                          float* logits_out, float* topk_w, int32_t* topk_ids, int out_ld,
+                          void* stream) {
   if (T < 0 || H <= 0) return fail(MOE355_EINVAL, "bad sizes T=%d H=%d", T, H);
   if (E < 1 || E > MOE355_MAX_EXPERTS)
     return fail(MOE355_EUNSUPPORTED, "E=%d outside [1, %d]", E, MOE355_MAX_EXPERTS);
@@ -199,6 +207,7 @@ int moe355_router_topk(const void* x, const void* gate, const float* bias, int T
   if (!valid_dtype(dtype)) return fail(MOE355_EINVAL, "unknown dtype %d", dtype);
   if (entropy_k_min < 0 || entropy_k_min > K)
     return fail(MOE355_EINVAL, "entropy_k_min=%d outside [0, K=%d]", entropy_k_min, K);
+  if (out_ld < K) return fail(MOE355_EINVAL, "output row stride %d < K=%d", out_ld, K);
   const int vec = 16 / elem_size(dtype);
   if (H % vec) return fail(MOE355_EUNSUPPORTED, "router needs H %% %d == 0", vec);
   if (T == 0) return MOE355_OK;
@@ -209,7 +218,7 @@ int moe355_router_topk(const void* x, const void* gate, const float* bias, int T
   a.topk_w = topk_w; a.topk_ids = topk_ids;
   a.T = T; a.H = H; a.E = E; a.K = K;
   a.renormalize = renormalize != 0; a.round_logits = round_logits != 0;
-  a.entropy_k_min = entropy_k_min;
+  a.entropy_k_min = entropy_k_min; a.out_ld = out_ld;
   return check_hip(launch_router(a, dtype, as_stream(stream)), "router_topk launch");
 }
 

@@ -178,6 +178,7 @@ struct RouterArgs {
   int32_t* topk_ids;    // [T,K]
   int T, H, E, K;
   int renormalize, round_logits, entropy_k_min;
+  int out_ld;           // row stride of topk_w / topk_ids (>= K)
 };
 
 struct PermuteArgs {

@@ -216,8 +216,8 @@ __global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
 
   for (int t = wave; t < ntok; t += kThreads / kWave)
     wave_topk(lg[t], a.E, a.K, a.renormalize, a.entropy_k_min, psel[wave], isel[wave],
-              a.topk_w + static_cast<size_t>(t0 + t) * a.K,
-              a.topk_ids + static_cast<size_t>(t0 + t) * a.K, lane);
+              a.topk_w + static_cast<size_t>(t0 + t) * a.out_ld,
+              a.topk_ids + static_cast<size_t>(t0 + t) * a.out_ld, lane);
 }
 
 // One wave per token on given fp32 logits.

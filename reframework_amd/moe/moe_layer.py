@@ -135,7 +135,7 @@ class FusedMoE(BaseOP):
             for _ in range(n_pieces)
         ])
         self._checked_tables: set = set()
-        self._shared_cols = None  # cached (key, shared expert ids [T,n], unit weights [T,n])
+        self._shared_cols = None  # cached (key, weights [T,K+n], ids [T,K+n]); see _route32
         self._cache: Optional[ExpertOffloadCache] = None
         self._cpu_split_enabled: bool = False
         self._predictor: Optional[Prediction] = None
@@ -229,16 +229,33 @@ class FusedMoE(BaseOP):
         return 0.0 if prev is None else max(0.0, (t - prev) * 1000.0)
 
     # ----------------------------------------------------------------- routing
-    def _route32(self, xd: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    def _route32(self, xd: torch.Tensor,
+                 with_shared_cols: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
         """Router kernel on ``xd`` ([T,H], model dtype, contiguous, on GPU):
-        (weights fp32 [T,K], ids int32 [T,K])."""
+        (weights fp32 [T,K], ids int32 [T,K]). With ``with_shared_cols`` (the
+        shared experts folded in as extra experts) the router writes into
+        [T, K+n] buffers whose last n columns already hold the shared ids E..
+        with weight 1, so no concatenation follows; the buffers are cached per
+        token count and stream, and reused by the next forward on that stream."""
         gate = self.gate.detach()
         if gate.device != xd.device:
             gate = gate.to(xd.device)
         gate = gate.to(self.dtype).contiguous()
         T = xd.shape[0]
-        w = torch.empty((T, self.top_k), dtype=torch.float32, device=xd.device)
-        ids = torch.empty((T, self.top_k), dtype=torch.int32, device=xd.device)
+        if with_shared_cols:
+            n = len(self.shared_w1)
+            # one pair per stream: forwards on different streams must not share
+            key = (T, n, xd.device, _capi.stream_handle(xd.device))
+            if self._shared_cols is None or self._shared_cols[0] != key:
+                ids = torch.empty((T, self.top_k + n), dtype=torch.int32, device=xd.device)
+                ids[:, self.top_k:] = torch.arange(self.num_experts, self.num_experts + n,
+                                                   dtype=torch.int32, device=xd.device)
+                w = torch.ones((T, self.top_k + n), dtype=torch.float32, device=xd.device)
+                self._shared_cols = (key, w, ids)
+            _, w, ids = self._shared_cols
+        else:
+            w = torch.empty((T, self.top_k), dtype=torch.float32, device=xd.device)
+            ids = torch.empty((T, self.top_k), dtype=torch.int32, device=xd.device)
         kmin = 0
         if self.entropy_adaptive_k:
             if self.entropy_k_min < 1:
@@ -305,15 +322,14 @@ class FusedMoE(BaseOP):
         s1, s2 = self._pointers(self.shared_w1, self.shared_w2)
         T, n = xd.shape[0], len(s1)
         if self._shared_folded:
-            key = (T, n, ids.dtype, ids.device)
-            if self._shared_cols is None or self._shared_cols[0] != key:
+            if ids.shape[1] == self.top_k + n:
+                ids2, w2_ = ids, w  # routed with the shared columns (_route32)
+            else:
                 ids_x = torch.arange(self.num_experts, self.num_experts + n, dtype=ids.dtype,
                                      device=ids.device).expand(T, n)
-                self._shared_cols = (key, ids_x, torch.ones((T, n), dtype=torch.float32,
-                                                            device=ids.device))
-            _, ids_x, ones = self._shared_cols
-            ids2 = torch.cat([ids, ids_x], dim=1)
-            w2_ = torch.cat([w, ones], dim=1)
+                ids2 = torch.cat([ids, ids_x], dim=1)
+                w2_ = torch.cat([w, torch.ones((T, n), dtype=torch.float32, device=ids.device)],
+                                dim=1)
             base = len(w1p)
             if expert_map is None:
                 emap = None if base == self.num_experts else \
@@ -343,7 +359,9 @@ class FusedMoE(BaseOP):
         x2 = x.reshape(-1, self.hidden_size)
         require_gpu(x2)
         xd = x2.to(self.dtype).contiguous()
-        w, ids = self._route32(xd)
+        # resident layer with folded shared experts: route straight into the
+        # [T, K+n] arrays the expert call takes
+        w, ids = self._route32(xd, with_shared_cols=not self.uses_offload and self._shared_folded)
         act = activation_code(self.activation)
 
         if self.uses_offload and env.get_chunk_size(0) > 0:

@@ -96,6 +96,9 @@ def test_entry_points_reject_null_arguments_without_launching():
     assert rc == -1 and "NULL" in lib.moe355_last_error().decode()
     rc = lib.moe355_topk_from_logits(None, 3, 8, 2, 1, None, None, None)
     assert rc == -1
+    rc = lib.moe355_router_topk_ld(None, None, None, 2, 64, 8, 2, _capi.BF16, 1, 0, 0, None, None,
+                                   None, 1, None)
+    assert rc == -1 and "stride" in lib.moe355_last_error().decode()
     p = _capi.make_plan(4, 256, 256, 8, 2, _capi.BF16)
     assert lib.moe355_permute(ctypes.byref(p), None, 0, None, 0, None, None) == -1
     assert lib.moe355_gate_up(ctypes.byref(p), None, None, 0, None, None) == -1

@@ -66,7 +66,10 @@ def _router(x, gate, bias, K, renorm, round_logits, kmin=0):
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("T,H,E,K", [(1, 4096, 8, 2), (77, 4096, 8, 2), (64, 2048, 64, 6),
-                                     (33, 1024, 16, 2), (5, 8192, 256, 8)])
+                                     (33, 1024, 16, 2), (5, 8192, 256, 8),
+                                     # 4 and 8 tokens per workgroup, 8 or 16 experts per pass
+                                     (300, 4096, 8, 2), (300, 2048, 64, 6), (1100, 1024, 8, 2),
+                                     (1100, 512, 64, 6)])
 def test_router_topk(dtype, T, H, E, K, dev):
     banner(f"router dtype={dtype} T={T} H={H} E={E} K={K}")
     dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
@@ -128,3 +131,20 @@ def test_router_rejects_bad_arguments(dev):
         _capi.router_topk(x, gate, None, 9, True, False, 0, w, ids)
     with pytest.raises(_capi.MoeLibError, match="entropy_k_min"):
         _capi.router_topk(x, gate, None, 2, True, False, 3, w, ids)
+
+
+@pytest.mark.parametrize("T,E,K,n", [(1, 64, 6, 2), (300, 8, 2, 1), (1100, 16, 2, 3)])
+def test_router_strided_output(T, E, K, n, dev):
+    """moe355_router_topk_ld: token t's K results land at row t of [T, K+n]
+    arrays, bit-equal to the unstrided router; columns K.. keep their values."""
+    g = torch.Generator().manual_seed(T + E)
+    x = torch.randn(T, 1024, generator=g).to(torch.bfloat16).to(dev)
+    gate = (torch.randn(E, 1024, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    w0, ids0, _ = _router(x, gate, None, K, True, True)
+    w = torch.full((T, K + n), -7.0, dtype=torch.float32, device=dev)
+    ids = torch.full((T, K + n), -9, dtype=torch.int32, device=dev)
+    _capi.router_topk(x, gate, None, K, True, True, 0, w, ids)
+    torch.cuda.synchronize()
+    w, ids = w.cpu().numpy(), ids.cpu().numpy()
+    assert np.array_equal(ids[:, :K], ids0) and np.array_equal(w[:, :K], w0)
+    assert (ids[:, K:] == -9).all() and (w[:, K:] == -7.0).all()
