@@ -205,7 +205,7 @@ struct FfnArgs {
   float* part;             // tiled gate_up: tail-split partial tiles, part_units x 256 KB
   int part_units;          // capacity of part in 256x256 fp32 tiles (0: no tail split)
   int grid;                // workgroups of the tiled launch (the fix-up recomputes its split)
-  int group_t;             // token tiles per item group (0: all; see decode_tile)
+  int group_t;             // token tiles per item group (0: all; -1: one group per expert; see decode_tile)
   const void* w[kMaxExperts];  // w1[e] ([2I,H]) or w2[e] ([H,I])
 };
 

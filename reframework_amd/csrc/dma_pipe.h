@@ -100,6 +100,24 @@ __device__ __forceinline__ Tile decode_tile(const FfnArgs& a, int L, int per_spl
   Tile t;
   t.split = L / per_split;
   const int rem = L - t.split * per_split;
+  if (a.group_t < 0) {
+    // One group per expert: its token tiles x all weight tiles, the token tile
+    // varying fastest. The group of item rem starts at the first tile b of the
+    // expert owning tile rem / n_wtiles (tiles of an expert are consecutive
+    // and tile_rows apart, so b follows from that tile's first row).
+    const int t0 = rem / a.n_wtiles;
+    const int e = tile_map[2 + 2 * t0];
+    const int eb = offsets[e], ee = offsets[e + 1];
+    const int b = t0 - (tile_map[3 + 2 * t0] - eb) / tile_rows;
+    const int ne = (ee - eb + tile_rows - 1) / tile_rows;
+    const int r2 = rem - b * a.n_wtiles;
+    t.wtile = r2 / ne;
+    const int tt = b + (r2 - t.wtile * ne);
+    t.e = e;
+    t.row0 = tile_map[3 + 2 * tt];
+    t.row_end = min(t.row0 + tile_rows, ee);
+    return t;
+  }
   // Items come in groups of gt token tiles x all weight tiles, the token tile
   // varying fastest inside a group; the last group may hold fewer token tiles.
   const int gfull = a.group_t > 0 ? a.group_t : n_t;
