@@ -76,6 +76,8 @@ typedef struct moe355_plan {
   size_t off_tile_map;     /* int32 [2 + 2*max_tiles]: count, 0, then (expert, first_row) pairs */
   size_t off_inter;        /* dtype [T*K, I] silu(gate)*up per permuted row */
   size_t off_y;            /* fp32  [down_splits, T*K, H] down-projection partials */
+  size_t off_part;         /* fp32 256x256 partial tiles of the tiled down projection's K-split
+                              last-round items, up to one per CU (empty for the other paths) */
 } moe355_plan;
 
 /* Library version (major*10000 + minor*100 + patch). */

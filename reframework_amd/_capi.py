@@ -58,6 +58,7 @@ class Plan(ctypes.Structure):
         ("off_tile_map", ctypes.c_size_t),
         ("off_inter", ctypes.c_size_t),
         ("off_y", ctypes.c_size_t),
+        ("off_part", ctypes.c_size_t),
     ]
 
 

@@ -119,8 +119,11 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
   const long long avg = R / act_e;
 
   const bool mfma = dtype != MOE355_F32;
+  // Token rows are addressed by 32-bit byte offsets whose bit 31 marks tile
+  // padding (loaded as zeros), so x must stay below 2 GB; weight offsets are
+  // 32-bit too.
   const bool tiled_ok = mfma && H % 256 == 0 && I % 128 == 0 &&
-                        static_cast<long long>(T) * H * esz < (1ll << 32) &&
+                        static_cast<long long>(T) * H * esz < (1ll << 31) &&
                         2ll * I * H * esz < (1ll << 32);
   const bool skinny_ok = mfma && H % 128 == 0 && I % 128 == 0;
   if (path < 0) {
@@ -185,6 +188,14 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
   p->off_tile_map = off;     off = align256(off + static_cast<size_t>(2 + 2 * p->max_tiles) * 4);
   p->off_inter = off;        off = align256(off + static_cast<size_t>(R) * I * esz);
   p->off_y = off;            off = align256(off + static_cast<size_t>(p->down_splits) * R * H * 4);
+  p->off_part = off;
+  if (p->path == MOE355_PATH_MFMA_TILED) {
+    // One 256 KB partial tile per CU at most: the tiled down projection cuts
+    // the items of a last, partly idle round along K over the idle CUs.
+    const long long work = static_cast<long long>(H / 256) * p->max_tiles * p->down_splits;
+    const long long units = std::min<long long>(work, moe355::device_cu_count());
+    off = align256(off + static_cast<size_t>(units) * 256 * 256 * 4);
+  }
   p->workspace_bytes = off;
   return MOE355_OK;
 }
@@ -359,6 +370,11 @@ int moe355_down(const moe355_plan* p, const void* const* w2, void* workspace, vo
   hipError_t err;
   if (p->path == MOE355_PATH_MFMA_TILED) {
     a.n_wtiles = p->H / 256;
+    // Partial tiles of the K-split last-round items (256x256 fp32 each).
+    a.part = at<float>(workspace, p->off_part);
+    a.part_units = p->workspace_bytes > p->off_part
+                       ? static_cast<int>((p->workspace_bytes - p->off_part) / (256 * 256 * 4))
+                       : 0;
     err = launch_down_tiled(a, p->dtype, as_stream(stream));
   } else if (p->path == MOE355_PATH_MFMA_MEDIUM) {
     a.n_wtiles = p->H / 256;

@@ -27,10 +27,10 @@
 // one step ahead. Rows are XOR-swizzled in 16-byte chunks (swz8) so the MFMA
 // operand reads are bank-conflict free. The kernel is persistent (one
 // workgroup per CU) and streams its steps across tile boundaries, so each
-// tile's pipeline fill overlaps the previous tile's epilogue. The gate_up
-// items left for a last, mostly idle round are split along K over the idle
-// CUs (work_split); their fp32 partial tiles are summed and activated by
-// gate_up_tail_fixup.
+// tile's pipeline fill overlaps the previous tile's epilogue. The items left
+// for a last, mostly idle round are split along K over the idle CUs
+// (work_split); their fp32 partial tiles are summed (and, for gate_up,
+// activated) by gate_up_tail_fixup / down_tail_fixup.
 #include "dma_pipe.h"
 
 namespace moe355 {
@@ -124,9 +124,9 @@ void ffn_tiled_kernel(const FfnArgs a) {
   const int n_work = a.splits * per_split;
   const int G = gridDim.x;
   const int nk = a.k_per_split / kSK;
-  // Work sequence L0, L0 + G, ...: whole items below ws.n_full, then (gate_up
-  // only) at most one tail unit per workgroup.
-  const WorkSplit ws = work_split(n_work, G, nk, kGateUp ? a.part_units : 0);
+  // Work sequence L0, L0 + G, ...: whole items below ws.n_full, then at most
+  // one tail unit per workgroup.
+  const WorkSplit ws = work_split(n_work, G, nk, a.part_units);
   const int n_seq = ws.n_full + ws.n_units;
   int Lc = xcd_remap(blockIdx.x, G);  // work item being multiplied
   if (Lc >= n_seq) return;
@@ -166,7 +166,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
   // Token cursor: work item xL, step xkt of [.., xke). gate_up token rows come
   // through row_src; they are fetched one item ahead.
   int xL = Lc, xkt = 0, xke = 0;
-  const char* xsrc;
+  __amdgpu_buffer_rsrc_t xsrc;
   uint32_t xoff[kLoadsPerOp];
   int grow[kLoadsPerOp];
   auto fetch_rows = [&](const Tile& t) {
@@ -181,18 +181,28 @@ void ffn_tiled_kernel(const FfnArgs a) {
     xke = w.ke;
     const int ln = opaque(lane);
     const size_t kbeg = static_cast<size_t>(t.split) * a.k_per_split;
+    // Rows past the group's end load zeros: their offsets get bit 31 set
+    // (valid offsets stay below 2^31, so no step of K wraps them back). The
+    // bit is OR-ed into an offset computed for every row alike: a select
+    // between the row offset and a constant became a branch per row, and in
+    // gate_up each branch waited for all loads in flight (the offset depends
+    // on the loaded row_src).
     if (kGateUp) {
-      xsrc = static_cast<const char*>(a.x) + kbeg * 2;
-#pragma unroll
-      for (int q = 0; q < kLoadsPerOp; ++q)
-        xoff[q] = static_cast<uint32_t>(grow[q]) * pitch + swz8(ln & 7, op_row(q, ln)) * 16;
-    } else {
-      xsrc = static_cast<const char*>(a.x) + (static_cast<size_t>(t.row0) * ld + kbeg) * 2;
+      xsrc = lds_rsrc(static_cast<const char*>(a.x) + kbeg * 2);
 #pragma unroll
       for (int q = 0; q < kLoadsPerOp; ++q) {
         const int r = op_row(q, ln);
-        const int xr = min(t.row0 + r, t.row_end - 1) - t.row0;
-        xoff[q] = static_cast<uint32_t>(xr) * pitch + swz8(ln & 7, r) * 16;
+        const uint32_t pad = t.row0 + r < t.row_end ? 0u : kPadOffset;
+        xoff[q] = (static_cast<uint32_t>(grow[q]) * pitch + swz8(ln & 7, r) * 16) | pad;
+      }
+    } else {
+      xsrc = lds_rsrc(static_cast<const char*>(a.x) +
+                      (static_cast<size_t>(t.row0) * ld + kbeg) * 2);
+#pragma unroll
+      for (int q = 0; q < kLoadsPerOp; ++q) {
+        const int r = op_row(q, ln);
+        const uint32_t pad = t.row0 + r < t.row_end ? 0u : kPadOffset;
+        xoff[q] = (static_cast<uint32_t>(r) * pitch + swz8(ln & 7, r) * 16) | pad;
       }
     }
   };
@@ -233,7 +243,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
   auto issue_x = [&](int b, int q0, int n) {
     uint8_t* dst = lds + b * kBufBytes + wave * kLoadsPerOp * 1024;
 #pragma unroll
-    for (int q = q0; q < q0 + n; ++q) dma16(xsrc + xkt * kSRowBytes + xoff[q], dst + q * 1024);
+    for (int q = q0; q < q0 + n; ++q) dma16_rsrc(xsrc, xkt * kSRowBytes + xoff[q], dst + q * 1024);
   };
 
   // MFMA operand rows of this wave inside a buffer.
@@ -369,7 +379,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
     // Epilogue. Lane (lr, kh) of block (i, j) holds, for q = 0..3, features
     // 8q + 4kh + 0..3 of the 32-row weight block and token lr of the token block.
     const int eln = opaque(lane), elr = eln & 31, ekh = eln >> 5;
-    if (kGateUp && cw.unit >= 0) {
+    if (cw.unit >= 0) {
       // K-part of a split tail item: raw fp32 accumulators to its partial slot.
       f32x4* pp = reinterpret_cast<f32x4*>(a.part) +
                   static_cast<size_t>(cw.unit * 4 + wave) * kPartVecsPerWave + eln;
@@ -485,6 +495,39 @@ __global__ __launch_bounds__(kThreads) void gate_up_tail_fixup(const FfnArgs a) 
   }
 }
 
+// Sums the S partial tiles of each split tail item of the tiled down
+// projection into the item's fp32 y plane (its K-split), with the epilogue's
+// lane mapping. Task (item, b, j) covers weight block b against token block j
+// of every wave: 16 KB read per part, 16 KB of y written at most.
+__global__ __launch_bounds__(kThreads) void down_tail_fixup(const FfnArgs a) {
+  const int n_t = a.tile_map[0];
+  const int per_split = a.n_wtiles * n_t;
+  const int nk = a.k_per_split / kSK;
+  const WorkSplit ws = work_split(a.splits * per_split, a.grid, nk, a.part_units);
+  const int tasks = ws.n_units / ws.S * 16;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int wave_w = wave >> 1, wave_t = wave & 1, lr = lane & 31, kh = lane >> 5;
+  for (int task = blockIdx.x; task < tasks; task += gridDim.x) {
+    const int it = task >> 4, b = (task >> 2) & 3, j = task & 3;
+    const Tile t = decode_tile(a, ws.n_full + it, per_split, n_t, kTileT);
+    const int prow = t.row0 + wave_t * 128 + j * 32 + lr;
+    if (prow >= t.row_end) continue;
+    f32x4 v[4] = {};
+    for (int p = 0; p < ws.S; ++p) {
+      const f32x4* pp = reinterpret_cast<const f32x4*>(a.part) +
+                        static_cast<size_t>((it * ws.S + p) * 4 + wave) * kPartVecsPerWave + lane;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] += pp[((b * 4 + j) * 4 + q) * kWave];
+    }
+    float* y = static_cast<float*>(a.out) + static_cast<size_t>(t.split) * a.R * a.H;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int h = t.wtile * kTileW + wave_w * 128 + b * 32 + 8 * q + 4 * kh;
+      store4<float>(y + static_cast<size_t>(prow) * a.H + h, v[q][0], v[q][1], v[q][2], v[q][3]);
+    }
+  }
+}
+
 template <bool kGateUp>
 hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   const long work = static_cast<long>(args.n_wtiles) * args.max_tiles * args.splits;
@@ -499,7 +542,7 @@ hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   // groups of 6 token tiles (which were -7 % on down against no grouping).
   a.group_t = -1;
   a.grid = static_cast<int>(work < device_cu_count() ? work : device_cu_count());
-  if (!kGateUp || !a.part) a.part_units = 0;
+  if (!a.part) a.part_units = 0;
   if (dtype == MOE355_BF16)
     ffn_tiled_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else
@@ -508,7 +551,9 @@ hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   if (err != hipSuccess || a.part_units == 0) return err;
   // The split depends on the device-side tile count; without a tail the
   // fix-up finds no task and exits.
-  if (dtype == MOE355_BF16)
+  if (!kGateUp)
+    down_tail_fixup<<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+  else if (dtype == MOE355_BF16)
     gate_up_tail_fixup<bf16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else
     gate_up_tail_fixup<f16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);

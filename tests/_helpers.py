@@ -63,7 +63,7 @@ def read_ws(plan: _capi.Plan, ws: torch.Tensor, off: int, n: int) -> np.ndarray:
 
 
 def tail_split(n_work: int, G: int, nk: int, cap: int) -> Tuple[int, int, int]:
-    """(n_full, n_units, S) of the tiled gate_up's tail split, as the kernel
+    """(n_full, n_units, S) of the tiled kernels' tail split, as the kernel
     derives it (reframework_amd/csrc/dma_pipe.h, work_split): lets a test
     state which shapes run the K-split tail and its fix-up."""
     R = n_work // G if G > 0 else 0
@@ -78,6 +78,17 @@ def tail_split(n_work: int, G: int, nk: int, cap: int) -> Tuple[int, int, int]:
             best, S = c, s
         s *= 2
     return (R * G, tail * S, S) if S > 1 else (n_work, 0, 1)
+
+
+def tiled_down_split(plan: _capi.Plan, counts: Sequence[int], cus: int) -> int:
+    """S of the tiled down projection's tail split for per-expert row counts
+    `counts` on `cus` CUs (1: no split); its partial tiles live at off_part."""
+    n_t = sum(-(-int(c) // plan.tile_rows) for c in counts)
+    n_wtiles = plan.H // 256
+    G = min(n_wtiles * plan.max_tiles * plan.down_splits, cus)
+    cap = (plan.workspace_bytes - plan.off_part) // (256 * 256 * 4)
+    nk = plan.I // plan.down_splits // 64
+    return tail_split(n_wtiles * n_t * plan.down_splits, G, nk, cap)[2]
 
 
 def tiled_gate_up_split(plan: _capi.Plan, counts: Sequence[int], cus: int) -> int:

@@ -25,7 +25,7 @@ def test_version_and_constants():
     assert _capi.version() == 100
     text = open(_capi.HEADER_PATH).read()
     assert "#define MOE355_MAX_EXPERTS 256" in text
-    assert ctypes.sizeof(_capi.Plan) == 12 * 4 + 8 * 8
+    assert ctypes.sizeof(_capi.Plan) == 12 * 4 + 9 * 8
 
 
 @pytest.mark.parametrize("T,H,I,E,K,dtype,path", [
@@ -45,14 +45,29 @@ def test_plan_paths_and_layout(T, H, I, E, K, dtype, path):
     p = _capi.make_plan(T, H, I, E, K, dtype)
     assert p.path == path and p.rows == T * K
     offs = [p.off_block_counts, p.off_offsets, p.off_slot_to_row, p.off_row_src, p.off_tile_map,
-            p.off_inter, p.off_y, p.workspace_bytes]
+            p.off_inter, p.off_y, p.off_part, p.workspace_bytes]
     assert all(o % 256 == 0 for o in offs) and offs == sorted(offs)
     esz = 4 if dtype == _capi.F32 else 2
     assert p.off_y - p.off_inter >= T * K * I * esz
-    assert p.workspace_bytes - p.off_y >= p.down_splits * T * K * H * 4
+    assert p.off_part - p.off_y >= p.down_splits * T * K * H * 4
+    if p.path == _capi.PATH_MFMA_TILED:
+        # one 256x256 fp32 partial tile per CU (256 without a GPU) for the down tail split
+        work = H // 256 * p.max_tiles * p.down_splits
+        assert p.workspace_bytes - p.off_part >= min(work, 256) * 256 * 256 * 4
+    else:
+        assert p.workspace_bytes == p.off_part
     assert p.off_tile_map - p.off_row_src >= 4 * T * K
     if p.path == _capi.PATH_MFMA_SKINNY:
         assert (I // 128) % p.down_splits == 0
+
+
+def test_tiled_path_keeps_token_offsets_below_2gb():
+    # token-row byte offsets are 32-bit with bit 31 marking padding rows
+    assert _capi.make_plan(262143, 4096, 14336, 8, 2, _capi.BF16).path == _capi.PATH_MFMA_TILED
+    assert _capi.make_plan(262144, 4096, 14336, 8, 2, _capi.BF16).path != _capi.PATH_MFMA_TILED
+    plan = _capi.Plan()
+    assert _capi.lib().moe355_make_plan_path(262144, 4096, 14336, 8, 2, _capi.BF16,
+                                             _capi.PATH_MFMA_TILED, ctypes.byref(plan)) == -2
 
 
 @pytest.mark.parametrize("T,K,E,tile,path", [(4096, 2, 8, 256, -1), (16, 2, 8, 16, -1),

@@ -2,10 +2,11 @@
 shapes whose last round is split along K.
 
 Reference: fused_experts (reframework/moe/fused.py:49-87). The tiled gate_up
-runs its items on one workgroup per CU; the items of a last, partly filled
-round are cut along K over the idle CUs, their fp32 partial tiles summed and
-activated by a fix-up kernel. These tests build routings whose tile counts
-put that split on (checked with the host replica of its rule), and compare
+and down run their items on one workgroup per CU; the items of a last,
+partly filled round are cut along K over the idle CUs, their fp32 partial
+tiles summed (and activated, for gate_up) by a fix-up kernel. These tests
+build routings whose tile counts put that split on (checked with the host
+replica of its rule), and compare
 sampled tokens (the first and last token of every expert group, whose rows
 sit in the first and last tiles, plus random ones) with the fp64 oracle:
   * <= 2e-2 max-relative against the fp64 oracle;
@@ -20,7 +21,7 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import ROUND, banner, gpu_fused, tiled_gate_up_split
+from _helpers import ROUND, banner, gpu_fused, tiled_down_split, tiled_gate_up_split
 from oracle import oracle
 from reframework_amd import _capi
 
@@ -74,11 +75,13 @@ def _check_sampled(out, x, w1, w2, w, ids, tokens, act=0):
 
 
 SPLIT_CASES = [
-    # name, H, I, E, counts, experts, dtype, act, expected S
-    ("no_full_round_s8", 4096, 256, 64, [256, 256, 256, 256], [3, 17, 40, 63], "bf16", 0, 8),
-    ("ragged_s4", 4096, 256, 64, [300, 200, 256, 268], [5, 17, 40, 63], "bf16", 0, 4),
-    ("full_round_then_tail", 1024, 2048, 8, [512] * 7 + [520], list(range(8)), "bf16", 0, 4),
-    ("f16_gelu", 4096, 256, 64, [256, 256, 256, 256], [0, 1, 2, 3], "f16", 1, 8),
+    # name, H, I, E, counts, experts, dtype, act, expected S of gate_up and of down
+    ("no_full_round_s8", 4096, 256, 64, [256, 256, 256, 256], [3, 17, 40, 63], "bf16", 0, (8, 1)),
+    ("ragged_s4", 4096, 256, 64, [300, 200, 256, 268], [5, 17, 40, 63], "bf16", 0, (4, 1)),
+    ("full_round_then_tail", 1024, 2048, 8, [512] * 7 + [520], list(range(8)), "bf16", 0, (4, 1)),
+    ("f16_gelu", 4096, 256, 64, [256, 256, 256, 256], [0, 1, 2, 3], "f16", 1, (8, 1)),
+    # 17 token tiles x 16 weight tiles: 272 down items, a 16-item last round cut 4 ways
+    ("down_tail_s4", 4096, 2048, 8, [512] * 7 + [700], list(range(8)), "bf16", 0, (8, 4)),
 ]
 
 
@@ -91,7 +94,7 @@ def test_tail_split_matches_oracle(case, dev):
     # forced: the automatic choice sees 16 rows per expert on average
     plan = _capi.make_plan(T, H, I, E, 1, _capi.dtype_code(dt), path=_capi.PATH_MFMA_TILED)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    S = tiled_gate_up_split(plan, counts, cus)
+    S = (tiled_gate_up_split(plan, counts, cus), tiled_down_split(plan, counts, cus))
     banner(f"tail split {name} T={T} H={H} I={I} E={E} path={plan.path} S={S} cus={cus}")
     assert plan.path == _capi.PATH_MFMA_TILED
     if cus == 256:
@@ -125,8 +128,14 @@ def test_mixtral_prefill_t4096_sampled_tokens(dev):
     plan = _capi.make_plan(T, H, I, E, K, _capi.BF16)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     S = tiled_gate_up_split(plan, counts, cus)
-    banner(f"mixtral T={T} path={plan.path} down_splits={plan.down_splits} gate_up tail S={S}")
+    Sd = tiled_down_split(plan, counts, cus)
+    banner(f"mixtral T={T} path={plan.path} down_splits={plan.down_splits} gate_up tail S={S} "
+           f"down tail S={Sd}")
     assert plan.path == _capi.PATH_MFMA_TILED
+    if cus == 256:
+        # 35 token tiles: 3920 gate_up items (80 in the last round) and 1120
+        # down items (96 in the last round), both cut in two along K
+        assert (S, Sd) == (2, 2)
     w1, w2 = _bank(E, H, I, torch.bfloat16, seed=13, dev=dev, scale=0.02)
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
     w = rng.random((T, K)).astype(np.float32)
