@@ -70,10 +70,12 @@ __device__ __forceinline__ void dma16(const void* src, uint8_t* dst) {
 // tokens zero).
 constexpr uint32_t kPadOffset = 0x80000000u;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t lds_rsrc(const void* base) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lds_rsrc(const void* base,
+                                                         int num_records = 0x7fffffff) {
   // Raw buffer (stride 0); dword 3 sets a 32-bit data format, without which
-  // gfx9 treats every untyped buffer access as out of range.
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+  // gfx9 treats every untyped buffer access as out of range. num_records -1
+  // (4 GB - 1) serves sources addressed by full 32-bit offsets (weights).
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, num_records, 0x00020000);
 }
 
 // One 1 KB direct-to-LDS load per wave from a buffer resource: lane i's 16

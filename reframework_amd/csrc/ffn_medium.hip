@@ -70,26 +70,32 @@ void ffn_medium_kernel(const FfnArgs a) {
       if (kGateUp && is_tok(q)) grow[q] = a.row_src[min(t.row0 + load_row(q), t.row_end - 1)];
   };
 
-  int Ll = Lc, lkt = 0;  // load cursor
-  const char* lw;        // weight source of the load cursor's item
-  const char* lx;        // token source
+  int Ll = Lc, lkt = 0;         // load cursor
+  __amdgpu_buffer_rsrc_t lw;    // weight source of the load cursor's item
+  __amdgpu_buffer_rsrc_t lx;    // token source
   uint32_t lgoff[kLPW];
   auto setup_load = [&](const Tile& t) {
     const size_t kbeg = static_cast<size_t>(t.split) * a.k_per_split;
-    lw = static_cast<const char*>(a.w[t.e]) + kbeg * 2;
-    lx = kGateUp ? static_cast<const char*>(a.x) + kbeg * 2
-                 : static_cast<const char*>(a.x) + (static_cast<size_t>(t.row0) * ld + kbeg) * 2;
+    lw = lds_rsrc(static_cast<const char*>(a.w[t.e]) + kbeg * 2, -1);
+    lx = lds_rsrc(kGateUp ? static_cast<const char*>(a.x) + kbeg * 2
+                          : static_cast<const char*>(a.x) +
+                                (static_cast<size_t>(t.row0) * ld + kbeg) * 2);
 #pragma unroll
     for (int q = 0; q < kLPW; ++q) {
       const int r = load_row(q);
       int src_row;
-      if (!is_tok(q))
+      uint32_t pad = 0;
+      if (!is_tok(q)) {
         src_row = kGateUp ? (r < kTileW / 2 ? t.wtile * (kTileW / 2) + r
                                             : a.I + t.wtile * (kTileW / 2) + (r - kTileW / 2))
                           : t.wtile * kTileW + r;
-      else
+      } else {
         src_row = kGateUp ? grow[q] : min(t.row0 + r, t.row_end - 1) - t.row0;
-      lgoff[q] = static_cast<uint32_t>(src_row) * pitch + swz(lane & 3, r) * 16;
+        // Token rows past the group's end load zeros (out of the resource's
+        // range), OR-ed in rather than selected (see the tiled kernel).
+        pad = t.row0 + r < t.row_end ? 0u : kPadOffset;
+      }
+      lgoff[q] = (static_cast<uint32_t>(src_row) * pitch + swz(lane & 3, r) * 16) | pad;
     }
   };
   auto prefetch_next_rows = [&]() {
@@ -110,7 +116,7 @@ void ffn_medium_kernel(const FfnArgs a) {
     }
   };
   auto issue = [&](uint8_t* lb, int q) {
-    dma16((is_tok(q) ? lx : lw) + lkt * kRowBytes + lgoff[q], lb + (kLPW * wave + q) * 1024);
+    dma16_rsrc(is_tok(q) ? lx : lw, lkt * kRowBytes + lgoff[q], lb + (kLPW * wave + q) * 1024);
   };
 
   // MFMA operand rows of this wave inside a stage.
