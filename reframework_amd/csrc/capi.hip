@@ -152,19 +152,29 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
   p->down_splits = 1;
   if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_MEDIUM) {
     // The persistent down kernels run (H/256 weight tiles x token tiles x
-    // splits) work items of I/(32*splits) k-steps on one workgroup per CU.
+    // splits) work items of I/(32*splits) 32-k steps on one workgroup per CU.
     // Pick the split that minimises the busiest CU's step count, charging each
     // extra split its fp32 partial plane (written once, read by the combine)
-    // at ~1.8e-6 steps per element; ties keep fewer splits.
+    // at ~1.8e-6 steps per element; ties keep fewer splits. The 256-row
+    // kernel cuts a partly idle last round along K (work_split, same rule),
+    // so its last round costs what that cut leaves.
     // Each split must be a whole number of pipeline steps: 64 k for the
     // 256-row kernel, 32 k for the 64-row one.
     const long long items = static_cast<long long>(H / 256) * p->max_tiles;
     const int cus = moe355::device_cu_count();
-    const int step_k = p->path == MOE355_PATH_MFMA_TILED ? 64 : 32;
+    const bool tiled = p->path == MOE355_PATH_MFMA_TILED;
+    const int step_k = tiled ? 64 : 32;
     double best = 0.0;
     for (int s = 1; s <= 8 && (I / step_k) % s == 0; s *= 2) {
-      const long long rounds = (items * s + cus - 1) / cus;
-      const double cost = static_cast<double>(rounds) * (I / 32 / s) +
+      const long long n = items * s, full = n / cus, tail = n % cus;
+      const double per_item = static_cast<double>(I / 32 / s);
+      double last = tail ? per_item : 0.0;
+      if (tiled && full > 0 && tail > 0) {
+        const int nk = I / 64 / s;
+        for (long long st = 2; st <= 16 && st * tail <= cus && nk % st == 0; st *= 2)
+          last = std::min(last, 2.0 * (static_cast<double>(nk) / st + st * tail / 14.0));
+      }
+      const double cost = static_cast<double>(full) * per_item + last +
                           (s - 1) * static_cast<double>(R) * H * 1.8e-6;
       if (s == 1 || cost < 0.97 * best) {
         best = cost;
@@ -190,11 +200,11 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
   p->off_y = off;            off = align256(off + static_cast<size_t>(p->down_splits) * R * H * 4);
   p->off_part = off;
   if (p->path == MOE355_PATH_MFMA_TILED) {
-    // One 256 KB partial tile per CU at most: the tiled down projection cuts
-    // the items of a last, partly idle round along K over the idle CUs.
-    const long long work = static_cast<long long>(H / 256) * p->max_tiles * p->down_splits;
-    const long long units = std::min<long long>(work, moe355::device_cu_count());
-    off = align256(off + static_cast<size_t>(units) * 256 * 256 * 4);
+    // One 256 KB partial tile per CU: the tiled kernels cut the items of a
+    // last, partly idle round along K over the idle CUs (at most one unit per
+    // CU). gate_up also has the y region before it, free until the down
+    // projection.
+    off = align256(off + static_cast<size_t>(moe355::device_cu_count()) * 256 * 256 * 4);
   }
   p->workspace_bytes = off;
   return MOE355_OK;
@@ -333,11 +343,11 @@ int moe355_gate_up(const moe355_plan* p, const void* x, const void* const* w1, i
   hipError_t err;
   if (p->path == MOE355_PATH_MFMA_TILED) {
     a.n_wtiles = p->I / 128;
-    // The y region is free until the down projection: it holds the partial
-    // tiles of the K-split tail items (256x256 fp32 each).
-    const size_t y_bytes = static_cast<size_t>(p->down_splits) * p->rows * p->H * 4;
+    // The y and part regions are free until the down projection: they hold
+    // the partial tiles of the K-split tail items (256x256 fp32 each).
     a.part = at<float>(workspace, p->off_y);
-    a.part_units = static_cast<int>(std::min<size_t>(y_bytes / (256 * 256 * 4), 4096));
+    a.part_units = static_cast<int>(
+        std::min<size_t>((p->workspace_bytes - p->off_y) / (256 * 256 * 4), 4096));
     err = launch_gate_up_tiled(a, p->dtype, as_stream(stream));
   } else if (p->path == MOE355_PATH_MFMA_MEDIUM) {
     a.n_wtiles = p->I / 128;

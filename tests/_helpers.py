@@ -97,5 +97,5 @@ def tiled_gate_up_split(plan: _capi.Plan, counts: Sequence[int], cus: int) -> in
     n_t = sum(-(-int(c) // plan.tile_rows) for c in counts)
     n_wtiles = plan.I // 128
     G = min(n_wtiles * plan.max_tiles, cus)
-    cap = plan.down_splits * plan.rows * plan.H * 4 // (256 * 256 * 4)
+    cap = (plan.workspace_bytes - plan.off_y) // (256 * 256 * 4)
     return tail_split(n_wtiles * n_t, G, plan.H // 64, min(cap, 4096))[2]

@@ -77,7 +77,7 @@ def _check_sampled(out, x, w1, w2, w, ids, tokens, act=0):
 SPLIT_CASES = [
     # name, H, I, E, counts, experts, dtype, act, expected S of gate_up and of down
     ("no_full_round_s8", 4096, 256, 64, [256, 256, 256, 256], [3, 17, 40, 63], "bf16", 0, (8, 1)),
-    ("ragged_s4", 4096, 256, 64, [300, 200, 256, 268], [5, 17, 40, 63], "bf16", 0, (4, 1)),
+    ("ragged_s8", 4096, 256, 64, [300, 200, 256, 268], [5, 17, 40, 63], "bf16", 0, (8, 1)),
     ("full_round_then_tail", 1024, 2048, 8, [512] * 7 + [520], list(range(8)), "bf16", 0, (4, 1)),
     ("f16_gelu", 4096, 256, 64, [256, 256, 256, 256], [0, 1, 2, 3], "f16", 1, (8, 1)),
     # 17 token tiles x 16 weight tiles: 272 down items, a 16-item last round cut 4 ways
@@ -133,9 +133,9 @@ def test_mixtral_prefill_t4096_sampled_tokens(dev):
            f"down tail S={Sd}")
     assert plan.path == _capi.PATH_MFMA_TILED
     if cus == 256:
-        # 35 token tiles: 3920 gate_up items (80 in the last round) and 1120
-        # down items (96 in the last round), both cut in two along K
-        assert (S, Sd) == (2, 2)
+        # 35 token tiles: 3920 gate_up items (80 in the last round) cut in two
+        # along K; one down split, 560 items (48 in the last round) cut in four
+        assert (S, Sd) == (2, 4) and plan.down_splits == 1
     w1, w2 = _bank(E, H, I, torch.bfloat16, seed=13, dev=dev, scale=0.02)
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
     w = rng.random((T, K)).astype(np.float32)
@@ -145,7 +145,7 @@ def test_mixtral_prefill_t4096_sampled_tokens(dev):
 
 def test_mixtral_t256_sampled_tokens(dev):
     """Mixtral-8x7B layer, T=256 (~64 rows per expert): the automatic plan
-    takes the 256-row kernel with an 8-way K-split down projection, and the
+    takes the 256-row kernel with a 2-way K-split down projection, and the
     112 x 8 gate_up items leave a 128-item last round that is cut along K."""
     T, H, I, E, K = 256, 4096, 14336, 8, 2
     rng = np.random.default_rng(17)
@@ -157,7 +157,7 @@ def test_mixtral_t256_sampled_tokens(dev):
     banner(f"mixtral T={T} path={plan.path} down_splits={plan.down_splits} gate_up tail S={S}")
     assert plan.path == _capi.PATH_MFMA_TILED
     if cus == 256:
-        assert S == 2 and plan.down_splits == 8
+        assert S == 2 and plan.down_splits == 2
     w1, w2 = _bank(E, H, I, torch.bfloat16, seed=19, dev=dev, scale=0.02)
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
     w = rng.random((T, K)).astype(np.float32)
