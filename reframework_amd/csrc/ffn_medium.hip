@@ -116,7 +116,7 @@ void ffn_medium_kernel(const FfnArgs a) {
     }
   };
   auto issue = [&](uint8_t* lb, int q) {
-    dma16_rsrc(is_tok(q) ? lx : lw, lkt * kRowBytes + lgoff[q], lb + (kLPW * wave + q) * 1024);
+    dma16_rsrc(is_tok(q) ? lx : lw, lgoff[q], lkt * kRowBytes, lb + (kLPW * wave + q) * 1024);
   };
 
   // MFMA operand rows of this wave inside a stage.

@@ -145,14 +145,15 @@ void ffn_tiled_kernel(const FfnArgs a) {
   // Weight cursor: work item wL, step wkt of [.., wke); source base and
   // per-load offsets.
   int wL = Lc, wkt = 0, wke = 0;
-  const char* wsrc;
+  __amdgpu_buffer_rsrc_t wsrc;
   uint32_t woff[kLoadsPerOp];
   auto setup_w = [&](const Work& w) {
     const Tile& t = w.t;
     wkt = w.kb;
     wke = w.ke;
     const int ln = opaque(lane);
-    wsrc = static_cast<const char*>(a.w[t.e]) + static_cast<size_t>(t.split) * a.k_per_split * 2;
+    wsrc = lds_rsrc(static_cast<const char*>(a.w[t.e]) + static_cast<size_t>(t.split) * a.k_per_split * 2,
+                    -1);
 #pragma unroll
     for (int q = 0; q < kLoadsPerOp; ++q) {
       const int r = op_row(q, ln);
@@ -238,12 +239,12 @@ void ffn_tiled_kernel(const FfnArgs a) {
   auto issue_w = [&](int b, int q0, int n) {
     uint8_t* dst = lds + b * kBufBytes + wave * kLoadsPerOp * 1024;
 #pragma unroll
-    for (int q = q0; q < q0 + n; ++q) dma16(wsrc + wkt * kSRowBytes + woff[q], dst + q * 1024);
+    for (int q = q0; q < q0 + n; ++q) dma16_rsrc(wsrc, woff[q], wkt * kSRowBytes, dst + q * 1024);
   };
   auto issue_x = [&](int b, int q0, int n) {
     uint8_t* dst = lds + b * kBufBytes + wave * kLoadsPerOp * 1024;
 #pragma unroll
-    for (int q = q0; q < q0 + n; ++q) dma16_rsrc(xsrc, xkt * kSRowBytes + xoff[q], dst + q * 1024);
+    for (int q = q0; q < q0 + n; ++q) dma16_rsrc(xsrc, xoff[q], xkt * kSRowBytes, dst + q * 1024);
   };
 
   // MFMA operand rows of this wave inside a buffer.
