@@ -182,11 +182,14 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
       }
     }
   } else if (p->path == MOE355_PATH_MFMA_SKINNY) {
-    // Spread the down projection (H/16 row groups per tile) over >= 4096 waves;
-    // each split covers a multiple of the kernel's 128-element k step.
+    // Spread the down projection (H/16 row groups per tile) over >= 8192 waves,
+    // at most 8 splits (Mixtral shape: 4 splits instead of 2 at 4 and 16
+    // tokens, down 98 -> 91 and 140 -> 133 us; 16 splits at one token are
+    // 2 us slower than 8); each split covers a multiple of the kernel's
+    // 128-element k step.
     const long long waves = static_cast<long long>(H / 16) * (p->max_tiles > 0 ? p->max_tiles : 1);
     int s = 1;
-    while (s < 16 && waves * s < 4096 && (I / 128) % (2 * s) == 0) s *= 2;
+    while (s < 8 && waves * s < 8192 && (I / 128) % (2 * s) == 0) s *= 2;
     p->down_splits = s;
   }
 
