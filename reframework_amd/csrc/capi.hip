@@ -46,7 +46,7 @@ T* at(void* ws, size_t off) {
 int check_plan(const moe355_plan* p) {
   if (!p) return fail(MOE355_EINVAL, "plan is NULL");
   if (p->E < 1 || p->E > MOE355_MAX_EXPERTS || p->K < 1 || p->K > p->E || !valid_dtype(p->dtype) ||
-      p->path < 0 || p->path > MOE355_PATH_MFMA_MEDIUM || p->rows != p->T * p->K)
+      p->path < 0 || p->path > MOE355_PATH_MFMA_TILED128 || p->rows != p->T * p->K)
     return fail(MOE355_EINVAL, "plan is not one filled by moe355_make_plan");
   return MOE355_OK;
 }
@@ -98,7 +98,8 @@ int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* 
 int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path,
                           moe355_plan* p) {
   if (!p) return fail(MOE355_EINVAL, "plan is NULL");
-  if (path < -1 || path > MOE355_PATH_MFMA_MEDIUM) return fail(MOE355_EINVAL, "unknown path %d", path);
+  if (path < -1 || path > MOE355_PATH_MFMA_TILED128)
+    return fail(MOE355_EINVAL, "unknown path %d", path);
   if (T < 0 || H <= 0 || I <= 0) return fail(MOE355_EINVAL, "bad sizes T=%d H=%d I=%d", T, H, I);
   if (E < 1 || E > MOE355_MAX_EXPERTS)
     return fail(MOE355_EUNSUPPORTED, "E=%d outside [1, %d]", E, MOE355_MAX_EXPERTS);
@@ -129,28 +130,33 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
   if (path < 0) {
     // Average rows per active expert decide (measured layer times, Mixtral,
     // Phi-3.5 and fine-grained shapes): weight streaming with 16-token tiles up
-    // to 10 rows (beyond that each 16-row tile re-streams the weights),
-    // 64-token tiles up to 48, 256-token tiles above (from ~48 rows the
-    // 256-row kernel's weight stream outruns the 64-row kernel despite its
-    // padding: Mixtral 256 tokens 0.67 vs 0.74 ms).
-    path = tiled_ok && avg > 48   ? MOE355_PATH_MFMA_TILED
-           : tiled_ok && avg > 10 ? MOE355_PATH_MFMA_MEDIUM
+    // to 10 rows (beyond that each 16-row tile re-streams the weights), the
+    // 256-row kernel on 128-row tiles up to 104 rows (Mixtral 64 and 256
+    // tokens: 0.55 and 0.59 ms against 0.56 and 0.65 with 256-row tiles and
+    // 0.56 and 0.74 with the 64-row kernel; fine-grained 512 tokens 0.31
+    // against 0.32 and 0.35), 256-row tiles above (Mixtral 512 tokens: 0.67
+    // against 0.68 ms). The 64-row kernel stays available when forced.
+    path = tiled_ok && avg > 104  ? MOE355_PATH_MFMA_TILED
+           : tiled_ok && avg > 10 ? MOE355_PATH_MFMA_TILED128
            : skinny_ok            ? MOE355_PATH_MFMA_SKINNY
                                   : MOE355_PATH_SIMT;
-  } else if (((path == MOE355_PATH_MFMA_TILED || path == MOE355_PATH_MFMA_MEDIUM) && !tiled_ok) ||
+  } else if (((path == MOE355_PATH_MFMA_TILED || path == MOE355_PATH_MFMA_TILED128 ||
+               path == MOE355_PATH_MFMA_MEDIUM) && !tiled_ok) ||
              (path == MOE355_PATH_MFMA_SKINNY && !skinny_ok)) {
     return fail(MOE355_EUNSUPPORTED, "path %d cannot run dtype %d with H=%d I=%d T=%d", path,
                 dtype, H, I, T);
   }
   p->path = path;
-  p->tile_rows = path == MOE355_PATH_MFMA_TILED    ? 256
-                 : path == MOE355_PATH_MFMA_SKINNY ? 16
-                                                   : 64;
+  const bool tiled = path == MOE355_PATH_MFMA_TILED || path == MOE355_PATH_MFMA_TILED128;
+  p->tile_rows = path == MOE355_PATH_MFMA_TILED      ? 256
+                 : path == MOE355_PATH_MFMA_TILED128 ? 128
+                 : path == MOE355_PATH_MFMA_SKINNY   ? 16
+                                                     : 64;
   p->max_tiles = R > 0 ? static_cast<int>((R + static_cast<long long>(act_e) * (p->tile_rows - 1)) /
                                           p->tile_rows)
                        : 0;
   p->down_splits = 1;
-  if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_MEDIUM) {
+  if (tiled || p->path == MOE355_PATH_MFMA_MEDIUM) {
     // The persistent down kernels run (H/256 weight tiles x token tiles x
     // splits) work items of I/(32*splits) 32-k steps on one workgroup per CU.
     // Pick the split that minimises the busiest CU's step count, charging each
@@ -162,7 +168,6 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
     // 256-row kernel, 32 k for the 64-row one.
     const long long items = static_cast<long long>(H / 256) * p->max_tiles;
     const int cus = moe355::device_cu_count();
-    const bool tiled = p->path == MOE355_PATH_MFMA_TILED;
     const int step_k = tiled ? 64 : 32;
     double best = 0.0;
     for (int s = 1; s <= 8 && (I / step_k) % s == 0; s *= 2) {
@@ -202,7 +207,7 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
   p->off_inter = off;        off = align256(off + static_cast<size_t>(R) * I * esz);
   p->off_y = off;            off = align256(off + static_cast<size_t>(p->down_splits) * R * H * 4);
   p->off_part = off;
-  if (p->path == MOE355_PATH_MFMA_TILED) {
+  if (tiled) {
     // One 256 KB partial tile per CU: the tiled kernels cut the items of a
     // last, partly idle round along K over the idle CUs (at most one unit per
     // CU). gate_up also has the y region before it, free until the down
@@ -344,8 +349,9 @@ int moe355_gate_up(const moe355_plan* p, const void* x, const void* const* w1, i
   a.splits = 1; a.k_per_split = p->H; a.act = act;
   for (int e = 0; e < p->E; ++e) a.w[e] = w1[e];
   hipError_t err;
-  if (p->path == MOE355_PATH_MFMA_TILED) {
+  if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_TILED128) {
     a.n_wtiles = p->I / 128;
+    a.tile_rows = p->tile_rows;
     // The y and part regions are free until the down projection: they hold
     // the partial tiles of the K-split tail items (256x256 fp32 each).
     a.part = at<float>(workspace, p->off_y);
@@ -381,8 +387,9 @@ int moe355_down(const moe355_plan* p, const void* const* w2, void* workspace, vo
   a.splits = p->down_splits; a.k_per_split = p->I / p->down_splits; a.act = 0;
   for (int e = 0; e < p->E; ++e) a.w[e] = w2[e];
   hipError_t err;
-  if (p->path == MOE355_PATH_MFMA_TILED) {
+  if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_TILED128) {
     a.n_wtiles = p->H / 256;
+    a.tile_rows = p->tile_rows;
     // Partial tiles of the K-split last-round items (256x256 fp32 each).
     a.part = at<float>(workspace, p->off_part);
     a.part_units = p->workspace_bytes > p->off_part

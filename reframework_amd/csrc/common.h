@@ -206,6 +206,7 @@ struct FfnArgs {
   int part_units;          // capacity of part in 256x256 fp32 tiles (0: no tail split)
   int grid;                // workgroups of the tiled launch (the fix-up recomputes its split)
   int group_t;             // token tiles per item group (0: all; -1: one group per expert; see decode_tile)
+  int tile_rows;           // token rows per tile of the tile map (tiled kernels: 256, or 128 for half tiles)
   const void* w[kMaxExperts];  // w1[e] ([2I,H]) or w2[e] ([H,I])
 };
 

@@ -59,6 +59,25 @@ __device__ __forceinline__ uint32_t swz8(int c, int r) {
   return static_cast<uint32_t>(c ^ ((r >> 1) & 7));
 }
 
+// Half tiles (the kernel instance for 128-row token tiles, chosen for groups
+// of about 128 rows or fewer, where 256-row tiles would be mostly padding):
+// token rows 0-63 go to LDS rows 0-63 and rows 64-127 to LDS rows 128-191, so
+// each wave of the 2x2 arrangement keeps its operand rows and multiplies only
+// its first two 32-row token blocks (8 MFMAs per sub-step instead of 16).
+// Weight loads, the pipeline and the barriers are those of full tiles.
+
+// Token row (offset in the tile) held by LDS row r; kTileT for none.
+__device__ __forceinline__ int tile_row_of(bool half, int r) {
+  if (!half) return r;
+  return r < 64 ? r : (r >= 128 && r < 192 ? r - 64 : kTileT);
+}
+
+// Token row (offset in the tile) of lane row lr of token block j of a wave
+// with token half wave_t; kTileT when the block is unused (half tiles).
+__device__ __forceinline__ int tile_row_of_block(bool half, int wave_t, int j, int lr) {
+  return half ? (j < 2 ? wave_t * 64 + j * 32 + lr : kTileT) : wave_t * 128 + j * 32 + lr;
+}
+
 __device__ __forceinline__ int ring_add(int b, int n) {  // (b + n) % kBufs, 0 <= n < kBufs
   b += n;
   return b >= kBufs ? b - kBufs : b;
@@ -72,16 +91,16 @@ struct Work {
 };
 
 __device__ __forceinline__ Work decode_work(const FfnArgs& a, const WorkSplit& ws, int L,
-                                            int per_split, int n_t, int nk) {
+                                            int per_split, int n_t, int nk, int tile_rows) {
   Work w;
   if (L < ws.n_full) {
-    w.t = decode_tile(a, L, per_split, n_t, kTileT);
+    w.t = decode_tile(a, L, per_split, n_t, tile_rows);
     w.kb = 0;
     w.ke = nk;
     w.unit = -1;
   } else {
     const int u = L - ws.n_full, len = nk / ws.S;
-    w.t = decode_tile(a, ws.n_full + u / ws.S, per_split, n_t, kTileT);
+    w.t = decode_tile(a, ws.n_full + u / ws.S, per_split, n_t, tile_rows);
     w.kb = (u % ws.S) * len;
     w.ke = w.kb + len;
     w.unit = u;
@@ -110,7 +129,7 @@ __device__ __forceinline__ Work decode_work(const FfnArgs& a, const WorkSplit& w
 // and X_{s+1} to (2s + 3) % 5, which held W_{s-1}. Weights thus have about
 // two steps to land and tokens one. Other vector-memory operations issued in
 // between (row_src prefetch, epilogue stores) only make the waits stricter.
-template <typename T, bool kGateUp>
+template <typename T, bool kGateUp, bool kHalf>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void ffn_tiled_kernel(const FfnArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kBufs * kBufBytes];
@@ -134,7 +153,9 @@ void ffn_tiled_kernel(const FfnArgs a) {
   const int ld = kGateUp ? a.H : a.I;  // elements per weight row and per token row
   const uint32_t pitch = static_cast<uint32_t>(ld * 2);
 
-  auto decode = [&](int L) { return decode_work(a, ws, L, per_split, n_t, nk); };
+  auto decode = [&](int L) {
+    return decode_work(a, ws, L, per_split, n_t, nk, kHalf ? kTileT / 2 : kTileT);
+  };
 
   // An operand buffer is 32 loads of 1 KB, 8 rows x 128 B each; wave w issues
   // loads q = 0..7, covering rows 8 (8 w + q) + i / 8 for lane i. Lane i writes
@@ -172,9 +193,10 @@ void ffn_tiled_kernel(const FfnArgs a) {
   int grow[kLoadsPerOp];
   auto fetch_rows = [&](const Tile& t) {
     const int ln = opaque(lane);
+    constexpr bool half = kHalf;
 #pragma unroll
     for (int q = 0; q < kLoadsPerOp; ++q)
-      grow[q] = a.row_src[min(t.row0 + op_row(q, ln), t.row_end - 1)];
+      grow[q] = a.row_src[min(t.row0 + tile_row_of(half, op_row(q, ln)), t.row_end - 1)];
   };
   auto setup_x = [&](const Work& w) {
     const Tile& t = w.t;
@@ -182,18 +204,19 @@ void ffn_tiled_kernel(const FfnArgs a) {
     xke = w.ke;
     const int ln = opaque(lane);
     const size_t kbeg = static_cast<size_t>(t.split) * a.k_per_split;
-    // Rows past the group's end load zeros: their offsets get bit 31 set
-    // (valid offsets stay below 2^31, so no step of K wraps them back). The
-    // bit is OR-ed into an offset computed for every row alike: a select
-    // between the row offset and a constant became a branch per row, and in
-    // gate_up each branch waited for all loads in flight (the offset depends
-    // on the loaded row_src).
+    // Rows past the group's end (and unused LDS rows of a half tile) load
+    // zeros: their offsets get bit 31 set (valid offsets stay below 2^31, so
+    // no step of K wraps them back). The bit is OR-ed into an offset computed
+    // for every row alike: a select between the row offset and a constant
+    // became a branch per row, and in gate_up each branch waited for all
+    // loads in flight (the offset depends on the loaded row_src).
+    constexpr bool half = kHalf;
     if (kGateUp) {
       xsrc = lds_rsrc(static_cast<const char*>(a.x) + kbeg * 2);
 #pragma unroll
       for (int q = 0; q < kLoadsPerOp; ++q) {
         const int r = op_row(q, ln);
-        const uint32_t pad = t.row0 + r < t.row_end ? 0u : kPadOffset;
+        const uint32_t pad = t.row0 + tile_row_of(half, r) < t.row_end ? 0u : kPadOffset;
         xoff[q] = (static_cast<uint32_t>(grow[q]) * pitch + swz8(ln & 7, r) * 16) | pad;
       }
     } else {
@@ -201,9 +224,9 @@ void ffn_tiled_kernel(const FfnArgs a) {
                       (static_cast<size_t>(t.row0) * ld + kbeg) * 2);
 #pragma unroll
       for (int q = 0; q < kLoadsPerOp; ++q) {
-        const int r = op_row(q, ln);
-        const uint32_t pad = t.row0 + r < t.row_end ? 0u : kPadOffset;
-        xoff[q] = (static_cast<uint32_t>(r) * pitch + swz8(ln & 7, r) * 16) | pad;
+        const int r = op_row(q, ln), tr = tile_row_of(half, r);
+        const uint32_t pad = t.row0 + tr < t.row_end ? 0u : kPadOffset;
+        xoff[q] = (static_cast<uint32_t>(tr) * pitch + swz8(ln & 7, r) * 16) | pad;
       }
     }
   };
@@ -297,14 +320,16 @@ void ffn_tiled_kernel(const FfnArgs a) {
   // bw/bx) and 4 loads (issue(0..3)) are spread over the first 12 MFMAs
   // (3 MFMA : 2 LDS reads : 1 load), so neither the LDS nor the texture unit
   // sees a burst from all four waves and the last read still has 4 MFMAs to
-  // land.
+  // land. Half tiles multiply and read token blocks 0-1 only (8 MFMAs and 6
+  // operand reads per sub-step).
   auto sub = [&](const u32x4* af, const u32x4* bf, int bw, int bx, int j, u32x4* na, u32x4* nb,
                  auto issue) {
+    constexpr int NJ = kHalf ? 2 : 4, NB = NJ;
     wait_lgkm0();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) acc[i][jj] = Mfma32<T>::mma(af[i], bf[jj], acc[i][jj]);
+      for (int jj = 0; jj < NJ; ++jj) acc[i][jj] = Mfma32<T>::mma(af[i], bf[jj], acc[i][jj]);
     // Memory operations in the order of the schedule below: the compiler keeps
     // LDS reads and direct-to-LDS loads in program order (it cannot tell that
     // they touch different buffers).
@@ -314,18 +339,29 @@ void ffn_tiled_kernel(const FfnArgs a) {
     for (int i = 0; i < 4; ++i) {
       na[i] = *reinterpret_cast<const u32x4*>(sw + arow[i] + coff[j]);
       issue(i);
-      nb[i] = *reinterpret_cast<const u32x4*>(sx + brow[i] + coff[j]);
+      if (i < NB) nb[i] = *reinterpret_cast<const u32x4*>(sx + brow[i] + coff[j]);
     }
+    if (!kHalf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global -> LDS load
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global -> LDS load
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        if (i < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -356,6 +392,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
   Work cw = decode(Lc);
   while (true) {
     const Tile& ct = cw.t;
+    constexpr bool half = kHalf;
     for (int kt = cw.kb; kt < cw.ke; ++kt) {
       const int bx = ring_add(bw, 1);
       const int nbw = ring_add(bw, 2), nbx = ring_add(bw, 3);  // step s+1
@@ -403,7 +440,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
         for (int b = 0; b < 2; ++b) {
   #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
+            const int prow = ct.row0 + tile_row_of_block(half, wave_t, j, elr);
             if (prow < ct.row_end) {
   #pragma unroll
               for (int q = 0; q < 4; ++q) {
@@ -434,7 +471,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
       for (int b = 0; b < 4; ++b) {
   #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
+          const int prow = ct.row0 + tile_row_of_block(half, wave_t, j, elr);
           if (prow < ct.row_end) {
   #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -473,8 +510,8 @@ __global__ __launch_bounds__(kThreads) void gate_up_tail_fixup(const FfnArgs a) 
   T* inter = static_cast<T*>(a.out);
   for (int task = blockIdx.x; task < tasks; task += gridDim.x) {
     const int it = task >> 3, b = (task >> 2) & 1, j = task & 3;
-    const Tile t = decode_tile(a, ws.n_full + it, per_split, n_t, kTileT);
-    const int prow = t.row0 + wave_t * 128 + j * 32 + lr;
+    const Tile t = decode_tile(a, ws.n_full + it, per_split, n_t, a.tile_rows);
+    const int prow = t.row0 + tile_row_of_block(a.tile_rows < kTileT, wave_t, j, lr);
     if (prow >= t.row_end) continue;
     f32x4 g[4] = {}, u[4] = {};
     for (int p = 0; p < ws.S; ++p) {
@@ -510,8 +547,8 @@ __global__ __launch_bounds__(kThreads) void down_tail_fixup(const FfnArgs a) {
   const int wave_w = wave >> 1, wave_t = wave & 1, lr = lane & 31, kh = lane >> 5;
   for (int task = blockIdx.x; task < tasks; task += gridDim.x) {
     const int it = task >> 4, b = (task >> 2) & 3, j = task & 3;
-    const Tile t = decode_tile(a, ws.n_full + it, per_split, n_t, kTileT);
-    const int prow = t.row0 + wave_t * 128 + j * 32 + lr;
+    const Tile t = decode_tile(a, ws.n_full + it, per_split, n_t, a.tile_rows);
+    const int prow = t.row0 + tile_row_of_block(a.tile_rows < kTileT, wave_t, j, lr);
     if (prow >= t.row_end) continue;
     f32x4 v[4] = {};
     for (int p = 0; p < ws.S; ++p) {
@@ -545,9 +582,11 @@ hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   a.grid = static_cast<int>(work < device_cu_count() ? work : device_cu_count());
   if (!a.part) a.part_units = 0;
   if (dtype == MOE355_BF16)
-    ffn_tiled_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    a.tile_rows < kTileT ? ffn_tiled_kernel<bf16, kGateUp, true><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
+                         : ffn_tiled_kernel<bf16, kGateUp, false><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else
-    ffn_tiled_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    a.tile_rows < kTileT ? ffn_tiled_kernel<f16, kGateUp, true><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
+                         : ffn_tiled_kernel<f16, kGateUp, false><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.part_units == 0) return err;
   // The split depends on the device-side tile count; without a tail the

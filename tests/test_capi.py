@@ -30,15 +30,16 @@ def test_version_and_constants():
 
 @pytest.mark.parametrize("T,H,I,E,K,dtype,path", [
     (4096, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
-    (256, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
-    (128, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_MEDIUM),
+    (512, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
+    (256, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED128),
+    (128, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED128),
     (16, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_SKINNY),
     (1, 4096, 14336, 8, 2, _capi.BF16, _capi.PATH_MFMA_SKINNY),
     (2048, 4096, 6400, 16, 2, _capi.BF16, _capi.PATH_MFMA_TILED),
     (8, 2048, 1408, 64, 6, _capi.BF16, _capi.PATH_MFMA_SKINNY),
     (4096, 2048, 1408, 64, 6, _capi.BF16, _capi.PATH_MFMA_TILED),
     (512, 1024, 2816, 8, 2, _capi.F32, _capi.PATH_SIMT),
-    (128, 1024, 2816, 8, 2, _capi.F16, _capi.PATH_MFMA_MEDIUM),
+    (128, 1024, 2816, 8, 2, _capi.F16, _capi.PATH_MFMA_TILED128),
     (512, 1024, 2816, 8, 2, _capi.F16, _capi.PATH_MFMA_TILED),
 ])
 def test_plan_paths_and_layout(T, H, I, E, K, dtype, path):
@@ -50,7 +51,7 @@ def test_plan_paths_and_layout(T, H, I, E, K, dtype, path):
     esz = 4 if dtype == _capi.F32 else 2
     assert p.off_y - p.off_inter >= T * K * I * esz
     assert p.off_part - p.off_y >= p.down_splits * T * K * H * 4
-    if p.path == _capi.PATH_MFMA_TILED:
+    if p.path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128):
         # one 256x256 fp32 partial tile per CU (256 without a GPU) for the tail splits
         assert p.workspace_bytes - p.off_part >= 256 * 256 * 256 * 4
     else:
@@ -71,7 +72,7 @@ def test_tiled_path_keeps_token_offsets_below_2gb():
 
 @pytest.mark.parametrize("T,K,E,tile,path", [(4096, 2, 8, 256, -1), (16, 2, 8, 16, -1),
                                              (8, 6, 64, 16, -1), (333, 3, 7, 64, -1),
-                                             (128, 2, 8, 64, -1), (777, 2, 5, 64, 3)])
+                                             (128, 2, 8, 128, -1), (777, 2, 5, 64, 3)])
 def test_tile_map_capacity_bounds_every_routing(T, K, E, tile, path):
     dtype = _capi.F32 if (tile == 64 and path < 0 and T == 333) else _capi.BF16
     H, I = (256, 256) if tile != 16 else (256, 128)
@@ -135,13 +136,14 @@ def test_zero_tokens_is_a_no_op():
                                     _capi.BF16, 0, None, 0, None, 0, None) == 0
 
 
-@pytest.mark.parametrize("path,tile", [(_capi.PATH_MFMA_TILED, 256), (_capi.PATH_MFMA_MEDIUM, 64),
-                                       (_capi.PATH_MFMA_SKINNY, 16), (_capi.PATH_SIMT, 64)])
+@pytest.mark.parametrize("path,tile", [(_capi.PATH_MFMA_TILED, 256), (_capi.PATH_MFMA_TILED128, 128),
+                                       (_capi.PATH_MFMA_MEDIUM, 64), (_capi.PATH_MFMA_SKINNY, 16),
+                                       (_capi.PATH_SIMT, 64)])
 def test_forced_path_plans(path, tile):
     p = _capi.make_plan(300, 512, 384, 8, 2, _capi.BF16, path)
     assert p.path == path and p.tile_rows == tile
     assert p.max_tiles >= -(-600 // tile)
-    if path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_MEDIUM):
+    if path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128, _capi.PATH_MFMA_MEDIUM):
         assert (384 // 32) % p.down_splits == 0
 
 
@@ -152,6 +154,8 @@ def test_forced_path_rejects_shapes_it_cannot_run():
     assert lib.moe355_make_plan_path(4, 256, 256, 8, 2, _capi.F32, _capi.PATH_MFMA_MEDIUM,
                                      ctypes.byref(plan)) == -2
     assert lib.moe355_make_plan_path(4, 384, 256, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED,
+                                     ctypes.byref(plan)) == -2
+    assert lib.moe355_make_plan_path(4, 384, 256, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED128,
                                      ctypes.byref(plan)) == -2
     assert lib.moe355_make_plan_path(4, 256, 256, 8, 2, _capi.BF16, 7, ctypes.byref(plan)) == -1
     assert "unknown path" in lib.moe355_last_error().decode()

@@ -81,9 +81,9 @@ CASES = [
     ("decode_t16", 16, 2, 8, 1024, 2048, "bf16", _capi.PATH_MFMA_SKINNY),
     ("decode_f16", 8, 2, 8, 512, 512, "f16", _capi.PATH_MFMA_SKINNY),
     ("finegrained_t8", 8, 6, 64, 256, 128, "bf16", _capi.PATH_MFMA_SKINNY),
-    ("medium_ragged", 150, 2, 8, 512, 384, "bf16", _capi.PATH_MFMA_MEDIUM),
-    ("medium_f16", 80, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_MEDIUM),
-    ("medium_e16", 300, 2, 16, 512, 256, "bf16", _capi.PATH_MFMA_MEDIUM),
+    ("half_tiles_ragged", 150, 2, 8, 512, 384, "bf16", _capi.PATH_MFMA_TILED128),
+    ("half_tiles_f16", 80, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_TILED128),
+    ("half_tiles_e16", 300, 2, 16, 512, 256, "bf16", _capi.PATH_MFMA_TILED128),
     ("prefill_ragged", 700, 2, 8, 512, 384, "bf16", _capi.PATH_MFMA_TILED),
     ("prefill_tiled", 1200, 2, 4, 512, 384, "bf16", _capi.PATH_MFMA_TILED),
     ("prefill_f16", 1000, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_TILED),
@@ -132,8 +132,8 @@ def test_gelu_activations(act, T, dev):
 @pytest.mark.parametrize("T,K,E,H,I,seed", [(700, 2, 8, 512, 384, 1), (333, 6, 18, 512, 256, 2),
                                             (1, 2, 8, 256, 256, 3), (2048, 2, 16, 512, 512, 4),
                                             (64, 1, 1, 256, 256, 5)])
-@pytest.mark.parametrize("path", [_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_MEDIUM,
-                                  _capi.PATH_MFMA_SKINNY])
+@pytest.mark.parametrize("path", [_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128,
+                                  _capi.PATH_MFMA_MEDIUM, _capi.PATH_MFMA_SKINNY])
 def test_every_mfma_family_on_every_shape(path, T, K, E, H, I, seed, dev):
     banner(f"forced path={path} T={T} K={K} E={E} H={H} I={I}")
     w1, w2 = make_bank(E, H, I, torch.bfloat16, seed=seed)
@@ -144,8 +144,8 @@ def test_every_mfma_family_on_every_shape(path, T, K, E, H, I, seed, dev):
     _check(out, x, w1, w2, w, ids)
 
 
-@pytest.mark.parametrize("path", [-1, _capi.PATH_MFMA_TILED])
-@pytest.mark.parametrize("m", [63, 64, 65, 255, 256, 257, 512, 513])
+@pytest.mark.parametrize("path", [-1, _capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128])
+@pytest.mark.parametrize("m", [63, 64, 65, 127, 128, 129, 255, 256, 257, 512, 513])
 def test_tile_boundary_group_sizes(m, path, dev):
     # all m tokens to expert 0 (K=1) plus one token on expert 3
     banner(f"tile boundary m={m} path={path}")
