@@ -165,8 +165,18 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
     // kernel cuts a partly idle last round along K (work_split, same rule),
     // so its last round costs what that cut leaves.
     // Each split must be a whole number of pipeline steps: 64 k for the
-    // 256-row kernel, 32 k for the 64-row one.
-    const long long items = static_cast<long long>(H / 256) * p->max_tiles;
+    // 256-row kernel, 32 k for the 64-row one. Token tiles are estimated per
+    // active expert as its average rows over the tile height plus half a tile
+    // for the ragged end, at least one (Mixtral 4096 tokens: 36, as routed;
+    // 128 and 256 tokens on 128-row tiles: 8): max_tiles is a worst case, and
+    // sizing the split by it cut layers finer than their real tile count pays
+    // for (Mixtral 256, 512 and 1024 tokens: down 0.201, 0.225 and 0.318 ms
+    // with the worst case, 0.183, 0.204 and 0.283 with the estimate).
+    const double est_tiles =
+        std::min(static_cast<double>(p->max_tiles),
+                 act_e * std::max(1.0, static_cast<double>(R) / act_e / p->tile_rows + 0.5));
+    const long long items =
+        static_cast<long long>(H / 256) * static_cast<long long>(est_tiles + 0.5);
     const int cus = moe355::device_cu_count();
     const int step_k = tiled ? 64 : 32;
     double best = 0.0;
