@@ -83,21 +83,25 @@ class Layer:
 
 
 def run_layer(layer, x, bufs, events=None):
-    """router -> permute -> gate_up -> down -> combine on the current stream."""
+    """router, then the routed experts on the current stream. Without events
+    the experts run as the layer runs them, one moe355_fused_experts call
+    (permute -> gate_up -> down -> combine; at decode sizes the grouping
+    happens inside gate_up). With events (the stage-timing pass) the stages
+    are called one by one with events between them."""
     from reframework_amd import _capi
 
     plan, ws, w, ids, out = bufs
     s = _capi.stream_handle(x.device)
     _capi.router_topk(x, layer.gate, layer.bias, layer.K, True, True, 0, w, ids, stream=s)
+    if not events:
+        _capi.fused_experts(x, layer.w1p, layer.w2p, layer.I, w, ids, 0, out, ws, stream=s)
+        return
     _capi.permute(plan, ids, ws, stream=s)
-    if events:
-        events[0].record()
+    events[0].record()
     _capi.gate_up(plan, x, layer.w1p, 0, ws, stream=s)
-    if events:
-        events[1].record()
+    events[1].record()
     _capi.down(plan, layer.w2p, ws, stream=s)
-    if events:
-        events[2].record()
+    events[2].record()
     _capi.combine(plan, w, out, False, ws, stream=s)
 
 

@@ -315,32 +315,64 @@ int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renorm
   return check_hip(launch_topk_from_logits(a, as_stream(stream)), "topk_from_logits launch");
 }
 
-int moe355_permute(const moe355_plan* p, const void* topk_ids, int ids_int64,
-                   const int32_t* expert_map, int map_len, void* workspace, void* stream) {
-  int rc = check_plan(p);
-  if (rc) return rc;
+}  // extern "C"
+
+namespace {
+
+// Checks the permute's arguments and fills its kernel arguments (the caller
+// has checked the plan and that it has rows).
+int permute_args(const moe355_plan* p, const void* topk_ids, int ids_int64,
+                 const int32_t* expert_map, int map_len, void* workspace, PermuteArgs* a) {
   if (map_len < 0 || map_len > MOE355_MAX_EXPERTS)
     return fail(MOE355_EUNSUPPORTED, "expert_map length %d outside [0, %d]", map_len,
                 MOE355_MAX_EXPERTS);
   if (map_len > 0 && !expert_map) return fail(MOE355_EINVAL, "expert_map is NULL");
   if (p->rows == 0) return MOE355_OK;
   if (!topk_ids || !workspace) return fail(MOE355_EINVAL, "NULL topk_ids or workspace");
-  PermuteArgs a{};
-  a.ids = topk_ids;
-  a.block_counts = at<int32_t>(workspace, p->off_block_counts);
-  a.offsets = at<int32_t>(workspace, p->off_offsets);
-  a.slot_to_row = at<int32_t>(workspace, p->off_slot_to_row);
-  a.row_src = at<int32_t>(workspace, p->off_row_src);
-  a.tile_map = at<int32_t>(workspace, p->off_tile_map);
-  a.R = p->rows; a.K = p->K; a.E = p->E; a.n_blocks = p->n_blocks;
-  a.tile_rows = p->tile_rows; a.max_tiles = p->max_tiles;
-  a.ids_int64 = ids_int64 != 0; a.map_len = map_len;
-  for (int i = 0; i < map_len; ++i) a.map[i] = expert_map[i];
+  *a = PermuteArgs{};
+  a->ids = topk_ids;
+  a->block_counts = at<int32_t>(workspace, p->off_block_counts);
+  a->offsets = at<int32_t>(workspace, p->off_offsets);
+  a->slot_to_row = at<int32_t>(workspace, p->off_slot_to_row);
+  a->row_src = at<int32_t>(workspace, p->off_row_src);
+  a->tile_map = at<int32_t>(workspace, p->off_tile_map);
+  a->R = p->rows; a->K = p->K; a->E = p->E; a->n_blocks = p->n_blocks;
+  a->tile_rows = p->tile_rows; a->max_tiles = p->max_tiles;
+  a->ids_int64 = ids_int64 != 0; a->map_len = map_len;
+  for (int i = 0; i < map_len; ++i) a->map[i] = expert_map[i];
+  return MOE355_OK;
+}
+
+// moe355_gate_up, or with self (skinny path, <= 64 routed slots) the
+// self-permuting gate_up that also does the permute's work.
+int gate_up_impl(const moe355_plan* p, const void* x, const void* const* w1, int act,
+                 void* workspace, void* stream, const PermuteArgs* self);
+
+}  // namespace
+
+extern "C" {
+
+int moe355_permute(const moe355_plan* p, const void* topk_ids, int ids_int64,
+                   const int32_t* expert_map, int map_len, void* workspace, void* stream) {
+  int rc = check_plan(p);
+  if (rc) return rc;
+  PermuteArgs a;
+  if ((rc = permute_args(p, topk_ids, ids_int64, expert_map, map_len, workspace, &a))) return rc;
+  if (p->rows == 0) return MOE355_OK;
   return check_hip(launch_permute(a, as_stream(stream)), "permute launch");
 }
 
 int moe355_gate_up(const moe355_plan* p, const void* x, const void* const* w1, int act,
                    void* workspace, void* stream) {
+  return gate_up_impl(p, x, w1, act, workspace, stream, nullptr);
+}
+
+}  // extern "C"
+
+namespace {
+
+int gate_up_impl(const moe355_plan* p, const void* x, const void* const* w1, int act,
+                 void* workspace, void* stream, const PermuteArgs* self) {
   int rc = check_plan(p);
   if (rc) return rc;
   if (act < MOE355_ACT_SILU || act > MOE355_ACT_GELU_TANH)
@@ -373,6 +405,10 @@ int moe355_gate_up(const moe355_plan* p, const void* x, const void* const* w1, i
     err = launch_gate_up_medium(a, p->dtype, as_stream(stream));
   } else if (p->path == MOE355_PATH_MFMA_SKINNY) {
     a.n_wtiles = p->I / 16;
+    if (self) {
+      a.self_permute = 1;
+      a.perm = *self;
+    }
     err = launch_gate_up_skinny(a, p->dtype, as_stream(stream));
   } else {
     a.n_wtiles = (p->I + 63) / 64;
@@ -380,6 +416,10 @@ int moe355_gate_up(const moe355_plan* p, const void* x, const void* const* w1, i
   }
   return check_hip(err, "gate_up launch");
 }
+
+}  // namespace
+
+extern "C" {
 
 int moe355_down(const moe355_plan* p, const void* const* w2, void* workspace, void* stream) {
   int rc = check_plan(p);
@@ -448,8 +488,18 @@ int moe355_fused_experts(const void* x, const void* const* w1, const void* const
   if (!workspace || workspace_bytes < p.workspace_bytes)
     return fail(MOE355_EWORKSPACE, "workspace of %zu bytes, plan needs %zu", workspace_bytes,
                 p.workspace_bytes);
-  if ((rc = moe355_permute(&p, topk_ids, ids_int64, expert_map, map_len, workspace, stream))) return rc;
-  if ((rc = moe355_gate_up(&p, x, w1, act, workspace, stream))) return rc;
+  if (p.path == MOE355_PATH_MFMA_SKINNY && p.rows <= 64) {
+    // Decode sizes: the gate_up workgroups group the routed slots themselves
+    // (one launch fewer; the permute's outputs are still written for down and
+    // combine).
+    PermuteArgs pa;
+    if ((rc = permute_args(&p, topk_ids, ids_int64, expert_map, map_len, workspace, &pa))) return rc;
+    if ((rc = gate_up_impl(&p, x, w1, act, workspace, stream, &pa))) return rc;
+  } else {
+    if ((rc = moe355_permute(&p, topk_ids, ids_int64, expert_map, map_len, workspace, stream)))
+      return rc;
+    if ((rc = moe355_gate_up(&p, x, w1, act, workspace, stream))) return rc;
+  }
   if ((rc = moe355_down(&p, w2, workspace, stream))) return rc;
   return moe355_combine(&p, topk_w, out, accumulate_f32, workspace, stream);
 }

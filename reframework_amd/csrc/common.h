@@ -193,6 +193,19 @@ struct PermuteArgs {
   int32_t map[kMaxExperts];
 };
 
+// Local expert of routed slot `slot`, or -1 when the slot is dropped (an id
+// the optional map sends negative or outside [0, E), or that lies outside the
+// map).
+__device__ __forceinline__ int routed_expert(const PermuteArgs& a, int slot) {
+  long long id = a.ids_int64 ? static_cast<const int64_t*>(a.ids)[slot]
+                             : static_cast<long long>(static_cast<const int32_t*>(a.ids)[slot]);
+  if (a.map_len > 0) {
+    if (id < 0 || id >= a.map_len) return -1;
+    id = a.map[id];
+  }
+  return (id >= 0 && id < a.E) ? static_cast<int>(id) : -1;
+}
+
 struct FfnArgs {
   const void* x;           // gate_up: tokens [T,H]; down: inter [R,I]
   const int32_t* row_src;  // [R]
@@ -208,6 +221,11 @@ struct FfnArgs {
   int group_t;             // token tiles per item group (0: all; -1: one group per expert; see decode_tile)
   int tile_rows;           // token rows per tile of the tile map (tiled kernels: 256, or 128 for half tiles)
   const void* w[kMaxExperts];  // w1[e] ([2I,H]) or w2[e] ([H,I])
+  // Skinny gate_up only, when self_permute: every workgroup groups the <= 64
+  // routed slots of perm itself (no permute launch), and workgroup 0 writes
+  // perm's offsets, slot_to_row, row_src and tile_map for the later stages.
+  int self_permute;
+  PermuteArgs perm;
 };
 
 struct NormArgs {

@@ -26,6 +26,8 @@
 // reads what it wrote. gate_up fuses the gated activation; down writes fp32
 // partials per K-split, which the combine kernel sums, so the short down
 // projection of a decode step still spreads over every CU.
+#include <climits>
+
 #include "common.h"
 
 namespace moe355 {
@@ -65,7 +67,74 @@ __device__ __forceinline__ u32x4 load16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
-template <typename T, bool kGateUp>
+// Grouping of <= 64 routed slots by one wave, the same stable counting sort
+// as the permute kernels (experts ascending, slots ascending within an
+// expert): lane s holds slot s. Distinct experts are taken in ascending order
+// (at most 64 rounds of a wave minimum and a ballot). Returns, for token tile
+// ttile, its expert, first row and row end in meta[1..3] and the tile count
+// in meta[0]; rowsrc[row] = source token of each permuted row. With
+// write_global the wave also writes the permute's outputs (offsets,
+// slot_to_row, row_src, tile_map with kRows-row tiles) for the later stages.
+__device__ void group_small(const PermuteArgs& pa, int ttile, bool write_global, int* meta,
+                            int* rowsrc, int* dist_e, int* dist_start) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int e = lane < pa.R ? routed_expert(pa, lane) : -1;
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  unsigned long long todo = __ballot(e >= 0);
+  int row = -1, start = 0, tstart = 0, nd = 0;
+  int te = -1, trow0 = 0, tend = 0;
+  while (todo) {
+    int emin = ((todo >> lane) & 1ull) ? e : INT_MAX;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) emin = min(emin, __shfl_xor(emin, o, kWave));
+    const unsigned long long m = __ballot(e == emin);
+    const int cnt = __popcll(m), nt = (cnt + kRows - 1) / kRows;
+    if (e == emin) row = start + __popcll(m & lt_mask);
+    if (ttile >= tstart && ttile < tstart + nt) {
+      te = emin;
+      trow0 = start + (ttile - tstart) * kRows;
+      tend = min(trow0 + kRows, start + cnt);
+    }
+    if (write_global && lane < nt) {
+      pa.tile_map[2 + 2 * (tstart + lane)] = emin;
+      pa.tile_map[3 + 2 * (tstart + lane)] = start + lane * kRows;
+    }
+    if (lane == 0) {
+      dist_e[nd] = emin;
+      dist_start[nd] = start;
+    }
+    ++nd;
+    start += cnt;
+    tstart += nt;
+    todo &= ~m;
+  }
+  if (row >= 0) rowsrc[row] = lane / pa.K;
+  if (lane == 0) {
+    meta[0] = tstart;
+    meta[1] = te;
+    meta[2] = trow0;
+    meta[3] = tend;
+  }
+  if (!write_global) return;
+  if (lane < pa.R) pa.slot_to_row[lane] = row;
+  if (row >= 0) pa.row_src[row] = lane / pa.K;
+  if (lane == 0) {
+    pa.tile_map[0] = tstart;
+    pa.tile_map[1] = kRows;
+  }
+  // offsets[x] = rows of experts below x: the start of the first present
+  // expert >= x (the distinct experts are ascending), else the total.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int x = lane; x <= pa.E; x += kWave) {
+    int off = start;
+    for (int d = nd - 1; d >= 0; --d)
+      if (dist_e[d] >= x) off = dist_start[d];
+    pa.offsets[x] = off;
+  }
+}
+
+template <typename T, bool kGateUp, bool kSelfPermute>
 __global__ __launch_bounds__(kThreads) void ffn_skinny_kernel(const FfnArgs a) {
   constexpr int NOP = kGateUp ? 2 : 1;   // weight operands: gate (+ up)
   constexpr int D = kGateUp ? 2 : 4;     // steps in flight per wave
@@ -75,10 +144,24 @@ __global__ __launch_bounds__(kThreads) void ffn_skinny_kernel(const FfnArgs a) {
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int group = blockIdx.x * kWavesPerBlock + wave;
   const int ttile = blockIdx.y, split = blockIdx.z;
-  if (ttile >= a.tile_map[0] || group >= a.n_wtiles) return;
-  const int e = a.tile_map[2 + 2 * ttile];
-  const int row0 = a.tile_map[3 + 2 * ttile];
-  const int row_end = min(row0 + kRows, a.offsets[e + 1]);
+  int e, row0, row_end;
+  __shared__ int s_meta[4], s_rowsrc[kWave], s_dist_e[kWave], s_dist_start[kWave];
+  if (kSelfPermute) {
+    // Every wave reaches the barrier before any returns.
+    if (wave == 0)
+      group_small(a.perm, ttile, blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0, s_meta,
+                  s_rowsrc, s_dist_e, s_dist_start);
+    __syncthreads();
+    if (ttile >= s_meta[0] || group >= a.n_wtiles) return;
+    e = s_meta[1];
+    row0 = s_meta[2];
+    row_end = s_meta[3];
+  } else {
+    if (ttile >= a.tile_map[0] || group >= a.n_wtiles) return;
+    e = a.tile_map[2 + 2 * ttile];
+    row0 = a.tile_map[3 + 2 * ttile];
+    row_end = min(row0 + kRows, a.offsets[e + 1]);
+  }
 
   const int ld = kGateUp ? a.H : a.I;
   const int kbeg = split * a.k_per_split;
@@ -108,7 +191,9 @@ __global__ __launch_bounds__(kThreads) void ffn_skinny_kernel(const FfnArgs a) {
 
   const int prow = row0 + (lane & 15);
   const bool valid = prow < row_end;
-  const int xrow = kGateUp ? a.row_src[valid ? prow : row0] : (valid ? prow : row0);
+  const int xrow = !kGateUp     ? (valid ? prow : row0)
+                   : kSelfPermute ? s_rowsrc[valid ? prow : row0]
+                                  : a.row_src[valid ? prow : row0];
   const T* xp = static_cast<const T*>(a.x) + static_cast<size_t>(xrow) * ld + (lane >> 4) * 8;
   const u32x4 zero = {0, 0, 0, 0};
 
@@ -182,11 +267,18 @@ __global__ __launch_bounds__(kThreads) void ffn_skinny_kernel(const FfnArgs a) {
 template <bool kGateUp>
 hipError_t launch_skinny(const FfnArgs& a, int dtype, hipStream_t s) {
   if (a.n_wtiles == 0 || a.max_tiles == 0) return hipSuccess;
+  if (a.self_permute && (!kGateUp || a.perm.R > kWave)) return hipErrorInvalidValue;
   const dim3 grid((a.n_wtiles + kWavesPerBlock - 1) / kWavesPerBlock, a.max_tiles, a.splits);
-  if (dtype == MOE355_BF16)
-    ffn_skinny_kernel<bf16, kGateUp><<<grid, dim3(kThreads), 0, s>>>(a);
-  else
-    ffn_skinny_kernel<f16, kGateUp><<<grid, dim3(kThreads), 0, s>>>(a);
+  if (a.self_permute) {
+    if (dtype == MOE355_BF16)
+      ffn_skinny_kernel<bf16, true, true><<<grid, dim3(kThreads), 0, s>>>(a);
+    else
+      ffn_skinny_kernel<f16, true, true><<<grid, dim3(kThreads), 0, s>>>(a);
+  } else if (dtype == MOE355_BF16) {
+    ffn_skinny_kernel<bf16, kGateUp, false><<<grid, dim3(kThreads), 0, s>>>(a);
+  } else {
+    ffn_skinny_kernel<f16, kGateUp, false><<<grid, dim3(kThreads), 0, s>>>(a);
+  }
   return hipGetLastError();
 }
 

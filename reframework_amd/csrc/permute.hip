@@ -21,17 +21,6 @@ constexpr int kThreads = 256;
 constexpr int kRounds = kPermuteChunk / kThreads;
 constexpr int kWaves = kThreads / kWave;
 
-// Local expert of a routed slot, or -1 when the slot is dropped.
-__device__ __forceinline__ int slot_expert(const PermuteArgs& a, int slot) {
-  long long id = a.ids_int64 ? static_cast<const int64_t*>(a.ids)[slot]
-                             : static_cast<long long>(static_cast<const int32_t*>(a.ids)[slot]);
-  if (a.map_len > 0) {
-    if (id < 0 || id >= a.map_len) return -1;
-    id = a.map[id];
-  }
-  return (id >= 0 && id < a.E) ? static_cast<int>(id) : -1;
-}
-
 __global__ __launch_bounds__(kThreads) void count_kernel(const PermuteArgs a) {
   __shared__ int hist[kMaxExperts];
   const int b = blockIdx.x, tid = threadIdx.x;
@@ -41,7 +30,7 @@ __global__ __launch_bounds__(kThreads) void count_kernel(const PermuteArgs a) {
   for (int r = 0; r < kRounds; ++r) {
     const int slot = b * kPermuteChunk + r * kThreads + tid;
     if (slot < a.R) {
-      const int e = slot_expert(a, slot);
+      const int e = routed_expert(a, slot);
       if (e >= 0) atomicAdd(&hist[e], 1);
     }
   }
@@ -72,7 +61,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
     for (int r = 0; r < kRounds; ++r) {
       const int slot = r * kThreads + tid;
       if (slot < a.R) {
-        const int e = slot_expert(a, slot);
+        const int e = routed_expert(a, slot);
         if (e >= 0) atomicAdd(&total[e], 1);
       }
     }
@@ -157,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
     for (int i = tid; i < kWaves * a.E; i += kThreads) wave_cnt[i / a.E][i % a.E] = 0;
     __syncthreads();
     const int slot = b * kPermuteChunk + r * kThreads + tid;
-    const int e = slot < a.R ? slot_expert(a, slot) : -1;
+    const int e = slot < a.R ? routed_expert(a, slot) : -1;
     // Rank among lanes of this wave routed to the same expert, lower lanes first.
     int rank = 0;
     unsigned long long todo = __ballot(e >= 0);

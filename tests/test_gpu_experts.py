@@ -74,6 +74,58 @@ def test_permute_bit_exact(T, K, E, ids64, drop, dev):
     assert [tuple(p) for p in tm[2:2 + 2 * len(want)].reshape(-1, 2)] == want
 
 
+@pytest.mark.parametrize("T,K,E,ids64,drop", [
+    (1, 2, 8, False, False), (16, 2, 8, True, True), (32, 2, 8, False, False),
+    (8, 6, 64, True, False), (8, 8, 256, True, True), (3, 6, 64, False, True),
+])
+def test_decode_grouping_inside_gate_up_bit_exact(T, K, E, ids64, drop, dev):
+    """At decode sizes (skinny path, <= 64 routed slots) fused_experts skips
+    the permute launch: the gate_up workgroups group the slots themselves and
+    workgroup 0 writes the permute's outputs. Those outputs must equal the
+    oracle's grouping bit for bit, and the layer output the staged path's."""
+    H, I = 256, 256
+    banner(f"decode grouping in gate_up T={T} K={K} E={E} ids64={ids64} drop={drop}")
+    ids = skewed_ids(T, K, E, seed=T * E + K, skew=1.2)
+    emap = [(-1 if e % 5 == 3 else e) for e in range(E)] if drop else None
+    plan = _capi.make_plan(T, H, I, E, K, _capi.BF16)
+    assert plan.path == _capi.PATH_MFMA_SKINNY and plan.rows <= 64
+    w1, w2 = make_bank(E, H, I, torch.bfloat16, seed=T + E)
+    w1d = [w.to(dev).contiguous() for w in w1]
+    w2d = [w.to(dev).contiguous() for w in w2]
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16).to(dev)
+    tw = torch.from_numpy(np.random.default_rng(T).random((T, K)).astype(np.float32)).to(dev)
+    idt = torch.from_numpy(ids).to(dev)
+    idt = idt if ids64 else idt.int()
+    p1 = [w.data_ptr() for w in w1d]
+    p2 = [w.data_ptr() for w in w2d]
+    ws = torch.full((plan.workspace_bytes,), 0x5A, dtype=torch.uint8, device=dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    _capi.fused_experts(x, p1, p2, I, tw, idt, 0, out, ws, expert_map=emap)
+    # the staged entry points: permute launch, then the plain gate_up
+    staged = torch.empty_like(out)
+    ws2 = torch.empty_like(ws)
+    _capi.permute(plan, idt, ws2, expert_map=emap)
+    _capi.gate_up(plan, x, p1, 0, ws2)
+    _capi.down(plan, p2, ws2)
+    _capi.combine(plan, tw, staged, False, ws2)
+    torch.cuda.synchronize()
+    R = T * K
+    offsets, s2r, src = oracle.permute(ids, E, emap)
+    assert np.array_equal(read_ws(plan, ws, plan.off_offsets, E + 1), offsets)
+    assert np.array_equal(read_ws(plan, ws, plan.off_slot_to_row, R), s2r)
+    n = offsets[-1]
+    assert np.array_equal(read_ws(plan, ws, plan.off_row_src, R)[:n], src[:n])
+    counts = np.diff(offsets)
+    want = [(e, offsets[e] + j * plan.tile_rows) for e in range(E)
+            for j in range(-(-counts[e] // plan.tile_rows))]
+    tm = read_ws(plan, ws, plan.off_tile_map, 2 + 2 * plan.max_tiles)
+    assert tm[0] == len(want) <= plan.max_tiles and tm[1] == plan.tile_rows
+    assert [tuple(p) for p in tm[2:2 + 2 * len(want)].reshape(-1, 2)] == want
+    assert torch.equal(out, staged)
+    if not drop:
+        _check(out, x.cpu(), w1, w2, tw.cpu().numpy(), ids)
+
+
 # ------------------------------------------------------------ expert FFN
 CASES = [
     # name, T, K, E, H, I, dtype, expected path
