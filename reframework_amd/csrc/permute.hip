@@ -20,6 +20,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRounds = kPermuteChunk / kThreads;
 constexpr int kWaves = kThreads / kWave;
+static_assert(kMaxExperts <= 256, "the scatter ranks slots by the 8 bits of the expert id");
 
 __global__ __launch_bounds__(kThreads) void count_kernel(const PermuteArgs a) {
   __shared__ int hist[kMaxExperts];
@@ -147,17 +148,20 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
     __syncthreads();
     const int slot = b * kPermuteChunk + r * kThreads + tid;
     const int e = slot < a.R ? routed_expert(a, slot) : -1;
-    // Rank among lanes of this wave routed to the same expert, lower lanes first.
-    int rank = 0;
-    unsigned long long todo = __ballot(e >= 0);
-    while (todo) {
-      const int leader = __ffsll(static_cast<long long>(todo)) - 1;
-      const int ev = __shfl(e, leader, kWave);
-      const unsigned long long m = __ballot(e == ev);
-      if (e == ev) rank = __popcll(m & lt_mask);
-      if (lane == leader) wave_cnt[wave][ev] = __popcll(m);
-      todo &= ~m;
+    // Lanes of this wave routed to the same expert: the routed lanes that
+    // agree with this lane on each of the 8 bits of the expert id (E <= 256),
+    // one ballot per bit instead of one per distinct expert. The rank is the
+    // count of such lanes below this one; the lowest of them writes the
+    // wave's count.
+    unsigned long long same = __ballot(e >= 0);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const bool set = (e >> bit) & 1;
+      const unsigned long long m = __ballot(set);
+      same &= set ? m : ~m;
     }
+    const int rank = __popcll(same & lt_mask);
+    if (e >= 0 && rank == 0) wave_cnt[wave][e] = __popcll(same);
     __syncthreads();
     if (slot < a.R) {
       if (e >= 0) {
