@@ -220,6 +220,198 @@ __global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
               a.topk_ids + static_cast<size_t>(t0 + t) * a.out_ld, lane);
 }
 
+// Softmax + top-k + renormalisation of one token by a 16-lane group (the
+// lanes l .. l + 15 of one wave, sub = l % 16): lane sub holds experts
+// sub + 16 j, j < NV. Selection as wave_topk (value, then lower id on exact
+// ties), each reduction a 4-step butterfly inside the group. Lane sub == 0
+// writes the results. K <= 8.
+template <int NV>
+__device__ void group16_topk(const float* lg, int E, int K, int renorm, int kmin, float* w_out,
+                             int32_t* id_out, int sub) {
+  float v[NV];
+  bool live[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int e = sub + 16 * j;
+    live[j] = e < E;
+    v[j] = live[j] ? lg[e] : -INFINITY;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    if (live[j]) m = fmaxf(m, v[j]);
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    if (live[j]) s += expf(v[j] - m);
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
+  float hs = 0.f;
+  if (kmin > 0) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      if (live[j]) {
+        const float p = expf(v[j] - m) / s;
+        hs += p * logf(fmaxf(p, 1e-9f));
+      }
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) hs += __shfl_xor(hs, o, 16);
+    hs = -hs;
+  }
+  float psel[8];
+  int isel[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    psel[k] = 0.f;
+    isel[k] = 0;
+    if (k >= K) continue;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int e = sub + 16 * j;
+      if (live[j] && (v[j] > bv || (v[j] == bv && e < bi))) {
+        bv = v[j];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 16);
+      const int oi = __shfl_xor(bi, o, 16);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      if (sub + 16 * j == bi) live[j] = false;
+    psel[k] = expf(bv - m) / s;
+    isel[k] = bi;
+  }
+  if (sub != 0) return;
+  int kd = K;
+  if (kmin > 0) {
+    const float hn = E > 1 ? hs / logf(static_cast<float>(E)) : 0.f;
+    const float kf = rintf(static_cast<float>(kmin) + static_cast<float>(K - kmin) * hn);
+    kd = static_cast<int>(fminf(fmaxf(kf, static_cast<float>(kmin)), static_cast<float>(K)));
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k < K) {
+      psel[k] = k < kd ? psel[k] : 0.f;
+      sum += psel[k];
+    }
+  }
+  const bool norm = kmin > 0 || renorm;
+  const float denom = kmin > 0 ? fmaxf(sum, 1e-9f) : sum;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k < K) {
+      w_out[k] = norm ? psel[k] / denom : psel[k];
+      id_out[k] = isel[k];
+    }
+  }
+}
+
+template <typename T>
+struct Mfma16R;
+
+template <>
+struct Mfma16R<bf16> {
+  __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma16R<f16> {
+  __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// Prefill-sized router on MFMA: 16 tokens per workgroup, the 4 waves splitting
+// H in quarters. Each wave multiplies its 16 token rows (A, 16 x 32 per step)
+// by 16-expert groups of gate rows (B) with v_mfma_f32_16x16x32, operands
+// loaded straight from global memory in MFMA layout (lane l: row l % 16, k
+// chunk l / 16); the 4 quarter sums are added in fixed order through LDS.
+// Lane l then holds logits of tokens 4 (l / 16) + 0..3 for expert l % 16 of
+// each group. A group of 16 lanes per token does the softmax and top-k
+// (group16_topk).
+// The fp32 VALU router re-reads the gate per 8 tokens and spends E*H FMAs per
+// token on the VALU: at 4096 tokens, 64 experts and H = 2048 it took 54 us.
+template <typename T, int NG>
+__global__ __launch_bounds__(kThreads) void router_mfma_kernel(const RouterArgs a) {
+  constexpr int kTok = 16, EP = 16 * NG;
+  __shared__ float part[kThreads / kWave][kTok][EP];
+  __shared__ float lg[kTok][EP];
+  const int t0 = blockIdx.x * kTok;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int r = lane & 15, kq = lane >> 4;
+  const int hq = a.H / 4;
+  const T* xr = static_cast<const T*>(a.x) + static_cast<size_t>(min(t0 + r, a.T - 1)) * a.H +
+                wave * hq + kq * 8;
+  const T* gr[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+    gr[g] = static_cast<const T*>(a.gate) + static_cast<size_t>(min(16 * g + r, a.E - 1)) * a.H +
+            wave * hq + kq * 8;
+  f32x4 acc[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // U k-steps per batch, all their loads issued before the first MFMA (no
+  // exit inside a batch: a conditional exit let the compiler wait for each
+  // step's loads in turn); the remainder runs one step at a time.
+  constexpr int U = NG == 1 ? 8 : 4;
+  auto batch = [&](int k, auto uc) {
+    constexpr int NU = decltype(uc)::value;
+    u32x4 av[NU], bv[NU][NG];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      av[u] = *reinterpret_cast<const u32x4*>(xr + k + 32 * u);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) bv[u][g] = *reinterpret_cast<const u32x4*>(gr[g] + k + 32 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) acc[g] = Mfma16R<T>::mma(av[u], bv[u][g], acc[g]);
+  };
+  int k = 0;
+  for (; k + 32 * U <= hq; k += 32 * U) batch(k, std::integral_constant<int, U>{});
+  for (; k < hq; k += 32) batch(k, std::integral_constant<int, 1>{});
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[wave][4 * kq + i][16 * g + r] = acc[g][i];
+  __syncthreads();
+  for (int i = tid; i < kTok * EP; i += kThreads) {
+    const int t = i / EP, e = i % EP;
+    if (t0 + t < a.T && e < a.E) {
+      float l = (part[0][t][e] + part[1][t][e]) + (part[2][t][e] + part[3][t][e]);
+      if (a.round_logits) l = to_f32(from_f32<T>(l));
+      if (a.bias) l += a.bias[e];
+      lg[t][e] = l;
+      if (a.logits_out) a.logits_out[static_cast<size_t>(t0 + t) * a.E + e] = l;
+    }
+  }
+  __syncthreads();
+  // 16 lanes per token (tid = 16 t + sub).
+  const int tt = tid / 16;
+  if (t0 + tt < a.T)
+    group16_topk<NG>(lg[tt], a.E, a.K, a.renormalize, a.entropy_k_min,
+                     a.topk_w + static_cast<size_t>(t0 + tt) * a.out_ld,
+                     a.topk_ids + static_cast<size_t>(t0 + tt) * a.out_ld, tid & 15);
+}
+
 // One wave per token on given fp32 logits.
 __global__ __launch_bounds__(kThreads) void topk_logits_kernel(const RouterArgs a) {
   __shared__ float psel[kThreads / kWave][kMaxExperts];
@@ -240,6 +432,20 @@ hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
   // for the workgroup's token count, so E = 64 at one token costs two passes
   // (two memory round trips) rather than eight.
   const dim3 block(kThreads);
+  if constexpr (!std::is_same<T, float>::value) {
+    // Prefill sizes on MFMA (16 tokens per workgroup); the VALU kernels keep
+    // the decode sizes, where one workgroup per token has the lowest latency.
+    if (a.T >= 1024 && a.K <= 8 && a.E <= 64 && a.H % 128 == 0) {
+      const dim3 grid((a.T + 15) / 16);
+      if (a.E <= 16)
+        router_mfma_kernel<T, 1><<<grid, block, 0, s>>>(a);
+      else if (a.E <= 32)
+        router_mfma_kernel<T, 2><<<grid, block, 0, s>>>(a);
+      else
+        router_mfma_kernel<T, 4><<<grid, block, 0, s>>>(a);
+      return hipGetLastError();
+    }
+  }
   if (a.T >= 1024)
     router_kernel<T, 8, 8><<<dim3((a.T + 7) / 8), block, 0, s>>>(a);
   else if (a.T >= 256 && a.E > 8)
