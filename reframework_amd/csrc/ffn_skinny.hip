@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kThreads) void ffn_skinny_kernel(const FfnArgs a) {
 template <bool kGateUp>
 hipError_t launch_skinny(const FfnArgs& a, int dtype, hipStream_t s) {
   if (a.n_wtiles == 0 || a.max_tiles == 0) return hipSuccess;
-  if (a.self_permute && (!kGateUp || a.perm.R > kWave)) return hipErrorInvalidValue;
+  if (a.self_permute && (!kGateUp || a.perm.R > kWave)) return hipErrorInvalidValue;  // one wave groups
   const dim3 grid((a.n_wtiles + kWavesPerBlock - 1) / kWavesPerBlock, a.max_tiles, a.splits);
   if (a.self_permute) {
     if (dtype == MOE355_BF16)

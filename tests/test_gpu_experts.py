@@ -75,14 +75,20 @@ def test_permute_bit_exact(T, K, E, ids64, drop, dev):
 
 
 @pytest.mark.parametrize("T,K,E,ids64,drop", [
-    (1, 2, 8, False, False), (16, 2, 8, True, True), (32, 2, 8, False, False),
-    (8, 6, 64, True, False), (8, 8, 256, True, True), (3, 6, 64, False, True),
+    # grouped inside gate_up (<= 16 slots over <= 32 experts)
+    (1, 2, 8, False, False), (8, 2, 8, True, True), (4, 4, 32, False, True),
+    (5, 3, 16, True, False), (2, 8, 32, False, False),
+    # permute launch, same checks
+    (16, 2, 8, True, True), (32, 2, 8, False, False), (8, 6, 64, True, False),
+    (8, 8, 256, True, True), (3, 6, 64, False, True),
 ])
 def test_decode_grouping_inside_gate_up_bit_exact(T, K, E, ids64, drop, dev):
-    """At decode sizes (skinny path, <= 64 routed slots) fused_experts skips
-    the permute launch: the gate_up workgroups group the slots themselves and
-    workgroup 0 writes the permute's outputs. Those outputs must equal the
-    oracle's grouping bit for bit, and the layer output the staged path's."""
+    """At decode sizes (skinny path, <= 16 routed slots over <= 32 experts)
+    fused_experts skips the permute launch: the gate_up workgroups group the
+    slots themselves and workgroup 0 writes the permute's outputs. Those
+    outputs must equal the oracle's grouping bit for bit, and the layer output
+    the staged path's (larger cases take the permute launch and are held to
+    the same checks)."""
     H, I = 256, 256
     banner(f"decode grouping in gate_up T={T} K={K} E={E} ids64={ids64} drop={drop}")
     ids = skewed_ids(T, K, E, seed=T * E + K, skew=1.2)
