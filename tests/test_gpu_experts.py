@@ -87,8 +87,8 @@ def test_decode_grouping_inside_gate_up_bit_exact(T, K, E, ids64, drop, dev):
     fused_experts skips the permute launch: the gate_up workgroups group the
     slots themselves and workgroup 0 writes the permute's outputs. Those
     outputs must equal the oracle's grouping bit for bit, and the layer output
-    the staged path's (larger cases take the permute launch and are held to
-    the same checks)."""
+    (also accumulated into fp32) the staged path's (larger cases take the
+    permute launch and are held to the same checks)."""
     H, I = 256, 256
     banner(f"decode grouping in gate_up T={T} K={K} E={E} ids64={ids64} drop={drop}")
     ids = skewed_ids(T, K, E, seed=T * E + K, skew=1.2)
@@ -130,6 +130,16 @@ def test_decode_grouping_inside_gate_up_bit_exact(T, K, E, ids64, drop, dev):
     assert torch.equal(out, staged)
     if not drop:
         _check(out, x.cpu(), w1, w2, tw.cpu().numpy(), ids)
+    # accumulate into an fp32 output (the streaming layer's mode): the same sums
+    base = torch.randn(T, H, generator=torch.Generator().manual_seed(7)).to(dev)
+    acc_f, acc_s = base.clone(), base.clone()
+    _capi.fused_experts(x, p1, p2, I, tw, idt, 0, acc_f, ws, expert_map=emap, accumulate_f32=True)
+    _capi.permute(plan, idt, ws2, expert_map=emap)
+    _capi.gate_up(plan, x, p1, 0, ws2)
+    _capi.down(plan, p2, ws2)
+    _capi.combine(plan, tw, acc_s, True, ws2)
+    torch.cuda.synchronize()
+    assert torch.equal(acc_f, acc_s)
 
 
 # ------------------------------------------------------------ expert FFN
