@@ -11,8 +11,10 @@ sampled tokens (the first and last token of every expert group, whose rows
 sit in the first and last tiles, plus random ones) with the fp64 oracle:
   * <= 2e-2 max-relative against the fp64 oracle;
   * <= 4e-3 against the oracle that rounds the intermediate like the kernels.
-The full-size case is the Mixtral-8x7B layer (H=4096, I=14336, E=8, K=2) at
-T=4096, the prefill workload the throughput figures are quoted on.
+The full-size cases are the Mixtral-8x7B layer (H=4096, I=14336, E=8, K=2) at
+T=4096 and 256, the Phi-3.5-MoE layer at T=2048 with Zipf-skewed routing, and
+the fine-grained layer (64 experts top-6 plus 2 shared) at T=4096: the shapes
+the throughput figures are quoted on.
 """
 
 from __future__ import annotations
@@ -164,3 +166,40 @@ def test_mixtral_t256_sampled_tokens(dev):
     w = rng.random((T, K)).astype(np.float32)
     out = gpu_fused(x, w1, w2, w, ids)
     _check_sampled(out, x, w1, w2, w, ids, _sample_tokens(ids, 8, seed=6))
+
+
+def test_phi35_t2048_sampled_tokens(dev):
+    """Phi-3.5-MoE-shape layer (H=4096, I=6400, E=16, K=2) at 2048 tokens with
+    Zipf-skewed routing: the ragged groups of the bench's Phi config (some
+    experts a fraction of a 256-row tile, others several tiles)."""
+    T, H, I, E, K = 2048, 4096, 6400, 16, 2
+    rng = np.random.default_rng(21)
+    pop = 1.0 / np.arange(1, E + 1) ** 1.1
+    scores = np.log(pop)[None, :] + rng.gumbel(size=(T, E))
+    ids = np.argsort(-scores, axis=1)[:, :K].astype(np.int64)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    plan = _capi.make_plan(T, H, I, E, K, _capi.BF16)
+    banner(f"phi-3.5 T={T} path={plan.path} counts={counts.tolist()}")
+    assert plan.path == _capi.PATH_MFMA_TILED
+    w1, w2 = _bank(E, H, I, torch.bfloat16, seed=23, dev=dev, scale=0.02)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    w = rng.random((T, K)).astype(np.float32)
+    out = gpu_fused(x, w1, w2, w, ids)
+    _check_sampled(out, x, w1, w2, w, ids, _sample_tokens(ids, 8, seed=7))
+
+
+def test_finegrained_t4096_with_shared_columns_sampled_tokens(dev):
+    """Fine-grained layer (H=2048, I=1408, 64 routed experts top-6 plus 2
+    shared experts folded in as two always-routed columns) at 4096 tokens."""
+    T, H, I, E, K = 4096, 2048, 1408, 66, 8
+    rng = np.random.default_rng(31)
+    routed = np.argsort(rng.random((T, 64)), axis=1)[:, :6]
+    ids = np.concatenate([routed, np.full((T, 1), 64), np.full((T, 1), 65)], axis=1).astype(np.int64)
+    plan = _capi.make_plan(T, H, I, E, K, _capi.BF16)
+    banner(f"fine-grained T={T} path={plan.path} down_splits={plan.down_splits}")
+    assert plan.path == _capi.PATH_MFMA_TILED
+    w1, w2 = _bank(E, H, I, torch.bfloat16, seed=33, dev=dev, scale=0.02)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    w = np.concatenate([rng.random((T, 6)), np.ones((T, 2))], axis=1).astype(np.float32)
+    out = gpu_fused(x, w1, w2, w, ids)
+    _check_sampled(out, x, w1, w2, w, ids, _sample_tokens(ids, 8, seed=9))
