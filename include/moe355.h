@@ -55,7 +55,7 @@ extern "C" {
 #define MOE355_PATH_MFMA_TILED 0 /* 256x256 bf16/f16 MFMA tiles, prefill-sized groups */
 #define MOE355_PATH_MFMA_SKINNY 1 /* weight-streaming 16x16x32 MFMA, decode-sized groups */
 #define MOE355_PATH_SIMT 2        /* fp32 FMA tiles: fp32 layers and unaligned shapes */
-#define MOE355_PATH_MFMA_MEDIUM 3 /* 256x64 bf16/f16 MFMA tiles, medium groups */
+#define MOE355_PATH_MFMA_MEDIUM 3 /* 256x64 bf16/f16 MFMA tiles (chosen only when forced) */
 #define MOE355_PATH_MFMA_TILED128 4 /* the 256x256 kernel on 128-row token tiles, groups of ~128 rows */
 
 /* Execution plan of one fused_experts call. Filled by moe355_make_plan() from
@@ -154,7 +154,10 @@ int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renorm
 
 /* Fill `plan` for a fused_experts call of this shape. Host-side; reads the
  * current device's CU count (256 without a device) to choose the down
- * projection's K-split, and launches nothing. */
+ * projection's K-split, and launches nothing. The kernel family follows the
+ * average rows per active expert (T*K / min(T*K, E)): up to 10 skinny, up to
+ * 104 the tiled kernel on 128-row tiles, above it 256-row tiles; fp32 and
+ * shapes the MFMA kernels do not tile take the SIMT family. */
 int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* plan);
 
 /* moe355_make_plan with the kernel family forced (`path` = MOE355_PATH_*, or -1
