@@ -76,7 +76,9 @@ typedef struct moe355_plan {
   size_t off_row_src;      /* int32 [T*K]    source token of each permuted row */
   size_t off_tile_map;     /* int32 [2 + 2*max_tiles]: count, 0, then (expert, first_row) pairs */
   size_t off_inter;        /* dtype [T*K, I] silu(gate)*up per permuted row */
-  size_t off_y;            /* fp32  [down_splits, T*K, H] down-projection partials */
+  size_t off_y;            /* fp32  [down_splits, T*K, H] down-projection partials; for the
+                              tiled paths with down_splits == 1, dtype [T*K, H] (rounded to
+                              the layer dtype, as the reference's bf16 matmul returns it) */
   size_t off_part;         /* fp32 256x256 partial tiles of the tiled down projection's K-split
                               last-round items, up to one per CU (empty for the other paths) */
 } moe355_plan;
@@ -199,7 +201,8 @@ int moe355_down(const moe355_plan* plan, const void* const* w2, void* workspace,
 /*
  * Weighted combine back to token order:
  *   out[t] = sum_k topk_w[t,k] * sum_s y[s, slot_to_row[t*K+k]]   (dropped slots skipped)
- * accumulated in fp32, k ascending. Replaces `y * w; out.index_add_(0, tok, y)`
+ * accumulated in fp32, k ascending, y read in the format the plan's down
+ * projection writes (see off_y). Replaces `y * w; out.index_add_(0, tok, y)`
  * (reframework/moe/fused.py:84-86). With accumulate_f32 = 0, out has the plan
  * dtype and is overwritten; with 1, out is fp32 and the sum is added to it (the
  * fp32 accumulator of FusedMoE._forward_streaming, moe_layer.py:370,415).

@@ -252,13 +252,15 @@ int oracle_permute(const int64_t* ids, int T, int K, int E, const int32_t* map, 
 /* out[t] = sum_k w[t,k] * down_e(act(gate_e x_t) * up_e x_t), e = ids[t,k],
  * all in fp64. w1[e] is [2I,H] (gate rows first), w2[e] is [H,I], given as
  * per-expert pointers of `w_type` elements. inter_round rounds the activated
- * intermediate to the product's storage type (0 none, 1 bf16, 2 f16, 3 f32).
+ * intermediate to the product's storage type (0 none, 1 bf16, 2 f16, 3 f32);
+ * y_round likewise rounds each slot's down-projection output y before it is
+ * weighted (fused.py:83: `y = inter @ w2[e].t()` returns the model dtype).
  * Slots with id outside [0,E) contribute nothing. tokens (optional) restricts
  * the computation to the listed token indices (others left untouched). */
 int oracle_fused_experts(const void* x, int x_type, const void* const* w1, const void* const* w2,
                          int w_type, const float* topk_w, const int64_t* ids, int T, int H, int I,
-                         int E, int K, int act, int inter_round, const int32_t* tokens,
-                         int n_tokens, double* out) {
+                         int E, int K, int act, int inter_round, int y_round,
+                         const int32_t* tokens, int n_tokens, double* out) {
   const int n = tokens ? n_tokens : T;
   init_half_table();
 #pragma omp parallel
@@ -282,7 +284,8 @@ int oracle_fused_experts(const void* x, int x_type, const void* const* w1, const
           const double u = dot_row(w1[e], (size_t)(I + i) * H, w_type, xr, H);
           inter[i] = round_to(gate_act(act, g) * u, inter_round);
         }
-        for (int h = 0; h < H; ++h) o[h] += wt * dot_row(w2[e], (size_t)h * I, w_type, inter, I);
+        for (int h = 0; h < H; ++h)
+          o[h] += wt * round_to(dot_row(w2[e], (size_t)h * I, w_type, inter, I), y_round);
       }
     }
     free(xr);

@@ -43,7 +43,7 @@ def lib() -> ctypes.CDLL:
         h.oracle_permute.argtypes = [P, I, I, I, P, I, P, P, P]
         h.oracle_permute.restype = I
         h.oracle_fused_experts.argtypes = [P, I, ctypes.POINTER(P), ctypes.POINTER(P), I, P, P,
-                                           I, I, I, I, I, I, I, P, I, P]
+                                           I, I, I, I, I, I, I, I, P, I, P]
         h.oracle_fused_experts.restype = I
         h.oracle_round.argtypes = [P, ctypes.c_size_t, I]
         h.oracle_round.restype = None
@@ -116,8 +116,12 @@ def permute(ids: np.ndarray, E: int, expert_map: Optional[Sequence[int]] = None)
 def fused_experts(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch.Tensor],
                   topk_w: np.ndarray, ids: np.ndarray, activation: int = 0,
                   inter_round: int = ROUND_NONE,
-                  tokens: Optional[Sequence[int]] = None) -> np.ndarray:
-    """fp64 [T,H] output of the routed experts (rows outside ``tokens`` are 0)."""
+                  tokens: Optional[Sequence[int]] = None,
+                  y_round: int = ROUND_NONE) -> np.ndarray:
+    """fp64 [T,H] output of the routed experts (rows outside ``tokens`` are 0).
+    ``inter_round`` / ``y_round`` round the activated intermediate / each
+    slot's down-projection output to a storage type, as the reference's
+    model-dtype matmuls do (fused.py:80-83)."""
     xt, tx = _raw(x)
     w1c = [_raw(w)[0] for w in w1]
     w2c = [_raw(w)[0] for w in w2]
@@ -134,7 +138,7 @@ def fused_experts(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torc
     out = np.zeros((T, H), dtype=np.float64)
     tok = None if tokens is None else np.ascontiguousarray(tokens, dtype=np.int32)
     lib().oracle_fused_experts(xt.data_ptr(), tx, p1, p2, tw, tw_arr.ctypes.data,
-                               id_arr.ctypes.data, T, H, I, E, K, activation, inter_round,
+                               id_arr.ctypes.data, T, H, I, E, K, activation, inter_round, y_round,
                                None if tok is None else tok.ctypes.data,
                                0 if tok is None else len(tok), out.ctypes.data)
     return out

@@ -417,6 +417,16 @@ int gate_up_impl(const moe355_plan* p, const void* x, const void* const* w1, int
   return check_hip(err, "gate_up launch");
 }
 
+// Whether the down projection leaves y in the layer dtype ([rows, H], one
+// plane) rather than fp32 split partials: the tiled kernels with one K-split.
+// This is the reference's own rounding (its `inter @ w2[e].t()` returns the
+// model dtype) and halves the y traffic of down and combine. Split partials
+// stay fp32 (their sum is rounded once, by the combine).
+bool y_narrow(const moe355_plan* p) {
+  return (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_TILED128) &&
+         p->down_splits == 1 && p->dtype != MOE355_F32;
+}
+
 }  // namespace
 
 extern "C" {
@@ -440,6 +450,7 @@ int moe355_down(const moe355_plan* p, const void* const* w2, void* workspace, vo
   if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_TILED128) {
     a.n_wtiles = p->H / 256;
     a.tile_rows = p->tile_rows;
+    a.y16 = y_narrow(p);
     // Partial tiles of the K-split last-round items (256x256 fp32 each).
     a.part = at<float>(workspace, p->off_part);
     a.part_units = p->workspace_bytes > p->off_part
@@ -473,6 +484,7 @@ int moe355_combine(const moe355_plan* p, const float* topk_w, void* out, int acc
   a.out = out;
   a.T = p->T; a.K = p->K; a.H = p->H; a.R = p->rows; a.splits = p->down_splits;
   a.accumulate = accumulate_f32 != 0;
+  a.y16 = y_narrow(p);
   return check_hip(launch_combine(a, p->dtype, as_stream(stream)), "combine launch");
 }
 

@@ -4,7 +4,8 @@
 // (reframework/moe/fused.py:84-86). Every token owns one workgroup and reads
 // its K permuted rows (summing the down-projection K-splits on the way), so
 // there are no atomics and the k order is fixed: results are deterministic.
-// HBM bound: T*K*H*4*S bytes in, T*H*elem out.
+// HBM bound: T*K*H*4*S bytes in (T*K*H*elem when y is in the layer dtype),
+// T*H*elem out.
 #include "common.h"
 
 namespace moe355 {
@@ -12,11 +13,26 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Workgroup (t, hb) produces out[t, hb*1024 .. +1024): each thread one
-// 16-byte group of 4 features. The K slots' rows and weights are uniform per
-// workgroup; the S split partials of every slot are issued as independent
-// loads, so a decode-size combine costs one round trip, not S*K of them.
-template <typename OutT, int S>
+// Four consecutive y elements as fp32.
+template <typename Y>
+__device__ __forceinline__ f32x4 load4(const Y* p) {
+  const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+  float o[8];
+  Vec16<Y>::unpack(u32x4{v.x, v.y, 0u, 0u}, o);
+  return f32x4{o[0], o[1], o[2], o[3]};
+}
+
+template <>
+__device__ __forceinline__ f32x4 load4<float>(const float* p) {
+  return *reinterpret_cast<const f32x4*>(p);
+}
+
+// Workgroup (t, hb) produces out[t, hb*1024 .. +1024): each thread one group
+// of 4 features. The K slots' rows and weights are uniform per workgroup; the
+// S split partials of every slot are issued as independent loads, so a
+// decode-size combine costs one round trip, not S*K of them. Y is fp32 for
+// split partials, or the layer dtype (one split, y16).
+template <typename OutT, typename Y, int S>
 __global__ __launch_bounds__(kThreads) void combine_kernel(const CombineArgs a) {
   const int t = blockIdx.x;
   const int h = (blockIdx.y * kThreads + threadIdx.x) * 4;
@@ -27,10 +43,10 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const CombineArgs a) 
     const int row = a.slot_to_row[t * a.K + k];
     if (row < 0) continue;
     const float w = a.topk_w[t * a.K + k];
-    const float* yr = a.y + static_cast<size_t>(row) * a.H + h;
+    const Y* yr = static_cast<const Y*>(a.y) + static_cast<size_t>(row) * a.H + h;
     f32x4 part[S];
 #pragma unroll
-    for (int s = 0; s < S; ++s) part[s] = *reinterpret_cast<const f32x4*>(yr + s * plane);
+    for (int s = 0; s < S; ++s) part[s] = load4<Y>(yr + s * plane);
     f32x4 ys = part[0];
 #pragma unroll
     for (int s = 1; s < S; ++s) ys += part[s];
@@ -53,14 +69,22 @@ __global__ __launch_bounds__(kThreads) void cast_kernel(const float* src, OutT* 
 }
 
 template <typename OutT>
-hipError_t launch_combine_t(const CombineArgs& a, hipStream_t s) {
+hipError_t launch_combine_t(const CombineArgs& a, int dtype, hipStream_t s) {
   const dim3 grid(a.T, (a.H + kThreads * 4 - 1) / (kThreads * 4)), block(kThreads);
+  if (a.y16) {
+    if (a.splits != 1 || dtype == MOE355_F32) return hipErrorInvalidValue;
+    if (dtype == MOE355_BF16)
+      combine_kernel<OutT, bf16, 1><<<grid, block, 0, s>>>(a);
+    else
+      combine_kernel<OutT, f16, 1><<<grid, block, 0, s>>>(a);
+    return hipGetLastError();
+  }
   switch (a.splits) {
-    case 1: combine_kernel<OutT, 1><<<grid, block, 0, s>>>(a); break;
-    case 2: combine_kernel<OutT, 2><<<grid, block, 0, s>>>(a); break;
-    case 4: combine_kernel<OutT, 4><<<grid, block, 0, s>>>(a); break;
-    case 8: combine_kernel<OutT, 8><<<grid, block, 0, s>>>(a); break;
-    case 16: combine_kernel<OutT, 16><<<grid, block, 0, s>>>(a); break;
+    case 1: combine_kernel<OutT, float, 1><<<grid, block, 0, s>>>(a); break;
+    case 2: combine_kernel<OutT, float, 2><<<grid, block, 0, s>>>(a); break;
+    case 4: combine_kernel<OutT, float, 4><<<grid, block, 0, s>>>(a); break;
+    case 8: combine_kernel<OutT, float, 8><<<grid, block, 0, s>>>(a); break;
+    case 16: combine_kernel<OutT, float, 16><<<grid, block, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -68,11 +92,12 @@ hipError_t launch_combine_t(const CombineArgs& a, hipStream_t s) {
 
 }  // namespace
 
+// out_dtype is the layer dtype (the type of y when a.y16).
 hipError_t launch_combine(const CombineArgs& a, int out_dtype, hipStream_t s) {
   if (a.T == 0) return hipSuccess;
-  if (a.accumulate || out_dtype == MOE355_F32) return launch_combine_t<float>(a, s);
-  if (out_dtype == MOE355_BF16) return launch_combine_t<bf16>(a, s);
-  return launch_combine_t<f16>(a, s);
+  if (a.accumulate || out_dtype == MOE355_F32) return launch_combine_t<float>(a, out_dtype, s);
+  if (out_dtype == MOE355_BF16) return launch_combine_t<bf16>(a, out_dtype, s);
+  return launch_combine_t<f16>(a, out_dtype, s);
 }
 
 hipError_t launch_cast_f32(const float* src, void* dst, size_t n, int dtype, hipStream_t s) {

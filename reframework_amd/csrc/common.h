@@ -211,7 +211,7 @@ struct FfnArgs {
   const int32_t* row_src;  // [R]
   const int32_t* tile_map; // [2 + 2*max_tiles]
   const int32_t* offsets;  // [E+1]
-  void* out;               // gate_up: inter [R,I]; down: y [S,R,H] fp32
+  void* out;               // gate_up: inter [R,I]; down: y [S,R,H] fp32, or [R,H] in the layer dtype (y16)
   int H, I, R;
   int max_tiles, n_wtiles, splits, k_per_split;
   int act;
@@ -220,6 +220,7 @@ struct FfnArgs {
   int grid;                // workgroups of the tiled launch (the fix-up recomputes its split)
   int group_t;             // token tiles per item group (0: all; -1: one group per expert; see decode_tile)
   int tile_rows;           // token rows per tile of the tile map (tiled kernels: 256, or 128 for half tiles)
+  int y16;                 // tiled down with one K-split: y rounded to the layer dtype
   const void* w[kMaxExperts];  // w1[e] ([2I,H]) or w2[e] ([H,I])
   // Skinny gate_up only, when self_permute: every workgroup groups the <= 64
   // routed slots of perm itself (no permute launch), and workgroup 0 writes
@@ -240,12 +241,13 @@ struct NormArgs {
 };
 
 struct CombineArgs {
-  const float* y;            // [S,R,H]
+  const void* y;             // [S,R,H] fp32, or [R,H] in the layer dtype (y16)
   const float* topk_w;       // [T,K]
   const int32_t* slot_to_row;  // [T*K]
   void* out;                 // [T,H]
   int T, K, H, R, splits;
   int accumulate;
+  int y16;
 };
 
 // Compute units of the current device (256 when it cannot be queried, e.g. on a

@@ -466,7 +466,10 @@ void ffn_tiled_kernel(const FfnArgs a) {
       else
         epilogue(std::false_type{});
     } else {
-      float* y = static_cast<float*>(a.out) + static_cast<size_t>(ct.split) * a.R * a.H;
+      // y rows: fp32 partials of this item's K-split, or (y16: one split) the
+      // layer dtype, as the reference's bf16 `inter @ w2[e].t()` returns.
+      T* y16 = static_cast<T*>(a.out);
+      float* y32 = static_cast<float*>(a.out) + static_cast<size_t>(ct.split) * a.R * a.H;
   #pragma unroll
       for (int b = 0; b < 4; ++b) {
   #pragma unroll
@@ -476,8 +479,13 @@ void ffn_tiled_kernel(const FfnArgs a) {
   #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const int h = ct.wtile * kTileW + wave_w * 128 + b * 32 + 8 * q + 4 * ekh;
-              store4<float>(y + static_cast<size_t>(prow) * a.H + h, acc[b][j][4 * q],
-                            acc[b][j][4 * q + 1], acc[b][j][4 * q + 2], acc[b][j][4 * q + 3]);
+              const size_t o = static_cast<size_t>(prow) * a.H + h;
+              const float v0 = acc_read(acc[b][j][4 * q]), v1 = acc_read(acc[b][j][4 * q + 1]);
+              const float v2 = acc_read(acc[b][j][4 * q + 2]), v3 = acc_read(acc[b][j][4 * q + 3]);
+              if (a.y16)
+                store4<T>(y16 + o, v0, v1, v2, v3);
+              else
+                store4<float>(y32 + o, v0, v1, v2, v3);
             }
           }
           acc[b][j] = f32x16{};
@@ -534,9 +542,11 @@ __global__ __launch_bounds__(kThreads) void gate_up_tail_fixup(const FfnArgs a) 
 }
 
 // Sums the S partial tiles of each split tail item of the tiled down
-// projection into the item's fp32 y plane (its K-split), with the epilogue's
-// lane mapping. Task (item, b, j) covers weight block b against token block j
-// of every wave: 16 KB read per part, 16 KB of y written at most.
+// projection into the item's y plane (its K-split; Y = the layer dtype when
+// y16), with the epilogue's lane mapping. Task (item, b, j) covers weight
+// block b against token block j of every wave: 16 KB read per part, 16 KB of
+// y written at most.
+template <typename Y>
 __global__ __launch_bounds__(kThreads) void down_tail_fixup(const FfnArgs a) {
   const int n_t = a.tile_map[0];
   const int per_split = a.n_wtiles * n_t;
@@ -557,11 +567,11 @@ __global__ __launch_bounds__(kThreads) void down_tail_fixup(const FfnArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[q] += pp[((b * 4 + j) * 4 + q) * kWave];
     }
-    float* y = static_cast<float*>(a.out) + static_cast<size_t>(t.split) * a.R * a.H;
+    Y* y = static_cast<Y*>(a.out) + static_cast<size_t>(t.split) * a.R * a.H;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int h = t.wtile * kTileW + wave_w * 128 + b * 32 + 8 * q + 4 * kh;
-      store4<float>(y + static_cast<size_t>(prow) * a.H + h, v[q][0], v[q][1], v[q][2], v[q][3]);
+      store4<Y>(y + static_cast<size_t>(prow) * a.H + h, v[q][0], v[q][1], v[q][2], v[q][3]);
     }
   }
 }
@@ -591,8 +601,12 @@ hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   if (err != hipSuccess || a.part_units == 0) return err;
   // The split depends on the device-side tile count; without a tail the
   // fix-up finds no task and exits.
-  if (!kGateUp)
-    down_tail_fixup<<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+  if (!kGateUp && !a.y16)
+    down_tail_fixup<float><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+  else if (!kGateUp && dtype == MOE355_BF16)
+    down_tail_fixup<bf16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+  else if (!kGateUp)
+    down_tail_fixup<f16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else if (dtype == MOE355_BF16)
     gate_up_tail_fixup<bf16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else

@@ -125,6 +125,30 @@ def test_inter_rounding_modes_bound_the_difference():
     assert 0 < oracle.max_rel(rh, exact) < 2 ** -10
 
 
+def test_y_rounding_applies_per_slot_before_the_weight():
+    """y_round rounds each slot's down-projection output, then weights it: with
+    one slot, out = w * round(y), where y is the unweighted, unrounded output."""
+    E, H, I, T = 3, 64, 48, 8
+    w1, w2 = _layer(E, H, I)
+    x = torch.randn(T, H)
+    ids = np.array([[1]] * T, np.int64)
+    y = oracle.fused_experts(x, w1, w2, np.ones((T, 1), np.float32), ids)
+    wt = np.float32(0.3)
+    for mode in (oracle.ROUND_BF16, oracle.ROUND_F16):
+        got = oracle.fused_experts(x, w1, w2, np.full((T, 1), wt, np.float32), ids, y_round=mode)
+        assert np.array_equal(got, float(wt) * oracle.round_array(y, mode))
+        # rounding after the weight (or not at all) would differ
+        assert not np.array_equal(got, oracle.round_array(float(wt) * y, mode))
+    # two slots: the sum of the two rounded, weighted slot outputs
+    ids2 = np.array([[1, 2]] * T, np.int64)
+    w2s = np.array([[0.25, 0.75]] * T, np.float32)
+    got = oracle.fused_experts(x, w1, w2, w2s, ids2, y_round=oracle.ROUND_BF16)
+    ya = oracle.fused_experts(x, w1, w2, np.ones((T, 1), np.float32), ids2[:, :1])
+    yb = oracle.fused_experts(x, w1, w2, np.ones((T, 1), np.float32), ids2[:, 1:])
+    want = 0.25 * oracle.round_array(ya, oracle.ROUND_BF16) + 0.75 * oracle.round_array(yb, oracle.ROUND_BF16)
+    assert np.allclose(got, want, rtol=0, atol=1e-15)
+
+
 def test_round_array_matches_torch_casts():
     v = np.random.default_rng(4).normal(size=1000) * 10
     v32 = v.astype(np.float32).astype(np.float64)
