@@ -55,7 +55,7 @@ extern "C" {
 #define MOE355_PATH_MFMA_TILED 0 /* 256x256 bf16/f16 MFMA tiles, prefill-sized groups */
 #define MOE355_PATH_MFMA_SKINNY 1 /* weight-streaming 16x16x32 MFMA, decode-sized groups */
 #define MOE355_PATH_SIMT 2        /* fp32 FMA tiles: fp32 layers and unaligned shapes */
-#define MOE355_PATH_MFMA_MEDIUM 3 /* 256x64 bf16/f16 MFMA tiles (chosen only when forced) */
+/* 3 is unused (a 256x64-tile family that no workload chose was removed) */
 #define MOE355_PATH_MFMA_TILED128 4 /* the 256x256 kernel on 128-row token tiles, groups of ~128 rows */
 
 /* Execution plan of one fused_experts call. Filled by moe355_make_plan() from

@@ -24,7 +24,7 @@ HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__fil
 
 F32, BF16, F16 = 0, 1, 2
 ACT_CODES = {"silu": 0, "gelu": 1, "gelu_tanh": 2}
-PATH_MFMA_TILED, PATH_MFMA_SKINNY, PATH_SIMT, PATH_MFMA_MEDIUM, PATH_MFMA_TILED128 = 0, 1, 2, 3, 4
+PATH_MFMA_TILED, PATH_MFMA_SKINNY, PATH_SIMT, PATH_MFMA_TILED128 = 0, 1, 2, 4
 MAX_EXPERTS = 256
 
 _DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}

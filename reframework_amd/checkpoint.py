@@ -9,7 +9,9 @@ read lazily, tensor by tensor, from the ``*.safetensors`` files:
   * ``translate_key`` maps Mixtral / PhiMoE (``block_sparse_moe``, ``w1`` gate,
     ``w3`` up, ``w2`` down) and Qwen2-MoE (``shared_expert``) names onto the
     names FusedMoE uses (moe/moe_layer.py:631-660, plus
-    ``shared_experts.{gate,up,down}_proj`` for shared experts);
+    ``shared_experts.{gate,up,down}_proj`` for shared experts). A layer with
+    Qwen2-MoE's per-token ``shared_expert_gate`` is refused: FusedMoE's shared
+    experts are ungated, and loading it would silently drop the gate;
   * ``load_moe_layer`` copies one layer's router, experts and shared experts
     into a FusedMoE's parameters;
   * ``load_moe_layer_offload`` copies the router (and shared experts) into the
@@ -102,10 +104,24 @@ def _expert_keys(prefix: str, e: int) -> Tuple[str, str, str]:
     return (f"{p}.gate_proj.weight", f"{p}.up_proj.weight", f"{p}.down_proj.weight")
 
 
+def _reject_gated_shared_expert(index: SafetensorsIndex, prefix: str) -> None:
+    """Qwen2-MoE scales its shared expert's output per token by
+    sigmoid(x . shared_expert_gate); FusedMoE adds its shared experts with
+    weight 1 (the ungated form of litemoe/src/litemoe/model/model.py:192-195).
+    Loading such a layer would run without the gate and give wrong outputs,
+    so it is refused."""
+    gated = [k for k in _layer_keys(index, prefix) if ".shared_expert_gate." in k]
+    if gated:
+        raise ValueError(f"{prefix}: {gated[0]} gates the shared expert per token "
+                         "(Qwen2-MoE); FusedMoE adds shared experts ungated and cannot "
+                         "load this layer")
+
+
 def load_moe_layer(index: SafetensorsIndex, moe, prefix: str) -> LayerLoadReport:
     """Copy router, routed experts and shared experts of the layer at
     ``prefix`` (e.g. ``model.layers.3.mlp``) into ``moe``'s parameters, one
     tensor at a time."""
+    _reject_gated_shared_expert(index, prefix)
     rep = LayerLoadReport(prefix)
     expected = list(moe.state_dict(prefix=prefix).keys())
     for key in expected:
@@ -124,6 +140,7 @@ def load_moe_layer_offload(index: SafetensorsIndex, moe, prefix: str, device,
     """Router and shared experts into ``moe``; routed experts straight from the
     checkpoint into a new ExpertOffloadCache's host pool (``moe`` then runs
     in offload mode). Returns (cache, report)."""
+    _reject_gated_shared_expert(index, prefix)
     rep = LayerLoadReport(prefix)
     dense = [k for k in moe.state_dict(prefix=prefix).keys() if ".experts." not in k]
     for key in dense:

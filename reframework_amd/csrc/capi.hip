@@ -46,7 +46,8 @@ T* at(void* ws, size_t off) {
 int check_plan(const moe355_plan* p) {
   if (!p) return fail(MOE355_EINVAL, "plan is NULL");
   if (p->E < 1 || p->E > MOE355_MAX_EXPERTS || p->K < 1 || p->K > p->E || !valid_dtype(p->dtype) ||
-      p->path < 0 || p->path > MOE355_PATH_MFMA_TILED128 || p->rows != p->T * p->K)
+      p->path < 0 || p->path > MOE355_PATH_MFMA_TILED128 || p->path == 3 ||
+      p->rows != p->T * p->K)
     return fail(MOE355_EINVAL, "plan is not one filled by moe355_make_plan");
   return MOE355_OK;
 }
@@ -98,7 +99,7 @@ int moe355_make_plan(int T, int H, int I, int E, int K, int dtype, moe355_plan* 
 int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path,
                           moe355_plan* p) {
   if (!p) return fail(MOE355_EINVAL, "plan is NULL");
-  if (path < -1 || path > MOE355_PATH_MFMA_TILED128)
+  if (path < -1 || path > MOE355_PATH_MFMA_TILED128 || path == 3)
     return fail(MOE355_EINVAL, "unknown path %d", path);
   if (T < 0 || H <= 0 || I <= 0) return fail(MOE355_EINVAL, "bad sizes T=%d H=%d I=%d", T, H, I);
   if (E < 1 || E > MOE355_MAX_EXPERTS)
@@ -132,16 +133,15 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
     // Phi-3.5 and fine-grained shapes): weight streaming with 16-token tiles up
     // to 10 rows (beyond that each 16-row tile re-streams the weights), the
     // 256-row kernel on 128-row tiles up to 104 rows (Mixtral 64 and 256
-    // tokens: 0.55 and 0.59 ms against 0.56 and 0.65 with 256-row tiles and
-    // 0.56 and 0.74 with the 64-row kernel; fine-grained 512 tokens 0.31
-    // against 0.32 and 0.35), 256-row tiles above (Mixtral 512 tokens: 0.67
-    // against 0.68 ms). The 64-row kernel stays available when forced.
+    // tokens: 0.55 and 0.59 ms against 0.56 and 0.65 with 256-row tiles;
+    // fine-grained 512 tokens 0.31 against 0.32), 256-row tiles above
+    // (Mixtral 512 tokens: 0.67 against 0.68 ms).
     path = tiled_ok && avg > 104  ? MOE355_PATH_MFMA_TILED
            : tiled_ok && avg > 10 ? MOE355_PATH_MFMA_TILED128
            : skinny_ok            ? MOE355_PATH_MFMA_SKINNY
                                   : MOE355_PATH_SIMT;
-  } else if (((path == MOE355_PATH_MFMA_TILED || path == MOE355_PATH_MFMA_TILED128 ||
-               path == MOE355_PATH_MFMA_MEDIUM) && !tiled_ok) ||
+  } else if (((path == MOE355_PATH_MFMA_TILED || path == MOE355_PATH_MFMA_TILED128) &&
+              !tiled_ok) ||
              (path == MOE355_PATH_MFMA_SKINNY && !skinny_ok)) {
     return fail(MOE355_EUNSUPPORTED, "path %d cannot run dtype %d with H=%d I=%d T=%d", path,
                 dtype, H, I, T);
@@ -156,18 +156,17 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
                                           p->tile_rows)
                        : 0;
   p->down_splits = 1;
-  if (tiled || p->path == MOE355_PATH_MFMA_MEDIUM) {
+  if (tiled) {
     // The persistent down kernels run (H/256 weight tiles x token tiles x
     // splits) work items of I/(32*splits) 32-k steps on one workgroup per CU.
     // Pick the split that minimises the busiest CU's step count, charging each
     // extra split its fp32 partial plane (written once, read by the combine)
-    // at ~1.8e-6 steps per element; ties keep fewer splits. The 256-row
-    // kernel cuts a partly idle last round along K (work_split, same rule),
-    // so its last round costs what that cut leaves.
-    // Each split must be a whole number of pipeline steps: 64 k for the
-    // 256-row kernel, 32 k for the 64-row one. Token tiles are estimated per
-    // active expert as its average rows over the tile height plus half a tile
-    // for the ragged end, at least one (Mixtral 4096 tokens: 36, as routed;
+    // at ~1.8e-6 steps per element; ties keep fewer splits. The kernel cuts a
+    // partly idle last round along K (work_split, same rule), so its last
+    // round costs what that cut leaves. Each split must be a whole number of
+    // 64-k pipeline steps. Token tiles are estimated per active expert as its
+    // average rows over the tile height plus half a tile for the ragged end,
+    // at least one (Mixtral 4096 tokens: 36, as routed;
     // 128 and 256 tokens on 128-row tiles: 8): max_tiles is a worst case, and
     // sizing the split by it cut layers finer than their real tile count pays
     // for (Mixtral 256, 512 and 1024 tokens: down 0.201, 0.225 and 0.318 ms
@@ -178,13 +177,12 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
     const long long items =
         static_cast<long long>(H / 256) * static_cast<long long>(est_tiles + 0.5);
     const int cus = moe355::device_cu_count();
-    const int step_k = tiled ? 64 : 32;
     double best = 0.0;
-    for (int s = 1; s <= 8 && (I / step_k) % s == 0; s *= 2) {
+    for (int s = 1; s <= 8 && (I / 64) % s == 0; s *= 2) {
       const long long n = items * s, full = n / cus, tail = n % cus;
       const double per_item = static_cast<double>(I / 32 / s);
       double last = tail ? per_item : 0.0;
-      if (tiled && full > 0 && tail > 0) {
+      if (full > 0 && tail > 0) {
         const int nk = I / 64 / s;
         for (long long st = 2; st <= 16 && st * tail <= cus && nk % st == 0; st *= 2)
           last = std::min(last, 2.0 * (static_cast<double>(nk) / st + st * tail / 14.0));
@@ -400,9 +398,6 @@ int gate_up_impl(const moe355_plan* p, const void* x, const void* const* w1, int
     a.part_units = static_cast<int>(
         std::min<size_t>((p->workspace_bytes - p->off_y) / (256 * 256 * 4), 4096));
     err = launch_gate_up_tiled(a, p->dtype, as_stream(stream));
-  } else if (p->path == MOE355_PATH_MFMA_MEDIUM) {
-    a.n_wtiles = p->I / 128;
-    err = launch_gate_up_medium(a, p->dtype, as_stream(stream));
   } else if (p->path == MOE355_PATH_MFMA_SKINNY) {
     a.n_wtiles = p->I / 16;
     if (self) {
@@ -457,9 +452,6 @@ int moe355_down(const moe355_plan* p, const void* const* w2, void* workspace, vo
                        ? static_cast<int>((p->workspace_bytes - p->off_part) / (256 * 256 * 4))
                        : 0;
     err = launch_down_tiled(a, p->dtype, as_stream(stream));
-  } else if (p->path == MOE355_PATH_MFMA_MEDIUM) {
-    a.n_wtiles = p->H / 256;
-    err = launch_down_medium(a, p->dtype, as_stream(stream));
   } else if (p->path == MOE355_PATH_MFMA_SKINNY) {
     a.n_wtiles = p->H / 16;
     err = launch_down_skinny(a, p->dtype, as_stream(stream));

@@ -263,8 +263,6 @@ hipError_t launch_topk_from_logits(const RouterArgs& a, hipStream_t s);
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
 hipError_t launch_gate_up_tiled(const FfnArgs& a, int dtype, hipStream_t s);
 hipError_t launch_down_tiled(const FfnArgs& a, int dtype, hipStream_t s);
-hipError_t launch_gate_up_medium(const FfnArgs& a, int dtype, hipStream_t s);
-hipError_t launch_down_medium(const FfnArgs& a, int dtype, hipStream_t s);
 hipError_t launch_gate_up_skinny(const FfnArgs& a, int dtype, hipStream_t s);
 hipError_t launch_down_skinny(const FfnArgs& a, int dtype, hipStream_t s);
 hipError_t launch_gate_up_simt(const FfnArgs& a, int dtype, hipStream_t s);

@@ -1,24 +1,12 @@
-// Helpers shared by the LDS-pipelined MFMA kernels (ffn_tiled.hip,
-// ffn_medium.hip): 64-byte LDS rows swizzled in 16-byte chunks, direct-to-LDS
-// global loads, vmcnt-bounded workgroup barriers and the 32x32x16 MFMA.
+// Helpers of the LDS-pipelined MFMA grouped GEMM (ffn_tiled.hip): direct-to-LDS
+// buffer loads, vmcnt-bounded workgroup barriers, the 32x32x16 MFMA, the work
+// item decode and the tail split.
 #pragma once
 
 #include "common.h"
 
 namespace moe355 {
 namespace pipe {
-
-constexpr int kBK = 32;             // k elements per pipeline step
-constexpr int kRowBytes = kBK * 2;  // 64 B: 4 chunks of 16 B
-
-// Physical 16-byte chunk of logical chunk c (0..3) in LDS row r (64 B). Four
-// consecutive rows fill one 256-byte span of a 64-bank LDS; XOR with
-// (r >> 2) & 3 gives the four such spans of any 16 consecutive rows different
-// chunk columns, so 16 rows read at one logical chunk hit 16 distinct 16-byte
-// bank groups. The map is an involution.
-__device__ __forceinline__ uint32_t swz(int c, int r) {
-  return static_cast<uint32_t>(c ^ ((r >> 2) & 3));
-}
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(4))) int32_t const_i32;
@@ -53,11 +41,6 @@ __device__ __forceinline__ void dma_barrier() {
 __device__ __forceinline__ int opaque(int v) {
   asm volatile("" : "+v"(v));
   return v;
-}
-
-// One 1 KB direct-to-LDS load per wave: lane i's 16 bytes land at dst + 16 i.
-__device__ __forceinline__ void dma16(const void* src, uint8_t* dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void*)(dst), 16, 0, 0);
 }
 
 // Direct-to-LDS loads through a buffer resource over [base, base + 2 GB - 1):

@@ -153,13 +153,17 @@ class Prediction:
 class _Slot:
     """One HBM buffer holding an expert's w1 then w2, plus its stream events."""
 
-    __slots__ = ("buf", "w1", "w2", "ready", "free_after", "refs")
+    __slots__ = ("buf", "w1", "w2", "ready", "last_copy", "free_after", "refs")
 
     def __init__(self, buf: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor) -> None:
         self.buf = buf
         self.w1 = w1
         self.w2 = w2
         self.ready: Optional[torch.cuda.Event] = None  # copy into the slot finished
+        # The last copy into the slot, kept after release: a slot evicted
+        # before anything read it may still be filling on one layer's copy
+        # stream when another layer's copy stream takes it.
+        self.last_copy: Optional[torch.cuda.Event] = None
         self.free_after: Optional[torch.cuda.Event] = None  # last reader finished
         self.refs = 0
 
@@ -303,6 +307,10 @@ class ExpertOffloadCache:
         total = 0
         for s1, s2 in shapes:
             total += s1[0] * s1[1] + s2[0] * s2[1]
+        if self._copy_stream is not None:
+            # copies out of the pool being replaced must finish before the
+            # pinned allocator can reuse its pages
+            self._copy_stream.synchronize()
         try:
             buf = torch.empty(total, dtype=self.dtype, pin_memory=True)
             self._pinned = True
@@ -595,6 +603,12 @@ class ExpertOffloadCache:
         return make()
 
     def _release(self, slot: _Slot) -> None:
+        """Return a slot to the free list once its last holder lets go. Its
+        next copy (``_fill``, possibly on another layer's copy stream) waits
+        for ``free_after`` (every kernel queued so far on the compute stream,
+        the slot's readers among them) and for ``last_copy`` (the copy that
+        filled it, which nothing may have waited for if the slot was evicted
+        unread)."""
         slot.refs -= 1
         if slot.refs > 0:
             return
@@ -631,17 +645,25 @@ class ExpertOffloadCache:
             cs = self._side_stream()
             if slot.free_after is not None:
                 cs.wait_event(slot.free_after)
+            if slot.last_copy is not None:
+                cs.wait_event(slot.last_copy)
             src = self._host_buf.data_ptr() + self._host_off[idx] * self._host_buf.element_size()
             t0 = None
             if self._copy_log is not None:
                 t0 = torch.cuda.Event(enable_timing=True)
                 t0.record(cs)
             _capi.h2d_async(slot.buf.data_ptr(), src, nbytes, cs.cuda_stream)
+            # The copy is raw hipMemcpyAsync: tell torch's device allocator
+            # that the copy stream uses the slot, so a dropped slot's memory
+            # is not handed out again before the copy is done. (The host pool
+            # is only replaced after the copy stream drains: _alloc_pool.)
+            slot.buf.record_stream(cs)
             ev = torch.cuda.Event(enable_timing=t0 is not None)
             ev.record(cs)
             if t0 is not None:
                 self._copy_log.append((t0, ev, nbytes))
             slot.ready = ev
+            slot.last_copy = ev
             slot.refs = 1
             self._slot_of[idx] = slot
             self._lru[idx] = (slot.w1, slot.w2)

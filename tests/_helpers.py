@@ -99,3 +99,36 @@ def tiled_gate_up_split(plan: _capi.Plan, counts: Sequence[int], cus: int) -> in
     G = min(n_wtiles * plan.max_tiles, cus)
     cap = (plan.workspace_bytes - plan.off_y) // (256 * 256 * 4)
     return tail_split(n_wtiles * n_t, G, plan.H // 64, min(cap, 4096))[2]
+
+
+def y_round_of(plan: _capi.Plan, dt: torch.dtype) -> int:
+    """Rounding mode of each slot's down-projection output y under ``plan``:
+    the layer dtype on the tiled paths with one K-split (the reference's
+    model-dtype ``inter @ w2[e].t()``), none (fp32 y) on every other path."""
+    tiled = plan.path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128)
+    return ROUND[dt] if tiled and plan.down_splits == 1 and dt != torch.float32 else 0
+
+
+def _round_to(a: np.ndarray, dt: torch.dtype) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dt).float().numpy()
+
+
+def assert_y_rounding(got: np.ndarray, ref_expected: np.ndarray, ref_other: np.ndarray,
+                      dt: torch.dtype) -> None:
+    """The output follows the oracle with the plan's rounding of y, not the
+    other one: its RMS distance to ``ref_expected`` is below 0.95x that to
+    ``ref_other`` (an independent rounding of y adds a second error term of
+    about the size of the output's own rounding, ~0.7x expected). Skipped
+    where the two oracles round to the same outputs in the layer dtype (one
+    slot of weight 1 per token: rounding y and then the output is rounding
+    once)."""
+    if dt == torch.float32:
+        return
+    differ = np.mean(_round_to(ref_expected, dt) != _round_to(ref_other, dt))
+    if differ < 0.2:
+        return
+    d_exp = float(np.sqrt(np.mean((got - ref_expected) ** 2)))
+    d_oth = float(np.sqrt(np.mean((got - ref_other) ** 2)))
+    print(f"  y rounding: rms to expected {d_exp:.3e}, to the other {d_oth:.3e} "
+          f"(ratio {d_exp / max(d_oth, 1e-300):.3f}, outputs differing {differ:.2f})", flush=True)
+    assert d_exp < 0.95 * d_oth

@@ -72,7 +72,7 @@ def test_tiled_path_keeps_token_offsets_below_2gb():
 
 @pytest.mark.parametrize("T,K,E,tile,path", [(4096, 2, 8, 256, -1), (16, 2, 8, 16, -1),
                                              (8, 6, 64, 16, -1), (333, 3, 7, 64, -1),
-                                             (128, 2, 8, 128, -1), (777, 2, 5, 64, 3)])
+                                             (128, 2, 8, 128, -1), (777, 2, 5, 128, 4)])
 def test_tile_map_capacity_bounds_every_routing(T, K, E, tile, path):
     dtype = _capi.F32 if (tile == 64 and path < 0 and T == 333) else _capi.BF16
     H, I = (256, 256) if tile != 16 else (256, 128)
@@ -137,13 +137,13 @@ def test_zero_tokens_is_a_no_op():
 
 
 @pytest.mark.parametrize("path,tile", [(_capi.PATH_MFMA_TILED, 256), (_capi.PATH_MFMA_TILED128, 128),
-                                       (_capi.PATH_MFMA_MEDIUM, 64), (_capi.PATH_MFMA_SKINNY, 16),
+                                       (_capi.PATH_MFMA_SKINNY, 16),
                                        (_capi.PATH_SIMT, 64)])
 def test_forced_path_plans(path, tile):
     p = _capi.make_plan(300, 512, 384, 8, 2, _capi.BF16, path)
     assert p.path == path and p.tile_rows == tile
     assert p.max_tiles >= -(-600 // tile)
-    if path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128, _capi.PATH_MFMA_MEDIUM):
+    if path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128):
         assert (384 // 32) % p.down_splits == 0
 
 
@@ -151,13 +151,15 @@ def test_forced_path_rejects_shapes_it_cannot_run():
     lib = _capi.lib()
     plan = _capi.Plan()
     # fp32 has no MFMA family; H=384 is not a multiple of the 256-row weight tile
-    assert lib.moe355_make_plan_path(4, 256, 256, 8, 2, _capi.F32, _capi.PATH_MFMA_MEDIUM,
+    assert lib.moe355_make_plan_path(4, 256, 256, 8, 2, _capi.F32, _capi.PATH_MFMA_TILED,
                                      ctypes.byref(plan)) == -2
     assert lib.moe355_make_plan_path(4, 384, 256, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED,
                                      ctypes.byref(plan)) == -2
     assert lib.moe355_make_plan_path(4, 384, 256, 8, 2, _capi.BF16, _capi.PATH_MFMA_TILED128,
                                      ctypes.byref(plan)) == -2
     assert lib.moe355_make_plan_path(4, 256, 256, 8, 2, _capi.BF16, 7, ctypes.byref(plan)) == -1
+    # 3 was a removed family's number
+    assert lib.moe355_make_plan_path(4, 256, 256, 8, 2, _capi.BF16, 3, ctypes.byref(plan)) == -1
     assert "unknown path" in lib.moe355_last_error().decode()
 
 

@@ -126,3 +126,27 @@ def test_offload_load_requires_every_routed_expert(tmp_path):
 def test_missing_checkpoint_is_an_error(tmp_path):
     with pytest.raises(FileNotFoundError):
         SafetensorsIndex(tmp_path)
+
+
+@pytest.mark.parametrize("offload", [False, True])
+def test_qwen2_moe_shared_expert_gate_is_refused(tmp_path, offload):
+    """Qwen2-MoE gates its shared expert per token (sigmoid(x . g)); the
+    layer's shared experts are ungated, so such a checkpoint must not load
+    into it silently."""
+    H, I, E = 16, 8, 4
+    g = torch.Generator().manual_seed(2)
+    p = "model.layers.0.mlp"
+    sd = {f"{p}.gate.weight": torch.randn(E, H, generator=g),
+          f"{p}.shared_expert_gate.weight": torch.randn(1, H, generator=g)}
+    for e in range(E):
+        for n, shp in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+            sd[f"{p}.experts.{e}.{n}.weight"] = torch.randn(*shp, generator=g)
+    for n, shp in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+        sd[f"{p}.shared_expert.{n}.weight"] = torch.randn(*shp, generator=g)
+    save_file(sd, str(tmp_path / "m.safetensors"))
+    moe = FusedMoE(E, 2, H, I, dtype=torch.float32, n_shared_experts=1)
+    with pytest.raises(ValueError, match="shared_expert_gate"):
+        if offload:
+            load_moe_layer_offload(SafetensorsIndex(tmp_path), moe, p, "cpu", 2)
+        else:
+            load_moe_layer(SafetensorsIndex(tmp_path), moe, p)

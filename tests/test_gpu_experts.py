@@ -19,7 +19,8 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import DT, ROUND, banner, gpu_fused, make_bank, read_ws, skewed_ids
+from _helpers import (DT, ROUND, assert_y_rounding, banner, gpu_fused, make_bank, read_ws,
+                      skewed_ids, y_round_of)
 from oracle import oracle
 from reframework_amd import _capi
 from reframework_amd.moe import fused_experts
@@ -30,23 +31,30 @@ TOL_EXACT = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
 TOL_ROUNDED = {torch.float32: 1e-5, torch.bfloat16: 4e-3, torch.float16: 2e-3}
 
 
-def _check(out: torch.Tensor, x, w1, w2, w, ids, act=0, tokens=None):
+def _check(out: torch.Tensor, x, w1, w2, w, ids, act=0, tokens=None, path=-1):
+    """Output against the fp64 oracle and against the oracle that rounds the
+    intermediate, and y where the plan's kernels do (``path`` as given to
+    gpu_fused: the plan is rebuilt here to know which rounding applies)."""
     dt = w1[0].dtype
+    T, H = x.shape
+    plan = _capi.make_plan(T, H, w1[0].shape[0] // 2, len(w1), ids.shape[1],
+                           _capi.dtype_code(dt), path)
+    yr = y_round_of(plan, dt)
     got = out.float().cpu().numpy().astype(np.float64)
     exact = oracle.fused_experts(x, w1, w2, w, ids, activation=act, tokens=tokens)
     rounded = oracle.fused_experts(x, w1, w2, w, ids, activation=act, inter_round=ROUND[dt],
-                                   tokens=tokens)
-    # The tiled paths with one down K-split also round y to the layer dtype
-    # (as the reference's matmul does); the others keep it in fp32.
-    rounded_y = oracle.fused_experts(x, w1, w2, w, ids, activation=act, inter_round=ROUND[dt],
-                                     y_round=ROUND[dt], tokens=tokens)
+                                   y_round=yr, tokens=tokens)
+    other = oracle.fused_experts(x, w1, w2, w, ids, activation=act, inter_round=ROUND[dt],
+                                 y_round=0 if yr else ROUND[dt], tokens=tokens)
     if tokens is not None:
-        got, exact, rounded, rounded_y = got[tokens], exact[tokens], rounded[tokens], rounded_y[tokens]
+        got, exact, rounded, other = got[tokens], exact[tokens], rounded[tokens], other[tokens]
     e1 = oracle.max_rel(got, exact)
-    e2 = min(oracle.max_rel(got, rounded), oracle.max_rel(got, rounded_y))
-    print(f"  max_rel vs fp64 {e1:.2e}, vs rounded intermediate (and y) {e2:.2e}", flush=True)
+    e2 = oracle.max_rel(got, rounded)
+    print(f"  path {plan.path} splits {plan.down_splits}: max_rel vs fp64 {e1:.2e}, vs the "
+          f"oracle rounding inter{' and y' if yr else ''} {e2:.2e}", flush=True)
     assert e1 <= TOL_EXACT[dt]
     assert e2 <= TOL_ROUNDED[dt]
+    assert_y_rounding(got, rounded, other, dt)
 
 
 # ------------------------------------------------------------------ permute
@@ -206,7 +214,7 @@ def test_gelu_activations(act, T, dev):
                                             (1, 2, 8, 256, 256, 3), (2048, 2, 16, 512, 512, 4),
                                             (64, 1, 1, 256, 256, 5)])
 @pytest.mark.parametrize("path", [_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128,
-                                  _capi.PATH_MFMA_MEDIUM, _capi.PATH_MFMA_SKINNY])
+                                  _capi.PATH_MFMA_SKINNY])
 def test_every_mfma_family_on_every_shape(path, T, K, E, H, I, seed, dev):
     banner(f"forced path={path} T={T} K={K} E={E} H={H} I={I}")
     w1, w2 = make_bank(E, H, I, torch.bfloat16, seed=seed)
@@ -214,7 +222,7 @@ def test_every_mfma_family_on_every_shape(path, T, K, E, H, I, seed, dev):
     ids = skewed_ids(T, K, E, seed=seed, skew=1.1)
     w = np.random.default_rng(seed).random((T, K)).astype(np.float32)
     out = gpu_fused(x, w1, w2, w, ids, path=path)
-    _check(out, x, w1, w2, w, ids)
+    _check(out, x, w1, w2, w, ids, path=path)
 
 
 @pytest.mark.parametrize("path", [-1, _capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128])
@@ -229,7 +237,7 @@ def test_tile_boundary_group_sizes(m, path, dev):
     w1, w2 = make_bank(E, H, I, torch.bfloat16, seed=m)
     x = torch.randn(T, H).to(torch.bfloat16)
     w = np.ones((T, 1), np.float32)
-    _check(gpu_fused(x, w1, w2, w, ids, path=path), x, w1, w2, w, ids)
+    _check(gpu_fused(x, w1, w2, w, ids, path=path), x, w1, w2, w, ids, path=path)
 
 
 def test_dropped_slots_and_expert_map(dev):

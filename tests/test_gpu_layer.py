@@ -43,7 +43,7 @@ def _oracle_layer(moe_cpu_w1, moe_cpu_w2, x_cpu, logits, K, renorm=True, act=0, 
                                 activation=act, inter_round=round_mode or 0, tokens=tokens), ids
 
 
-@pytest.mark.parametrize("dtype,T", [(torch.float32, 256), (torch.bfloat16, 512),
+@pytest.mark.parametrize("dtype,T", [(torch.float32, 512), (torch.bfloat16, 512),
                                      (torch.float16, 64), (torch.bfloat16, 3)])
 def test_tiny_config_layer_matches_oracle(dtype, T, dev):
     """The tiny CPU-reference shape: hidden 1024, 8 experts, top-2, ffn 2816."""
@@ -346,3 +346,107 @@ def test_shared_pool_across_layers_matches_resident(dev, monkeypatch):
         assert torch.allclose(o.float(), w.float(), rtol=0, atol=2e-3 * w.float().abs().max().item())
     ev = sum(m._cache.stats.evictions for m in layers)
     assert ev > 0 and pool.n_slots <= 3 + 2 and len(pool) <= 3 + 2
+
+
+def test_substitute_aliases_hbm_slot_then_refills(dev, monkeypatch):
+    """Similarity substitution on HBM slots (reference: offload_cache.py:713-
+    732): a miss served by the most similar resident expert makes the kernels
+    read that expert's slot under the missing id (two LRU entries, one slot,
+    two references). Once every entry aliasing the slot is evicted, the slot
+    goes back to the free list and is refilled with another expert, which the
+    kernels then read. Steps are queued without host synchronisation, so the
+    refill must wait for the kernels that read the alias; every step's output
+    is checked against the oracle with the expert each step really ran."""
+    monkeypatch.delenv("RE_CHUNK_SIZE", raising=False)
+    monkeypatch.setenv("RE_MAX_PACK", "8")
+    banner("substitution aliases an HBM slot, then the slot is refilled")
+    E, H, I, T = 8, 256, 512, 4
+    layer = synth.make_layer(synth.MoEShape("t", H, E, 1, I), torch.bfloat16, seed=21)
+    moe = FusedMoE(num_experts=E, top_k=1, hidden_size=H, intermediate_size=I,
+                   dtype=torch.bfloat16)
+    sd = {"gate.weight": torch.zeros(E, H, dtype=torch.bfloat16)}
+    for e in range(E):
+        sd["gate.weight"][e, e] = 10.0  # a token spiked at dim d routes to expert d
+        sd[f"experts.{e}.gate_proj.weight"] = layer["w1"][e][:I]
+        sd[f"experts.{e}.up_proj.weight"] = layer["w1"][e][I:]
+        sd[f"experts.{e}.down_proj.weight"] = layer["w2"][e]
+    moe.load_state_dict(sd)
+    moe.gate.data = moe.gate.data.to(dev)
+    cache = moe.build_offload_cache(dev, lru_capacity=2)
+
+    def tokens(d, seed):
+        x = synth.make_tokens(T, H, torch.bfloat16, seed=seed).float() * 0.05
+        x[:, d] = 5.0
+        return x.to(torch.bfloat16).to(dev)
+
+    sim = torch.zeros(E, E)
+    sim[1, 0] = 1.0               # expert 1's miss takes expert 0's slot
+    sim[2, 0], sim[2, 1] = 0.5, 0.9  # expert 2's takes expert 1's entry (expert 0's slot)
+    # (routed expert, expert whose weights the step runs, sim table on?)
+    plan = [(0, 0, False), (1, 0, True), (2, 0, True), (3, 3, False), (4, 4, False),
+            (5, 5, False), (1, 1, False), (5, 5, False)]
+    outs, xs = [], []
+    slot_a = None
+    for step, (d, _, use_sim) in enumerate(plan):
+        cache.sim_table = sim if use_sim else None
+        x = tokens(d, seed=step)
+        xs.append(x)
+        outs.append(moe(x))
+        if step == 0:
+            slot_a = cache._slot_of[0]
+        if step == 2:
+            # entries 1 and 2 alias expert 0's slot; entry 0 was evicted
+            assert cache._slot_of[2] is slot_a and slot_a.refs == 2 and 0 not in cache._lru
+        if step == 5:
+            # every alias evicted: expert 5 was copied into the same slot
+            assert cache._slot_of[5] is slot_a and slot_a.refs == 1
+    torch.cuda.synchronize()
+    assert cache.stats.subs == 2
+    for step, (d, ran, _) in enumerate(plan):
+        x = xs[step].cpu()
+        ref = oracle.fused_experts(x, [layer["w1"][ran]], [layer["w2"][ran]],
+                                   np.ones((T, 1), np.float32), np.zeros((T, 1), np.int64))
+        err = oracle.max_rel(outs[step].float().cpu().numpy(), ref)
+        print(f"  step {step}: routed {d}, ran expert {ran}: max_rel {err:.2e}", flush=True)
+        assert err <= 2e-2
+
+
+def test_shared_pool_with_lookahead_matches_resident(dev, monkeypatch):
+    """Layers sharing one small ExpertPool, each with a predictor: the
+    lookahead loads experts on its layer's copy stream, and the next layer's
+    requests evict many of them from the pool before anything reads them;
+    their slots are then refilled on another layer's copy stream. Each refill
+    must wait for the copy still filling the slot as well as for the slot's
+    readers: every step of a chained decode must equal the resident layers."""
+    from reframework_amd.moe import ExpertPool
+
+    monkeypatch.delenv("RE_CHUNK_SIZE", raising=False)
+    monkeypatch.setenv("RE_MAX_PACK", "8")
+    banner("shared pool + lookahead across layers")
+    E, K, H, I, n_layers = 8, 2, 1024, 1024, 3
+    pool = ExpertPool(capacity=4)
+    refs, layers = [], []
+    for li in range(n_layers):
+        refs.append(_build(E, K, H, I, torch.bfloat16, seed=30 + li, gate_sigma=0.2).to(dev))
+        m = _build(E, K, H, I, torch.bfloat16, seed=30 + li, gate_sigma=0.2)
+        m.gate.data = m.gate.data.to(dev)
+        m.build_offload_cache(dev, lru_capacity=2, pool=pool)
+        m.attach_predictor(window=4)
+        m._cache._bw_gb_s = None  # lookahead bounded by pool room only
+        layers.append(m)
+    outs, wants = [], []
+    for step in range(16):
+        x = synth.make_tokens(1, H, torch.bfloat16, seed=200 + step).to(dev)
+        y, z = x, x
+        for m, r in zip(layers, refs):
+            y = m(y)
+            z = r(z)
+        outs.append(y)
+        wants.append(z)
+    torch.cuda.synchronize()
+    predicts = sum(m._cache.stats.predicts for m in layers)
+    evictions = sum(m._cache.stats.evictions for m in layers)
+    print(f"  predicts {predicts}, evictions {evictions}, slots {pool.n_slots}", flush=True)
+    assert predicts > 0 and evictions > 0
+    for o, w in zip(outs, wants):
+        assert torch.allclose(o.float(), w.float(), rtol=0, atol=2e-3 * w.float().abs().max().item())

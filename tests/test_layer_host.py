@@ -74,3 +74,18 @@ def test_synth_shared_pieces_match_merged_tensors():
     assert torch.equal(sh["gate_proj"][8:], sh["w1"][1][:8])
     assert torch.equal(sh["up_proj"][:8], sh["w1"][0][8:])
     assert torch.equal(sh["down_proj"][:, 8:], sh["w2"][1])
+
+
+def test_available_is_false_without_a_gpu_or_library(monkeypatch):
+    """The drop-in import keeps the reference's modules where the MI355X path
+    cannot run: no visible GPU (this host), or a library that fails to load."""
+    import torch
+
+    from reframework_amd import _capi, moe
+
+    if not torch.cuda.is_available():
+        assert moe.available() is False
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(_capi, "LIB_PATH", "/nonexistent/libmoe355.so")
+    monkeypatch.setattr(_capi, "_lib", None)
+    assert moe.available() is False
