@@ -82,27 +82,35 @@ class Layer:
         return torch.randn(T, self.H, generator=g, device=self.dev).to(torch.bfloat16)
 
 
+STAGES = ("router", "permute", "gate_up", "down", "combine")
+
+
 def run_layer(layer, x, bufs, events=None):
     """router, then the routed experts on the current stream. Without events
     the experts run as the layer runs them, one moe355_fused_experts call
     (permute -> gate_up -> down -> combine; at decode sizes the grouping
-    happens inside gate_up). With events (the stage-timing pass) the stages
-    are called one by one with events between them."""
+    happens inside gate_up). With events (the stage-timing pass: six events
+    on the stream the kernels run on) the stages are called one by one with
+    an event before the first and after each."""
     from reframework_amd import _capi
 
     plan, ws, w, ids, out = bufs
     s = _capi.stream_handle(x.device)
+    if events:
+        events[0].record()
     _capi.router_topk(x, layer.gate, layer.bias, layer.K, True, True, 0, w, ids, stream=s)
     if not events:
         _capi.fused_experts(x, layer.w1p, layer.w2p, layer.I, w, ids, 0, out, ws, stream=s)
         return
-    _capi.permute(plan, ids, ws, stream=s)
-    events[0].record()
-    _capi.gate_up(plan, x, layer.w1p, 0, ws, stream=s)
     events[1].record()
-    _capi.down(plan, layer.w2p, ws, stream=s)
+    _capi.permute(plan, ids, ws, stream=s)
     events[2].record()
+    _capi.gate_up(plan, x, layer.w1p, 0, ws, stream=s)
+    events[3].record()
+    _capi.down(plan, layer.w2p, ws, stream=s)
+    events[4].record()
     _capi.combine(plan, w, out, False, ws, stream=s)
+    events[5].record()
 
 
 def make_bufs(layer, T):
@@ -132,63 +140,122 @@ def measure(layer, T, steps, warmup):
         run_layer(layer, x, bufs)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1000.0 / steps
-    # stage timing pass (events inserted between stages)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    # stage timing pass (events between the stages, on the kernels' stream)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
     for i in range(steps):
-        ev[i][3].record()
         run_layer(layer, x, bufs, events=ev[i])
-        ev[i][4].record()
     torch.cuda.synchronize()
-    gate_up = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
-    down = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
-    total_ev = sum(e[3].elapsed_time(e[4]) for e in ev) / steps
+    stage_ms = {name: sum(e[j].elapsed_time(e[j + 1]) for e in ev) / steps
+                for j, name in enumerate(STAGES)}
     ids = bufs[3].cpu().numpy()
     routed = sorted(set(int(v) for v in ids.reshape(-1)))
     plan, ws = bufs[0], bufs[1]
     tiles = int(ws[plan.off_tile_map:plan.off_tile_map + 4].cpu().view(torch.int32)[0])
-    return {"ms": ms, "gate_up_ms": gate_up, "down_ms": down, "layer_ev_ms": total_ev,
+    return {"ms": ms, "gate_up_ms": stage_ms["gate_up"], "down_ms": stage_ms["down"],
+            "stage_ms": stage_ms, "layer_ev_ms": sum(stage_ms.values()),
             "routed_experts": len(routed), "plan_path": plan.path,
             "down_splits": plan.down_splits, "token_tiles": tiles}
 
 
+def stage_rates(layer, T, m):
+    """Algorithmic bytes and achieved GB/s of the HBM-bound stages: the
+    router (x and the gate read, T*K weights and ids written), the permute
+    (it moves indices only: T*K ids read, slot_to_row / row_src and the
+    per-block counts written; token rows are gathered by gate_up), and the
+    combine (each routed slot's y row in the format the plan's down
+    projection writes, the routing weights and slot map, the output)."""
+    from reframework_amd import _capi
+
+    plan = _capi.make_plan(T, layer.H, layer.I, layer.E, layer.K, _capi.BF16)
+    R, H, E, K = T * layer.K, layer.H, layer.E, layer.K
+    y_narrow = plan.path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128) and \
+        plan.down_splits == 1
+    y_bytes = R * H * 2 if y_narrow else plan.down_splits * R * H * 4
+    alg = {"router": T * H * 2 + E * H * 2 + T * K * 8,
+           "permute": R * 4 + 3 * R * 4 + plan.n_blocks * E * 4 + (E + 1) * 4,
+           "combine": y_bytes + R * 8 + T * H * 2}
+    out = {}
+    for name, nbytes in alg.items():
+        ms = m["stage_ms"][name]
+        out[name] = {"us": round(ms * 1000.0, 2), "alg_bytes": nbytes,
+                     "gb_s": round(nbytes / (ms / 1000.0) / 1e9, 1),
+                     "hbm_frac": round(nbytes / (ms / 1000.0) / 1e9 / PEAK_HBM_GBS, 4)}
+    out["gate_up"] = {"us": round(m["stage_ms"]["gate_up"] * 1000.0, 2)}
+    out["down"] = {"us": round(m["stage_ms"]["down"] * 1000.0, 2)}
+    return out
+
+
+def usable_cores():
+    """Cores this process may run on: its CPU affinity, capped by a cgroup
+    CPU quota when one is set (a container's share of a larger host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "host CPU"
+
+
 def cpu_baseline(layer, T):
-    """The reference's resident forward (torch CPU, per-call bank stacking)
-    on a bounded sample of T tokens; tokens/s = T / median time."""
+    """The reference's resident forward restated in torch on the host CPU
+    (oracle/ref_torch.py), on every core this process may use, in two
+    variants: (i) faithful, stacking all experts into fresh banks on every
+    call as the reference does, (ii) with the banks stacked once beforehand.
+    Median of 3 runs after a warm-up, within a 30 s budget per variant;
+    tokens/s = T / median. ``value`` is the faithful variant."""
     import torch
 
     from oracle import ref_torch
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    cores = usable_cores()
+    torch.set_num_threads(cores)
     gate = layer.gate.cpu()
     w1 = [w.cpu() for w in layer.w1]
     w2 = [w.cpu() for w in layer.w2]
     bias = layer.bias.cpu()
     x = layer.inputs(T).cpu()
-    times = []
+    variants = {}
     with torch.no_grad():
-        ref_torch.forward(x[:8], gate, w1, w2, K, bias=bias)  # warm-up
-        budget_s = 30.0
-        t_start = time.perf_counter()
-        while len(times) < 3 and (time.perf_counter() - t_start) < budget_s:
-            t0 = time.perf_counter()
-            ref_torch.forward(x, gate, w1, w2, K, bias=bias)
-            times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": T / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+        stacked = (torch.stack(w1), torch.stack(w2))
+        for name, banks in (("faithful", None), ("pre_stacked", stacked)):
+            ref_torch.forward(x[:8], gate, w1, w2, K, bias=bias, stacked=banks)  # warm-up
+            times = []
+            t_start = time.perf_counter()
+            while len(times) < 3 and (time.perf_counter() - t_start) < 30.0:
+                t0 = time.perf_counter()
+                ref_torch.forward(x, gate, w1, w2, K, bias=bias, stacked=banks)
+                times.append(time.perf_counter() - t0)
+            times.sort()
+            med = times[len(times) // 2]
+            variants[name] = {"tokens_per_s": round(T / med, 1), "median_s": round(med, 4),
+                              "runs": len(times)}
+        del stacked
+    model = cpu_model()
+    return {"value": variants["faithful"]["tokens_per_s"], "unit": "tokens/s", "cores": cores,
+            "kind": "port", "host_cpus": os.cpu_count(), "cpu_model": model,
+            "variants": variants,
             "sample": f"reference resident forward restated in torch (oracle/ref_torch.py): "
-                      f"Mixtral shape bf16, {T} tokens, banks stacked per call, median of "
-                      f"{len(times)} run(s) of {med:.2f} s on {model or 'host CPU'}"}
+                      f"Mixtral shape bf16, {T} tokens, {cores} threads on {model}; value = "
+                      f"faithful variant (all experts stacked per call, median "
+                      f"{variants['faithful']['median_s']:.2f} s); pre-stacked banks: "
+                      f"{variants['pre_stacked']['tokens_per_s']:.0f} tokens/s"}
 
 
 def measured_traffic(T):
@@ -451,7 +518,8 @@ def main():
             "hbm_gb_s": round(alg_bytes / (m["ms"] / 1000.0) / 1e9, 1),
             "hbm_frac": round(alg_bytes / (m["ms"] / 1000.0) / 1e9 / PEAK_HBM_GBS, 4),
             "gate_up_ms": round(m["gate_up_ms"], 4), "down_ms": round(m["down_ms"], 4),
-            "path": m["plan_path"], "down_splits": m["down_splits"]}
+            "path": m["plan_path"], "down_splits": m["down_splits"],
+            "stages": stage_rates(layer, tok, m)}
 
     configs = {}
     names = [v.strip() for v in args.configs.split(",") if v.strip()]
@@ -490,6 +558,7 @@ def main():
         "grouped_gemm": {"tflops": round(grouped, 2), "mfma_frac": round(grouped / PEAK_BF16_TFLOPS, 4),
                          "gate_up_ms": round(head["gate_up_ms"], 4),
                          "down_ms": round(head["down_ms"], 4)},
+        "stages": stage_rates(layer, T, head),
         "decode": decode,
         "configs": configs,
     }

@@ -132,3 +132,31 @@ def assert_y_rounding(got: np.ndarray, ref_expected: np.ndarray, ref_other: np.n
     print(f"  y rounding: rms to expected {d_exp:.3e}, to the other {d_oth:.3e} "
           f"(ratio {d_exp / max(d_oth, 1e-300):.3f}, outputs differing {differ:.2f})", flush=True)
     assert d_exp < 0.95 * d_oth
+
+
+# Half an ulp of the output's own rounding (relative to the value) and the
+# noise allowed beyond it (relative to the largest output) in the tight check;
+# with y rounded, one ulp of a slot's y more (2^-7 bf16, 2^-10 f16 of it).
+_OUT_ROUND = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
+_NOISE = {torch.bfloat16: 1e-3, torch.float16: 5e-4}
+_Y_ULP = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}
+
+
+def assert_matches_rounded(got: np.ndarray, ref: np.ndarray, dt: torch.dtype,
+                           y_rounded: bool = False) -> float:
+    """Tight check against the oracle that rounds the intermediate (and y)
+    like the kernels: every output element within its own rounding to ``dt``
+    (half an ulp, <= 2^-8 |v| for bf16, 2^-11 |v| for f16) plus 1e-3 (bf16) /
+    5e-4 (f16) of the largest output, which covers fp32 accumulation order and
+    intermediates whose fp32 and fp64 values round to neighbouring values.
+    Where y is rounded too, a y whose fp32 and fp64 values straddle a rounding
+    boundary lands one ulp of y away: one more 2^-7 (bf16) / 2^-10 (f16) of the
+    largest output is allowed. Returns the excess over the rounding bound,
+    relative to max |ref|."""
+    scale = float(np.max(np.abs(ref))) or 1.0
+    excess = float(np.max(np.abs(got - ref) - _OUT_ROUND[dt] * np.abs(ref))) / scale
+    bar = _NOISE[dt] + (_Y_ULP[dt] if y_rounded else 0.0)
+    print(f"  beyond the output's own rounding: {max(excess, 0.0):.2e} of max|ref| "
+          f"(bar {bar:.1e})", flush=True)
+    assert excess <= bar
+    return excess
