@@ -221,6 +221,31 @@ int moe355_fused_experts(const void* x, const void* const* w1, const void* const
                          int K, int dtype, int act, void* out, int accumulate_f32,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Size of the library's static scratch (moe355_fused_experts_static). */
+#define MOE355_STATIC_SCRATCH_BYTES (64u << 20)
+
+/*
+ * moe355_fused_experts without a workspace argument: scratch comes from a
+ * static device array of MOE355_STATIC_SCRATCH_BYTES inside the library (one
+ * per device, held until the process ends), so the call allocates nothing
+ * and needs no buffer from the caller.
+ * No counterpart in the reference. It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.
+ * Limits: a shape whose plan needs more than MOE355_STATIC_SCRATCH_BYTES
+ * fails with MOE355_EWORKSPACE before launching anything (the tiled paths
+ * first drop their down-projection partial tiles, running that projection's
+ * last round whole). The calling thread's current device must be the device
+ * of `stream`. Every call on one device shares that device's array: calls
+ * that overlap on one device (other streams, other threads) race and must
+ * be serialised by the caller. Nothing in the array needs to start zeroed.
+ */
+int moe355_fused_experts_static(const void* x, const void* const* w1, const void* const* w2,
+                                const float* topk_w, const void* topk_ids, int ids_int64,
+                                const int32_t* expert_map, int map_len, int T, int H, int I,
+                                int E, int K, int dtype, int act, void* out, int accumulate_f32,
+                                void* stream);
+
 /*
  * Cast an fp32 [n] buffer to `dtype` (the final cast of the streaming path,
  * reframework/moe/moe_layer.py:418).

@@ -26,6 +26,7 @@ F32, BF16, F16 = 0, 1, 2
 ACT_CODES = {"silu": 0, "gelu": 1, "gelu_tanh": 2}
 PATH_MFMA_TILED, PATH_MFMA_SKINNY, PATH_SIMT, PATH_MFMA_TILED128 = 0, 1, 2, 4
 MAX_EXPERTS = 256
+STATIC_SCRATCH_BYTES = 64 << 20
 
 _DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -86,6 +87,8 @@ _SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "moe355_combine": (_I, [_PPLAN, _P, _P, _I, _P, _P]),
     "moe355_fused_experts": (_I, [_P, _PP, _PP, _P, _P, _I, _PI32, _I, _I, _I, _I, _I, _I, _I,
                                   _I, _P, _I, _P, _Z, _P]),
+    "moe355_fused_experts_static": (_I, [_P, _PP, _PP, _P, _P, _I, _PI32, _I, _I, _I, _I, _I,
+                                         _I, _I, _I, _P, _I, _P]),
     "moe355_cast_f32": (_I, [_P, _P, _Z, _I, _P]),
     "moe355_h2d_async": (_I, [_P, _P, _Z, _P]),
 }
@@ -291,6 +294,29 @@ def fused_experts(x: torch.Tensor, w1_ptrs: Sequence[int], w2_ptrs: Sequence[int
         _ptr(x), t1, t2, _ptr(topk_w), _ptr(topk_ids), int(topk_ids.dtype == torch.int64), mp,
         mlen, T, H, I, E, K, dtype_code(x.dtype), act, _ptr(out), int(accumulate_f32),
         _ptr(workspace), workspace.numel() * workspace.element_size(), s))
+
+
+def fused_experts_static(x: torch.Tensor, w1_ptrs: Sequence[int], w2_ptrs: Sequence[int], I: int,
+                         topk_w: torch.Tensor, topk_ids: torch.Tensor, act: int,
+                         out: torch.Tensor, expert_map: Optional[Sequence[int]] = None,
+                         accumulate_f32: bool = False, stream: Optional[int] = None) -> None:
+    """moe355_fused_experts_static: the routed-expert computation on the
+    library's static scratch (no workspace; see include/moe355.h for its
+    size limit and the rule that calls on one device must not overlap)."""
+    T, H = x.shape
+    K = topk_ids.shape[1]
+    E = len(w1_ptrs)
+    s = stream if stream is not None else stream_handle(x.device)
+    t1, _k1 = _ptr_table(w1_ptrs)
+    t2, _k2 = _ptr_table(w2_ptrs)
+    if expert_map:
+        m = (ctypes.c_int32 * len(expert_map))(*expert_map)
+        mp, mlen = ctypes.cast(m, _PI32), len(expert_map)
+    else:
+        mp, mlen = None, 0
+    _check("moe355_fused_experts_static", lib().moe355_fused_experts_static(
+        _ptr(x), t1, t2, _ptr(topk_w), _ptr(topk_ids), int(topk_ids.dtype == torch.int64), mp,
+        mlen, T, H, I, E, K, dtype_code(x.dtype), act, _ptr(out), int(accumulate_f32), s))
 
 
 def cast_f32(src: torch.Tensor, dst: torch.Tensor, stream: Optional[int] = None) -> None:

@@ -7,9 +7,16 @@
 #include <cstdio>
 #include <cstring>
 
+#include <mutex>
+
 #include "common.h"
 
 using namespace moe355;
+
+// Scratch of moe355_fused_experts_static: the workspace of callers that cannot
+// allocate. Each device that loads the library holds its own copy until the
+// process ends; see static_scratch for how host code reaches it.
+static __device__ __align__(256) unsigned char scratch[MOE355_STATIC_SCRATCH_BYTES];
 
 namespace {
 
@@ -27,6 +34,8 @@ int check_hip(hipError_t e, const char* what) {
   if (e == hipSuccess) return MOE355_OK;
   return fail(MOE355_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
+
+constexpr int kMaxDevices = 64;
 
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
@@ -67,9 +76,9 @@ int check_banks(const moe355_plan* p, const void* const* w, const char* name) {
 namespace moe355 {
 
 int device_cu_count() {
-  static int cached[64] = {0};
+  static int cached[kMaxDevices] = {0};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
     (void)hipGetLastError();
     return 256;
   }
@@ -422,6 +431,63 @@ bool y_narrow(const moe355_plan* p) {
          p->down_splits == 1 && p->dtype != MOE355_F32;
 }
 
+// permute -> gate_up -> down -> combine on a filled plan and a workspace of
+// plan.workspace_bytes (the body of both fused_experts entry points).
+int run_fused(const moe355_plan& p, const void* x, const void* const* w1, const void* const* w2,
+              const float* topk_w, const void* topk_ids, int ids_int64,
+              const int32_t* expert_map, int map_len, int act, void* out, int accumulate_f32,
+              void* workspace, void* stream) {
+  int rc;
+  if (p.path == MOE355_PATH_MFMA_SKINNY && p.rows <= 16 && p.E <= 32) {
+    // Decode sizes: the gate_up workgroups group the routed slots themselves
+    // (one launch fewer; the permute's outputs are still written for down and
+    // combine). Every workgroup pays the grouping (one round per distinct
+    // expert) before its weight stream, and a CU runs several workgroups in
+    // turn, so this pays only for a few slots over few experts: Mixtral one
+    // token 124.6 -> 122.7 us; 64 experts top-6 at 8 tokens went 132 -> 150.
+    PermuteArgs pa;
+    if ((rc = permute_args(&p, topk_ids, ids_int64, expert_map, map_len, workspace, &pa))) return rc;
+    if ((rc = gate_up_impl(&p, x, w1, act, workspace, stream, &pa))) return rc;
+  } else {
+    if ((rc = moe355_permute(&p, topk_ids, ids_int64, expert_map, map_len, workspace, stream)))
+      return rc;
+    if ((rc = moe355_gate_up(&p, x, w1, act, workspace, stream))) return rc;
+  }
+  if ((rc = moe355_down(&p, w2, workspace, stream))) return rc;
+  return moe355_combine(&p, topk_w, out, accumulate_f32, workspace, stream);
+}
+
+// Device address of this device's copy of `scratch`, looked up once per
+// device with that device current. The array's host-side name is only a
+// handle for the runtime: kernels must be given this address.
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int static_scratch(void* stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return check_hip(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MOE355_EUNSUPPORTED, "device %d outside [0, %d)", dev, kMaxDevices);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(as_stream(stream), &sdev);
+    if (e != hipSuccess) return check_hip(e, "hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(MOE355_EINVAL, "stream is on device %d but device %d is current", sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return check_hip(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(MOE355_EHIP, "hipGetSymbolAddress(scratch) gave NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOE355_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -492,23 +558,37 @@ int moe355_fused_experts(const void* x, const void* const* w1, const void* const
   if (!workspace || workspace_bytes < p.workspace_bytes)
     return fail(MOE355_EWORKSPACE, "workspace of %zu bytes, plan needs %zu", workspace_bytes,
                 p.workspace_bytes);
-  if (p.path == MOE355_PATH_MFMA_SKINNY && p.rows <= 16 && p.E <= 32) {
-    // Decode sizes: the gate_up workgroups group the routed slots themselves
-    // (one launch fewer; the permute's outputs are still written for down and
-    // combine). Every workgroup pays the grouping (one round per distinct
-    // expert) before its weight stream, and a CU runs several workgroups in
-    // turn, so this pays only for a few slots over few experts: Mixtral one
-    // token 124.6 -> 122.7 us; 64 experts top-6 at 8 tokens went 132 -> 150.
-    PermuteArgs pa;
-    if ((rc = permute_args(&p, topk_ids, ids_int64, expert_map, map_len, workspace, &pa))) return rc;
-    if ((rc = gate_up_impl(&p, x, w1, act, workspace, stream, &pa))) return rc;
-  } else {
-    if ((rc = moe355_permute(&p, topk_ids, ids_int64, expert_map, map_len, workspace, stream)))
-      return rc;
-    if ((rc = moe355_gate_up(&p, x, w1, act, workspace, stream))) return rc;
+  return run_fused(p, x, w1, w2, topk_w, topk_ids, ids_int64, expert_map, map_len, act, out,
+                   accumulate_f32, workspace, stream);
+}
+
+int moe355_fused_experts_static(const void* x, const void* const* w1, const void* const* w2,
+                                const float* topk_w, const void* topk_ids, int ids_int64,
+                                const int32_t* expert_map, int map_len, int T, int H, int I,
+                                int E, int K, int dtype, int act, void* out, int accumulate_f32,
+                                void* stream) {
+  moe355_plan p;
+  int rc = moe355_make_plan(T, H, I, E, K, dtype, &p);
+  if (rc) return rc;
+  if (T == 0) return MOE355_OK;
+  if (p.workspace_bytes > MOE355_STATIC_SCRATCH_BYTES) {
+    // The tiled paths' last region holds one fp32 partial tile per CU for the
+    // down projection's K-split tail; without it the down projection runs its
+    // last round whole (same results up to fp32 summation order).
+    const bool tiled = p.path == MOE355_PATH_MFMA_TILED || p.path == MOE355_PATH_MFMA_TILED128;
+    if (!tiled || p.off_part > MOE355_STATIC_SCRATCH_BYTES)
+      return fail(MOE355_EWORKSPACE,
+                  "fused_experts_static: T=%d H=%d I=%d E=%d K=%d needs %zu bytes of scratch, "
+                  "more than the library's static %u bytes; use moe355_fused_experts with a "
+                  "workspace",
+                  T, H, I, E, K, tiled ? p.off_part : p.workspace_bytes,
+                  static_cast<unsigned>(MOE355_STATIC_SCRATCH_BYTES));
+    p.workspace_bytes = p.off_part;
   }
-  if ((rc = moe355_down(&p, w2, workspace, stream))) return rc;
-  return moe355_combine(&p, topk_w, out, accumulate_f32, workspace, stream);
+  void* ws = nullptr;
+  if ((rc = static_scratch(stream, &ws))) return rc;
+  return run_fused(p, x, w1, w2, topk_w, topk_ids, ids_int64, expert_map, map_len, act, out,
+                   accumulate_f32, ws, stream);
 }
 
 int moe355_cast_f32(const float* src, void* dst, size_t n, int dtype, void* stream) {
