@@ -47,6 +47,10 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--profile", type=int, default=0,
                     help="profiling aid: run only the layer at this many tokens")
+    ap.add_argument("--profile-shape", type=str, default="mixtral",
+                    choices=("mixtral", "phi35moe", "finegrained"),
+                    help="profiling aid: the layer --profile runs (fine-grained: through "
+                         "FusedMoE.forward with its 2 shared experts)")
     ap.add_argument("--copy-calib", type=int, default=0,
                     help="profiling aid: device-to-device copies of this many bytes, the "
                          "known-size reference for HBM byte counters")
@@ -490,8 +494,18 @@ def main():
     layer = Layer(dev)
 
     if args.profile:
+        if args.profile_shape == "finegrained":
+            r = config_finegrained(dev, args.steps, args.warmup, tokens=(args.profile,))
+            print(json.dumps(r), flush=True)
+            return
+        if args.profile_shape == "phi35moe":
+            from reframework_amd import synth
+
+            del layer
+            layer = Layer(dev, hidden=4096, experts=16, top_k=2, ffn=6400,
+                          bias=synth.zipf_router_bias(16, 1.1))
         m = measure(layer, args.profile, args.steps, args.warmup)
-        print(json.dumps({"tokens": args.profile, **m}), flush=True)
+        print(json.dumps({"tokens": args.profile, "shape": args.profile_shape, **m}), flush=True)
         return
 
     T = args.tokens
