@@ -1,0 +1,396 @@
+"""CPU emulation of the HIP kernels' index math (no GPU).
+
+Each kernel's work decomposition is replayed on the host with the kernel's
+own formulas, and every index it forms is checked against the buffer it
+addresses, before any of it runs on a GPU:
+
+  * permute (count_kernel + scatter_kernel, reframework_amd/csrc/permute.hip):
+    the scatter's LDS tables (`total`, `base`, the per-wave `wave_cnt`) are
+    replayed per block, round and wave with every LDS word poisoned at kernel
+    start, so a read of a word the kernel never wrote fails; the ballot ranking
+    is replayed bit by bit. Every slot_to_row / row_src write must stay in
+    bounds, every row must be written once, and the result must equal the
+    oracle's stable grouping. A planted mistake (the per-round zeroing of
+    `wave_cnt` covering only wave 0's row, which once sent row_src out of
+    bounds on the GPU) must be caught.
+  * the tiled grouped GEMM (ffn_tiled.hip): the persistent schedule (XCD
+    remap, work_split's K-split tail, decode_tile's per-expert item groups)
+    must cover every (K-split, permuted row, weight tile) exactly once, by a
+    whole item or by all S K-parts of a split item, whose partial tiles stay
+    within the workspace; every token row the MFMAs read (all 256 rows of a
+    256-row tile; on 128-row tiles the two 64-row halves that sit in LDS rows
+    0-63 and 128-191) is a loaded row of the tile or a zero-filled padding
+    row, and every valid row is read; token and weight offsets stay in their
+    32-bit buffer ranges.
+  * the weight-streaming kernel's in-kernel grouping (ffn_skinny.hip,
+    group_small): its outputs must equal the permute's, and every tile it
+    hands a workgroup must lie inside one expert's rows.
+
+Shapes: the workloads the throughput figures are quoted on (Mixtral 1, 16,
+256 and 4096 tokens; Phi-3.5 2048 with Zipf-skewed routing; the fine-grained
+layer at 8 and 4096 tokens with its two shared columns) plus ragged and
+dropped-slot cases.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _helpers import skewed_ids
+from oracle import oracle
+from reframework_amd import _capi
+
+WAVE, THREADS = 64, 256
+WAVES = THREADS // WAVE
+CHUNK = 1024          # kPermuteChunk
+ROUNDS = CHUNK // THREADS
+POISON = -(1 << 40)   # an LDS word nobody wrote
+
+
+# ------------------------------------------------------------------ permute
+def _routed(ids_flat, emap, E):
+    """routed_expert(): the local expert of each slot, -1 when dropped."""
+    out = np.empty(len(ids_flat), np.int64)
+    for s, g in enumerate(ids_flat):
+        if emap:
+            out[s] = emap[g] if 0 <= g < len(emap) else -1
+        else:
+            out[s] = g if 0 <= g < E else -1
+        if out[s] >= E:
+            out[s] = -1
+    return out
+
+
+def emulate_permute(ids, E, tile_rows, max_tiles, emap=None, zero_first_row_only=False):
+    """Replays count_kernel / scatter_kernel. Returns (offsets, slot_to_row,
+    row_src, tile_map); raises AssertionError on an out-of-bounds index, a
+    row written twice or a read of unwritten LDS."""
+    T, K = ids.shape
+    R = T * K
+    e_of = _routed(ids.reshape(-1), emap, E)
+    n_blocks = -(-R // CHUNK)
+    counts = np.zeros((n_blocks, E), np.int64)  # count_kernel
+    for s in range(R):
+        if e_of[s] >= 0:
+            counts[s // CHUNK, e_of[s]] += 1
+    slot_to_row = np.full(R, POISON, np.int64)
+    row_src = np.full(R, POISON, np.int64)
+    offsets = tile_map = None
+    for b in range(n_blocks):
+        total = counts.sum(0) if n_blocks > 1 else counts[0].copy()
+        base = counts[:b].sum(0).astype(np.int64)
+        start = np.concatenate([[0], np.cumsum(total)])
+        tiles = -(-total // tile_rows)
+        tile_start = np.concatenate([[0], np.cumsum(tiles)])
+        tile_start[E] = min(tile_start[E], max_tiles)
+        base = base + start[:E]
+        if b == 0:
+            offsets = start.copy()
+            nt = int(tile_start[E])
+            tile_map = [nt, tile_rows]
+            for j in range(nt):
+                lo = int(np.searchsorted(tile_start[:E], j, side="right") - 1)
+                tile_map += [lo, int(start[lo] + (j - tile_start[lo]) * tile_rows)]
+        wave_cnt = np.full((WAVES, 256), POISON, np.int64)  # LDS at kernel start
+        r = 0
+        while r < ROUNDS and b * CHUNK + r * THREADS < R:
+            # per-round zeroing, as the kernel indexes it
+            for i in range(WAVES * E):
+                if zero_first_row_only:
+                    wave_cnt.reshape(-1)[i] = 0  # the flat-index mistake
+                else:
+                    wave_cnt[i // E, i % E] = 0
+            slots = b * CHUNK + r * THREADS + np.arange(THREADS)
+            es = np.array([e_of[s] if s < R else -1 for s in slots])
+            rank = np.zeros(THREADS, np.int64)
+            for w in range(WAVES):
+                lanes = es[w * WAVE:(w + 1) * WAVE]
+                routed = lanes >= 0
+                bits = [((lanes >> bit) & 1).astype(bool) for bit in range(8)]
+                for ln in range(WAVE):
+                    if not routed[ln]:
+                        continue
+                    same = routed.copy()
+                    for bit in range(8):
+                        same &= bits[bit] if bits[bit][ln] else ~bits[bit]
+                    rank[w * WAVE + ln] = int(same[:ln].sum())
+                    if rank[w * WAVE + ln] == 0:
+                        wave_cnt[w, lanes[ln]] = int(same.sum())
+            for t in range(THREADS):
+                s = slots[t]
+                if s >= R:
+                    continue
+                e = es[t]
+                if e < 0:
+                    slot_to_row[s] = -1
+                    continue
+                w = t // WAVE
+                assert all(wave_cnt[v, e] != POISON for v in range(w)), "unwritten LDS read"
+                row = int(base[e] + rank[t] + sum(wave_cnt[v, e] for v in range(w)))
+                assert 0 <= row < R, f"row {row} outside [0, {R})"
+                assert row_src[row] == POISON, f"row {row} written twice"
+                slot_to_row[s] = row
+                row_src[row] = s // K
+            for ee in range(E):
+                col = wave_cnt[:, ee]
+                assert (col != POISON).all(), "unwritten LDS read"
+                base[ee] += int(col.sum())
+            r += 1
+    return offsets, slot_to_row, row_src, tile_map
+
+
+def _mixtral_ids(T, seed=0):
+    return skewed_ids(T, 2, 8, seed=seed, skew=0.5)
+
+
+def _finegrained_ids(T, seed=0):
+    routed = np.argsort(np.random.default_rng(seed).random((T, 64)), axis=1)[:, :6]
+    return np.concatenate([routed, np.full((T, 1), 64), np.full((T, 1), 65)], 1).astype(np.int64)
+
+
+PERMUTE_CASES = [
+    ("mixtral_t1", lambda: _mixtral_ids(1), 8, None),
+    ("mixtral_t16", lambda: _mixtral_ids(16), 8, None),
+    ("mixtral_t256", lambda: _mixtral_ids(256), 8, None),
+    ("mixtral_t4096", lambda: _mixtral_ids(4096), 8, None),
+    ("phi35_t2048", lambda: skewed_ids(2048, 2, 16, seed=3, skew=1.1), 16, None),
+    ("finegrained_t8", lambda: _finegrained_ids(8), 66, None),
+    ("finegrained_t700_dropped", lambda: _finegrained_ids(700, 1), 66,
+     [(-1 if e % 5 == 3 else e) for e in range(66)]),
+]
+
+
+@pytest.mark.parametrize("name,make,E,emap", PERMUTE_CASES, ids=[c[0] for c in PERMUTE_CASES])
+def test_permute_emulation_in_bounds_and_equal_to_oracle(name, make, E, emap):
+    ids = make()
+    T, K = ids.shape
+    plan = _capi.make_plan(T, 4096, 14336, E, K, _capi.BF16)
+    offsets, s2r, src, tile_map = emulate_permute(ids, E, plan.tile_rows, plan.max_tiles, emap)
+    o_off, o_s2r, o_src = oracle.permute(ids, E, emap)
+    assert np.array_equal(offsets, o_off)
+    assert np.array_equal(s2r, o_s2r)
+    n = int(offsets[-1])
+    assert np.array_equal(src[:n], o_src[:n])
+    assert (src[n:] == POISON).all()  # rows past the routed ones are never written
+    assert tile_map[0] <= plan.max_tiles
+
+
+def test_permute_emulation_catches_partial_wave_table_zeroing():
+    """The planted mistake: clearing the first 4*E flat words of
+    wave_cnt[4][256] clears only wave 0's row; a multi-wave round must then
+    read stale (here: unwritten) counts."""
+    ids = _finegrained_ids(700, 1)
+    with pytest.raises(AssertionError):
+        emulate_permute(ids, 66, 256, 10_000, zero_first_row_only=True)
+
+
+# ------------------------------------------------------------- tiled GEMM
+def xcd_remap(pid, nwg):
+    xcd, slot = pid & 7, pid >> 3
+    q, rem = nwg >> 3, nwg & 7
+    base = xcd * (q + 1) if xcd < rem else rem * (q + 1) + (xcd - rem) * q
+    return base + slot
+
+
+def work_split(n_work, G, nk, cap):
+    """(n_full, n_units, S) as dma_pipe.h work_split derives it."""
+    Rr = n_work // G if G > 0 else 0
+    tail = n_work - Rr * G
+    if cap <= 0 or tail == 0:
+        return n_work, 0, 1
+    cap = min(cap, G)
+    best, S, s = 14 * nk, 1, 2
+    while s <= 16 and s * tail <= cap and nk % s == 0:
+        c = 14 * nk // s + s * tail
+        if c < best:
+            best, S = c, s
+        s *= 2
+    return (Rr * G, tail * S, S) if S > 1 else (n_work, 0, 1)
+
+
+def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
+    """Replays one tiled launch (gate_up or down) over per-expert row counts;
+    returns the number of work sequence entries. Asserts exactly-once
+    coverage, ragged-tile row coverage and buffer bounds."""
+    E, H, I = plan.E, plan.H, plan.I
+    tile_rows = plan.tile_rows
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    R = int(offs[-1])
+    tiles = [(e, int(offs[e] + r)) for e in range(E) for r in range(0, int(counts[e]), tile_rows)]
+    n_t = len(tiles)
+    assert n_t <= plan.max_tiles
+    S_d = 1 if gate_up else plan.down_splits
+    n_wt = I // 128 if gate_up else H // 256
+    per_split = n_wt * n_t
+    n_work = S_d * per_split
+    G = min(n_wt * plan.max_tiles * S_d, cus)
+    k_per_split = H if gate_up else I // S_d
+    nk = k_per_split // 64
+    if gate_up:
+        cap = min((plan.workspace_bytes - plan.off_y) // (256 * 256 * 4), 4096)
+    else:
+        cap = (plan.workspace_bytes - plan.off_part) // (256 * 256 * 4)
+    n_full, n_units, S = work_split(n_work, G, nk, cap)
+
+    def decode_tile(L):
+        split = L // per_split
+        rem = L - split * per_split
+        t0 = rem // n_wt
+        e = tiles[t0][0]
+        eb, ee = int(offs[e]), int(offs[e + 1])
+        b = t0 - (tiles[t0][1] - eb) // tile_rows
+        ne = (ee - eb + tile_rows - 1) // tile_rows
+        r2 = rem - b * n_wt
+        wt = r2 // ne
+        tt = b + (r2 - wt * ne)
+        row0 = tiles[tt][1]
+        assert tiles[tt][0] == e
+        return split, wt, e, row0, min(row0 + tile_rows, ee)
+
+    whole = np.zeros((S_d, R, n_wt), np.int64)
+    parts = {}
+    n_seq = n_full + n_units
+    lds_rows = np.arange(256)
+    for pid in range(G):
+        L = xcd_remap(pid, G)
+        while L < n_seq:
+            if L < n_full:
+                split, wt, e, r0, r1 = decode_tile(L)
+                whole[split, r0:r1, wt] += 1
+            else:
+                u = L - n_full
+                assert u < cap, f"partial tile {u} past the {cap} the workspace holds"
+                it = n_full + u // S
+                split, wt, e, r0, r1 = decode_tile(it)
+                parts.setdefault(it, []).append(u % S)
+            n = r1 - r0
+            assert 1 <= n <= tile_rows
+            half = tile_rows < 256
+            # tile row held by each LDS row (tile_row_of): 256 = none
+            held = np.where(~half | (lds_rows < 64), lds_rows,
+                            np.where((lds_rows >= 128) & (lds_rows < 192), lds_rows - 64, 256))
+            # tile rows the MFMAs read (tile_row_of_block over both token halves)
+            nblk = 2 if half else 4
+            read = {h * (64 if half else 128) + j * 32 + lr for h in range(2)
+                    for j in range(nblk) for lr in range(32)}
+            assert set(range(n)) <= read and max(read) < tile_rows
+            assert read <= set(held[held < 256].tolist())
+            # every LDS row is loaded from a valid row or zero-filled
+            valid = r0 + held < r1
+            src_rows = np.minimum(r0 + np.minimum(held, tile_rows - 1), r1 - 1)
+            assert (src_rows >= 0).all() and (src_rows < R).all()
+            pitch = (H if gate_up else I) * 2
+            if not gate_up:
+                assert ((held[valid]) * pitch + 7 * 16 + (nk - 1) * 128 < 2 ** 31).all()
+            # weight rows of the tile and their 32-bit offsets
+            if gate_up:
+                wr = np.concatenate([wt * 128 + np.arange(128), I + wt * 128 + np.arange(128)])
+                assert wr.max() < 2 * I
+                assert int(wr.max()) * pitch + 128 * nk <= 2 ** 32
+            else:
+                wr = wt * 256 + np.arange(256)
+                assert wr.max() < H
+            L += G
+    for it, ks in parts.items():
+        assert sorted(ks) == list(range(S)), f"item {it}: K-parts {ks}"
+        split, wt, e, r0, r1 = decode_tile(it)
+        whole[split, r0:r1, wt] += 1
+    assert (whole == 1).all(), "a (split, row, weight tile) is not covered exactly once"
+    # fix-up tasks cover the split items' rows once
+    tasks = n_units // S * (8 if gate_up else 16)
+    assert tasks == len(parts) * (8 if gate_up else 16)
+    return n_seq
+
+
+def _counts(ids, E):
+    return np.bincount(ids.reshape(-1), minlength=E)[:E]
+
+
+TILED_CASES = [
+    ("mixtral_t4096", 4096, 4096, 14336, 8, lambda: _mixtral_ids(4096)),
+    ("mixtral_t256", 256, 4096, 14336, 8, lambda: _mixtral_ids(256)),
+    ("mixtral_t1536", 1536, 4096, 14336, 8, lambda: _mixtral_ids(1536, 2)),
+    ("phi35_t2048", 2048, 4096, 6400, 16, lambda: skewed_ids(2048, 2, 16, seed=3, skew=1.1)),
+    ("finegrained_t4096", 4096, 2048, 1408, 66, lambda: _finegrained_ids(4096)),
+    ("ragged_e64", 1000, 4096, 256, 64, lambda: skewed_ids(1000, 1, 64, seed=5, skew=1.5)),
+]
+
+
+@pytest.mark.parametrize("gate_up", [True, False], ids=["gate_up", "down"])
+@pytest.mark.parametrize("name,T,H,I,E,make", TILED_CASES, ids=[c[0] for c in TILED_CASES])
+def test_tiled_schedule_covers_once_in_bounds(name, T, H, I, E, make, gate_up):
+    ids = make()
+    K = ids.shape[1]
+    plan = _capi.make_plan(T, H, I, E, K, _capi.BF16)
+    assert plan.path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128)
+    emulate_tiled(_counts(ids, E), plan, gate_up)
+    # the same routing on a forced 256-row tile map and a 128-row one
+    for path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128):
+        emulate_tiled(_counts(ids, E), _capi.make_plan(T, H, I, E, K, _capi.BF16, path), gate_up)
+
+
+@pytest.mark.parametrize("cus", [256, 80, 304])
+def test_tiled_schedule_on_other_cu_counts(cus):
+    """Workgroups per launch follow the device's CU count: the decomposition
+    holds for other counts too (the workspace is planned for 256 here)."""
+    ids = skewed_ids(3000, 2, 16, seed=8, skew=1.2)
+    plan = _capi.make_plan(3000, 4096, 2048, 16, 2, _capi.BF16)
+    for gate_up in (True, False):
+        emulate_tiled(_counts(ids, 16), plan, gate_up, cus=cus)
+
+
+# --------------------------------------------------- skinny in-kernel grouping
+def emulate_group_small(ids, E, emap=None, rows=16):
+    """Replays group_small: one wave groups <= 64 slots (lane s = slot s)."""
+    T, K = ids.shape
+    R = T * K
+    assert R <= WAVE
+    e = np.full(WAVE, -1, np.int64)
+    e[:R] = _routed(ids.reshape(-1), emap, E)
+    todo = e >= 0
+    start = tstart = 0
+    slot_to_row = np.full(R, -1, np.int64)
+    row_src = {}
+    tile_map = []
+    dist = []
+    while todo.any():
+        emin = int(e[todo].min())
+        m = e == emin
+        cnt = int(m.sum())
+        nt = -(-cnt // rows)
+        lanes = np.nonzero(m)[0]
+        for rk, ln in enumerate(lanes):
+            slot_to_row[ln] = start + rk
+            assert start + rk not in row_src
+            row_src[start + rk] = ln // K
+        for j in range(nt):
+            tile_map.append((emin, start + j * rows))
+        dist.append((emin, start))
+        start += cnt
+        tstart += nt
+        todo &= ~m
+    offsets = np.empty(E + 1, np.int64)
+    for x in range(E + 1):
+        off = start
+        for de, ds in reversed(dist):
+            if de >= x:
+                off = ds
+        offsets[x] = off
+    return offsets, slot_to_row, row_src, tile_map
+
+
+@pytest.mark.parametrize("T,K,E,drop", [(1, 2, 8, False), (8, 2, 8, True), (4, 4, 32, True),
+                                        (2, 8, 32, False), (5, 3, 16, False)])
+def test_skinny_grouping_equals_permute_and_stays_in_bounds(T, K, E, drop):
+    ids = skewed_ids(T, K, E, seed=T * E + K, skew=1.2)
+    emap = [(-1 if x % 5 == 3 else x) for x in range(E)] if drop else None
+    plan = _capi.make_plan(T, 4096, 14336, E, K, _capi.BF16)
+    assert plan.path == _capi.PATH_MFMA_SKINNY and plan.rows <= 16 and E <= 32
+    offsets, s2r, rsrc, tmap = emulate_group_small(ids, E, emap)
+    o_off, o_s2r, o_src = oracle.permute(ids, E, emap)
+    assert np.array_equal(offsets, o_off) and np.array_equal(s2r, o_s2r)
+    assert all(o_src[r] == t for r, t in rsrc.items())
+    assert len(tmap) <= plan.max_tiles
+    for (e, row0) in tmap:  # each tile inside its expert's rows
+        assert o_off[e] <= row0 < o_off[e + 1]
