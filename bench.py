@@ -43,6 +43,11 @@ def parse():
                     help="other workloads reported beside the headline ('' = none)")
     ap.add_argument("--offload-layers", type=int, default=4)
     ap.add_argument("--offload-steps", type=int, default=48)
+    ap.add_argument("--offload-tokens", type=int, default=8)
+    ap.add_argument("--offload-modes", type=str,
+                    default="max_pack_2_per_layer_lru,max_pack_2_shared_pool,exact_per_layer_lru,"
+                            "exact_shared_pool",
+                    help="offload residency/forward modes; also max_pack_2_per_layer_lru_lookahead")
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--profile", type=int, default=0,
@@ -159,6 +164,44 @@ def measure(layer, T, steps, warmup):
             "stage_ms": stage_ms, "layer_ev_ms": sum(stage_ms.values()),
             "routed_experts": len(routed), "plan_path": plan.path,
             "down_splits": plan.down_splits, "token_tiles": tiles}
+
+
+def rotating_pairs(layer, steps, warmup, rotate=True):
+    """One token per step whose two experts change every step, cycling
+    through the disjoint pairs (0,1), (2,3), (4,5), (6,7): an expert's weights
+    come back every four steps, after 2.1 GB of other weights, so nothing of
+    them survives in the 256 MB Infinity Cache (the plain decode bench
+    repeats one routing each step). Times the routed-expert call alone (the
+    router's output is replaced by these ids). rotate=False keeps the first
+    pair every step, for comparison."""
+    import torch
+
+    from reframework_amd import _capi
+
+    x = layer.inputs(1)
+    pairs = [torch.tensor([[2 * p, 2 * p + 1]], dtype=torch.int32, device=layer.dev)
+             for p in range(layer.E // 2)]
+    w = torch.tensor([[0.6, 0.4]], dtype=torch.float32, device=layer.dev)
+    out = torch.empty(1, layer.H, dtype=torch.bfloat16, device=layer.dev)
+    plan = _capi.make_plan(1, layer.H, layer.I, layer.E, 2, _capi.BF16)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=layer.dev)
+
+    def step(i):
+        _capi.fused_experts(x, layer.w1p, layer.w2p, layer.I, w,
+                            pairs[i % len(pairs) if rotate else 0], 0, out, ws)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    alg = 2 * 3 * layer.H * layer.I * 2 + 2 * layer.H * 2
+    return {"ms": round(ms, 4), "alg_bytes": alg,
+            "hbm_gb_s": round(alg / (ms / 1000.0) / 1e9, 1),
+            "hbm_frac": round(alg / (ms / 1000.0) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
 def stage_rates(layer, T, m):
@@ -347,23 +390,42 @@ def config_finegrained(dev, steps, warmup, tokens=(8, 4096)):
             "hidden": h, "experts": e, "top_k": k, "ffn": i, "shared_experts": ns, "tokens": out}
 
 
-def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
-    """Decode through expert offload: Mixtral-shape layers whose experts live
-    in one pinned host pool per layer, synthetic routing (p=0.7 repeat,
-    Zipf(1.2)); misses stream host->HBM on the caches' copy streams. Forwards:
-    the reference's default truncation to RE_MAX_PACK=2 experts, and the exact
-    streaming forward (every routed expert). Residency, same HBM budget of 2
-    experts per layer: (i) the reference's per-layer LRU of 2, (ii) one LRU
-    over (layer, expert) shared by all layers."""
+def _progress(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, thrash_steps=32,
+                          modes=("max_pack_2_per_layer_lru", "max_pack_2_shared_pool",
+                                 "exact_per_layer_lru", "exact_shared_pool")):
+    """Decode through expert offload: a stack of Mixtral-shape layers (8
+    experts each, 352 MB per expert in bf16) whose experts live in pinned host
+    memory, with HBM room for 2 experts per layer (64 of 256 experts for 32
+    layers). Synthetic routing (bypasses the router): per layer and token,
+    p=0.7 the previous step's pair again, else two experts from Zipf(1.2).
+    Misses stream host->HBM on the caches' copy streams.
+
+    Forwards: the reference's default truncation to RE_MAX_PACK=2 experts per
+    layer, and the exact streaming forward (every routed expert). Residency,
+    same HBM budget: (i) the reference's per-layer LRU of 2 (a layer may
+    overflow it while one request needs more), (ii) one LRU over (layer,
+    expert) shared by all layers (ExpertPool of 2 x layers slots). The exact
+    forward over the shared pool cycles ~5 experts per layer and step through
+    it (no reuse survives a step), so it runs ``thrash_steps`` steps; the
+    others run ``steps``. Mode "max_pack_2_per_layer_lru_lookahead" (not in
+    the default list) attaches the lookahead predictor, which loads the
+    predicted next-step experts while the current step computes; as in the
+    reference, a forward over more than one token counts as prefill and
+    resets it, so it engages at T = 1 only."""
     import torch
 
     from reframework_amd import _capi, synth
     from reframework_amd.moe import ExpertPool, FusedMoE
 
     h, e, k, i = 4096, 8, 2, 14336
+    t_setup = time.perf_counter()
     g = torch.Generator(device=dev).manual_seed(0)
     layers = []
-    for _ in range(n_layers):
+    for li in range(n_layers):
         moe = FusedMoE(e, k, h, i, dtype=torch.bfloat16).to(dev)
         with torch.no_grad():
             for prm in moe.parameters():
@@ -371,6 +433,8 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
         moe.build_offload_cache(dev, lru_capacity=2)
         layers.append(moe)
     torch.cuda.synchronize()
+    _progress(f"offload decode: {n_layers} layers staged in pinned host memory "
+              f"({time.perf_counter() - t_setup:.0f} s)")
     # peak pinned H2D on this host: one 1 GiB copy through the same entry point
     n = 1 << 30
     src = torch.empty(n, dtype=torch.uint8, pin_memory=True)
@@ -390,7 +454,9 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
     w_d = torch.from_numpy(w_all).to(dev)
     x = (torch.randn(T, h, generator=g, device=dev) * 0.5).to(torch.bfloat16)
 
-    def run_mode(pool, exact):
+    def run_mode(tag, pool, exact, n_steps, lookahead=False):
+        t_mode = time.perf_counter()
+
         def fwd(moe, y, st, li):
             if exact:  # every routed expert (the streaming forward with one chunk)
                 return moe._forward_streaming(y, w_d[st, li], ids_d[st, li], 0)
@@ -399,6 +465,10 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
         for moe in layers:
             moe._cache.use_pool(pool)
             moe._cache.log_copies(False)
+            moe._predictor = None
+            moe._cache._predictor = None
+            if lookahead:
+                moe.attach_predictor(window=8)
         for st in range(warmup_steps):
             y = x
             for li, moe in enumerate(layers):
@@ -408,7 +478,7 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
             moe._cache.stats.reset()
             moe._cache.log_copies(True)
         t0 = time.perf_counter()
-        for st in range(warmup_steps, warmup_steps + steps):
+        for st in range(warmup_steps, warmup_steps + n_steps):
             y = x
             for li, moe in enumerate(layers):
                 y = fwd(moe, y, st, li)
@@ -416,24 +486,32 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4):
         sec = time.perf_counter() - t0
         hits = sum(m._cache.stats.hits for m in layers)
         misses = sum(m._cache.stats.misses for m in layers)
+        predicts = sum(m._cache.stats.predicts for m in layers)
         nbytes, copy_ms = 0, 0.0
         for m in layers:
             b_, ms_ = m._cache.copy_summary()
             nbytes += b_
             copy_ms += ms_
         slots = pool.n_slots if pool is not None else sum(m._cache._n_slots for m in layers)
-        return {"tokens_per_s": round(T * steps / sec, 2), "ms_per_step": round(sec * 1000.0 / steps, 3),
-                "hbm_expert_slots": slots,
+        _progress(f"offload decode: {tag} done ({time.perf_counter() - t_mode:.0f} s)")
+        return {"steps": n_steps, "tokens_per_s": round(T * n_steps / sec, 2),
+                "ms_per_step": round(sec * 1000.0 / n_steps, 3), "hbm_expert_slots": slots,
                 "hit_rate": round(hits / max(1, hits + misses), 4), "hits": hits, "misses": misses,
+                "lookahead_loads": predicts,
                 "h2d_gb_s": round(nbytes / (copy_ms / 1000.0) / 1e9, 2) if copy_ms > 0 else None,
                 "h2d_bytes": nbytes, "copy_time_frac": round(copy_ms / 1000.0 / sec, 4)}
 
-    res = {"workload": "offload decode, mixtral-shape layers, 2 HBM experts per layer",
-           "layers": n_layers, "tokens": T, "steps": steps, "peak_pinned_h2d_gb_s": round(peak_h2d, 2)}
-    for exact in (False, True):
-        tag = "exact" if exact else "max_pack_2"
-        res[f"{tag}_per_layer_lru"] = run_mode(None, exact)
-        res[f"{tag}_shared_pool"] = run_mode(ExpertPool(capacity=2 * n_layers), exact)
+    res = {"workload": f"offload decode, {n_layers} mixtral-shape layers, {2 * n_layers} of "
+                       f"{e * n_layers} experts in HBM", "layers": n_layers, "tokens": T,
+           "peak_pinned_h2d_gb_s": round(peak_h2d, 2)}
+    for mode in modes:
+        exact = mode.startswith("exact")
+        shared = mode.endswith("shared_pool")
+        res[mode] = run_mode(mode, ExpertPool(capacity=2 * n_layers) if shared else None, exact,
+                             min(steps, thrash_steps) if exact and shared else steps,
+                             lookahead=mode.endswith("lookahead"))
+    for moe in layers:
+        moe._cache.use_pool(None)
     del layers
     torch.cuda.empty_cache()
     return res
@@ -534,6 +612,11 @@ def main():
             "gate_up_ms": round(m["gate_up_ms"], 4), "down_ms": round(m["down_ms"], 4),
             "path": m["plan_path"], "down_splits": m["down_splits"],
             "stages": stage_rates(layer, tok, m)}
+        if tok == 1:
+            decode["1"]["experts_only_same_pair"] = rotating_pairs(
+                layer, max(args.steps, 40), args.warmup, rotate=False)
+            decode["1"]["experts_only_rotating_pairs"] = rotating_pairs(
+                layer, max(args.steps, 40), args.warmup)
 
     configs = {}
     names = [v.strip() for v in args.configs.split(",") if v.strip()]
@@ -544,8 +627,9 @@ def main():
     if "norm_router" in names:
         configs["norm_router"] = config_norm_router(dev, args.steps, args.warmup)
     if "offload" in names:
-        configs["offload_decode"] = config_offload_decode(dev, args.offload_layers,
-                                                          args.offload_steps)
+        configs["offload_decode"] = config_offload_decode(
+            dev, args.offload_layers, args.offload_steps, T=args.offload_tokens,
+            modes=tuple(m for m in args.offload_modes.split(",") if m))
 
     cpu = None
     if not args.skip_cpu:

@@ -101,7 +101,10 @@ const char* moe355_last_error(void);
  * entropy_k_min > 0 enables the entropy-adaptive branch of route() (:326-342):
  *   k_dyn = clamp(rint(k_min + (K-k_min)*Hnorm(p)), k_min, K); weights past k_dyn
  *   are zeroed and the rest renormalised (ids are kept).
- * logits_out [T,E] fp32 is optional (NULL to skip).
+ * logits_out [T,E] fp32 is optional (NULL to skip). Given, it also serves as
+ * the router's scratch: below 256 tokens with more than 16 experts the logits
+ * are computed by (token, 8-expert) workgroups into it and selected by a
+ * second launch (the ids then follow those logits bit for bit, as always).
  */
 int moe355_router_topk(const void* x, const void* gate, const float* bias, int T, int H, int E,
                        int K, int dtype, int renormalize, int round_logits, int entropy_k_min,

@@ -13,6 +13,7 @@ import ctypes
 import os
 import re
 import threading
+from collections import OrderedDict
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
@@ -155,9 +156,26 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else int(t.data_ptr())
 
 
+# Host arrays of expert pointers, keyed by their contents: a decode step hands
+# the same tables to every call, and building a ctypes array per call cost
+# tens of microseconds of host time per 64-expert bank (more than the router
+# kernels at decode sizes). A table holds only the pointer values, so a cached
+# one is exactly the array the call would have built.
+_TABLES: "OrderedDict[Tuple[int, ...], ctypes.Array]" = OrderedDict()
+_TABLES_MAX = 256
+
+
 def _ptr_table(ptrs: Sequence[int]):
-    arr = (ctypes.c_void_p * len(ptrs))(*ptrs)
-    return ctypes.cast(arr, _PP), arr
+    """(array to pass for a pointer-table argument, keep-alive) of ``ptrs``."""
+    key = tuple(ptrs)
+    arr = _TABLES.get(key)
+    if arr is None:
+        arr = (ctypes.c_void_p * len(key))(*key)
+        with _lock:
+            _TABLES[key] = arr
+            if len(_TABLES) > _TABLES_MAX:
+                _TABLES.popitem(last=False)
+    return arr, arr
 
 
 # ------------------------------------------------------------------ wrappers
@@ -165,15 +183,28 @@ def version() -> int:
     return int(lib().moe355_version())
 
 
+_PLANS: "OrderedDict[Tuple[int, ...], Plan]" = OrderedDict()
+
+
 def make_plan(T: int, H: int, I: int, E: int, K: int, dtype: int, path: int = -1) -> Plan:
     """Execution plan of a fused_experts call; ``path`` forces a kernel family
-    (PATH_*), -1 lets the library choose."""
+    (PATH_*), -1 lets the library choose. Plans depend on the shape (and the
+    CU count, which one kind of device shares), so they are cached; the entry
+    points only read them. Do not modify a returned plan."""
+    key = (T, H, I, E, K, dtype, path)
+    plan = _PLANS.get(key)
+    if plan is not None:
+        return plan
     plan = Plan()
     if path < 0:
         _check("moe355_make_plan", lib().moe355_make_plan(T, H, I, E, K, dtype, ctypes.byref(plan)))
     else:
         _check("moe355_make_plan_path",
                lib().moe355_make_plan_path(T, H, I, E, K, dtype, path, ctypes.byref(plan)))
+    with _lock:
+        _PLANS[key] = plan
+        if len(_PLANS) > 1024:
+            _PLANS.popitem(last=False)
     return plan
 
 

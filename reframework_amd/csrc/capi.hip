@@ -318,7 +318,7 @@ int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renorm
   if (!logits || !topk_w || !topk_ids) return fail(MOE355_EINVAL, "NULL tensor argument");
   RouterArgs a{};
   a.logits_in = logits; a.topk_w = topk_w; a.topk_ids = topk_ids;
-  a.T = T; a.E = E; a.K = K; a.renormalize = renormalize != 0;
+  a.T = T; a.E = E; a.K = K; a.renormalize = renormalize != 0; a.out_ld = K;
   return check_hip(launch_topk_from_logits(a, as_stream(stream)), "topk_from_logits launch");
 }
 

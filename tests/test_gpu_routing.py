@@ -148,3 +148,33 @@ def test_router_strided_output(T, E, K, n, dev):
     w, ids = w.cpu().numpy(), ids.cpu().numpy()
     assert np.array_equal(ids[:, :K], ids0) and np.array_equal(w[:, :K], w0)
     assert (ids[:, K:] == -9).all() and (w[:, K:] == -7.0).all()
+
+
+@pytest.mark.parametrize("T,H,E,K,kmin,ld", [(8, 2048, 64, 6, 0, 8), (1, 2048, 64, 6, 0, 6),
+                                             (200, 1024, 32, 4, 0, 4), (16, 4096, 256, 8, 3, 8),
+                                             (3, 512, 17, 2, 0, 3)])
+def test_split_router_with_logits_buffer(T, H, E, K, kmin, ld, dev):
+    """Few tokens over many experts with a logits buffer: the logits come from
+    (token, 8-expert) workgroups and a second launch selects. Logits against
+    the fp64 oracle (rounded to bf16, plus the bias), ids bit-exact and
+    weights within 1e-6 on those logits, strided rows and the
+    entropy-adaptive branch included."""
+    banner(f"split router T={T} H={H} E={E} K={K} kmin={kmin} ld={ld}")
+    g = torch.Generator().manual_seed(T * E + K)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    gate = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(E, generator=g) * 0.5
+    w = torch.full((T, ld), -7.0, dtype=torch.float32, device=dev)
+    ids = torch.full((T, ld), -9, dtype=torch.int32, device=dev)
+    lg = torch.empty((T, E), dtype=torch.float32, device=dev)
+    _capi.router_topk(x.to(dev), gate.to(dev), bias.to(dev), K, True, True, kmin, w, ids,
+                      logits_out=lg)
+    torch.cuda.synchronize()
+    lg_h, w_h, ids_h = lg.cpu().numpy(), w.cpu().numpy(), ids.cpu().numpy()
+    ref = oracle.router_logits(x, gate, bias, round_mode=1)
+    ulp = np.abs(ref - bias.numpy()[None, :]) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(lg_h - ref) <= 1.01 * ulp + 1e-6)
+    ow, oids = oracle.topk(lg_h, K, True, entropy_k_min=kmin)
+    assert np.array_equal(ids_h[:, :K], oids)
+    assert np.max(np.abs(w_h[:, :K] - ow)) <= 1e-6
+    assert (ids_h[:, K:] == -9).all() and (w_h[:, K:] == -7.0).all()
