@@ -67,15 +67,38 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
       }
     }
   } else {
-    for (int e = tid; e < a.E; e += kThreads) {
-      int tot = 0, pre = 0;
-      for (int bb = 0; bb < a.n_blocks; ++bb) {
+    // Slots of expert e in all blocks (total) and in the blocks before this
+    // one (base), from the count table. Thread tid sums expert tid % E over
+    // part tid / E of the blocks (P = min(256 / E, 8) parts; one part when
+    // E > 128) with its loads unrolled, so they are in flight together; the
+    // parts are added in LDS, at most 8 per expert. One thread per expert
+    // walking every block paid one L2 round trip per block (32 for 64 experts
+    // at 4096 tokens).
+    __shared__ int ptot[kThreads], ppre[kThreads];
+    const int P = min(kThreads / a.E, 8);
+    const int e = tid % a.E, p = tid / a.E;
+    int tot = 0, pre = 0;
+    if (p < P) {
+      const int per = (a.n_blocks + P - 1) / P;
+      const int b1 = min(a.n_blocks, (p + 1) * per);
+#pragma unroll 8
+      for (int bb = p * per; bb < b1; ++bb) {
         const int c = a.block_counts[bb * a.E + e];
         tot += c;
-        if (bb < b) pre += c;
+        pre += bb < b ? c : 0;
       }
-      total[e] = tot;
-      base[e] = pre;
+    }
+    ptot[tid] = tot;
+    ppre[tid] = pre;
+    __syncthreads();
+    for (int x = tid; x < a.E; x += kThreads) {
+      int t2 = 0, p2 = 0;
+      for (int q = 0; q < P; ++q) {
+        t2 += ptot[q * a.E + x];
+        p2 += ppre[q * a.E + x];
+      }
+      total[x] = t2;
+      base[x] = p2;
     }
   }
   __syncthreads();

@@ -359,6 +359,9 @@ __global__ __launch_bounds__(kThreads) void router_mfma_kernel(const RouterArgs 
   const int hq = a.H / 4;
   const T* xr = static_cast<const T*>(a.x) + static_cast<size_t>(min(t0 + r, a.T - 1)) * a.H +
                 wave * hq + kq * 8;
+  // Lanes past the last expert load the last expert's row again (the same
+  // addresses as its own lanes, so no extra traffic); those logits are never
+  // read. A per-lane condition on the load made each one wait in turn.
   const T* gr[NG];
 #pragma unroll
   for (int g = 0; g < NG; ++g)
@@ -367,27 +370,46 @@ __global__ __launch_bounds__(kThreads) void router_mfma_kernel(const RouterArgs 
   f32x4 acc[NG];
 #pragma unroll
   for (int g = 0; g < NG; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // U k-steps per batch, all their loads issued before the first MFMA (no
-  // exit inside a batch: a conditional exit let the compiler wait for each
-  // step's loads in turn); the remainder runs one step at a time.
+  // Batches of U k-steps in two register sets: batch b + 1's loads are issued
+  // before batch b's MFMAs, so two batches of loads are in flight and a wave
+  // pays about one memory round trip for its whole quarter of H instead of
+  // one per batch (Mixtral shape, 4096 tokens: four batches of 8 steps per
+  // wave). No exit inside a batch: a conditional exit let the compiler wait
+  // for each step's loads in turn. The remainder runs one step at a time.
   constexpr int U = NG == 1 ? 8 : 4;
-  auto batch = [&](int k, auto uc) {
-    constexpr int NU = decltype(uc)::value;
-    u32x4 av[NU], bv[NU][NG];
+  u32x4 av[2][U], bv[2][U][NG];
+  auto issue = [&](u32x4 (&ab)[U], u32x4 (&bb)[U][NG], int k) {
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      av[u] = *reinterpret_cast<const u32x4*>(xr + k + 32 * u);
+    for (int u = 0; u < U; ++u) {
+      ab[u] = *reinterpret_cast<const u32x4*>(xr + k + 32 * u);
 #pragma unroll
-      for (int g = 0; g < NG; ++g) bv[u][g] = *reinterpret_cast<const u32x4*>(gr[g] + k + 32 * u);
+      for (int g = 0; g < NG; ++g)
+        bb[u][g] = *reinterpret_cast<const u32x4*>(gr[g] + k + 32 * u);
     }
-#pragma unroll
-    for (int u = 0; u < NU; ++u)
-#pragma unroll
-      for (int g = 0; g < NG; ++g) acc[g] = Mfma16R<T>::mma(av[u], bv[u][g], acc[g]);
   };
-  int k = 0;
-  for (; k + 32 * U <= hq; k += 32 * U) batch(k, std::integral_constant<int, U>{});
-  for (; k < hq; k += 32) batch(k, std::integral_constant<int, 1>{});
+  auto compute = [&](const u32x4 (&ab)[U], const u32x4 (&bb)[U][NG]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) acc[g] = Mfma16R<T>::mma(ab[u], bb[u][g], acc[g]);
+  };
+  const int nb = hq / (32 * U);
+  if (nb > 0) issue(av[0], bv[0], 0);
+  int b = 0;
+  for (; b + 2 <= nb; b += 2) {
+    issue(av[1], bv[1], (b + 1) * 32 * U);
+    compute(av[0], bv[0]);
+    if (b + 2 < nb) issue(av[0], bv[0], (b + 2) * 32 * U);
+    compute(av[1], bv[1]);
+  }
+  if (b < nb) compute(av[0], bv[0]);
+  for (int k = nb * 32 * U; k < hq; k += 32) {
+    const u32x4 a1 = *reinterpret_cast<const u32x4*>(xr + k);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      acc[g] = Mfma16R<T>::mma(a1, *reinterpret_cast<const u32x4*>(gr[g] + k), acc[g]);
+    }
+  }
 #pragma unroll
   for (int g = 0; g < NG; ++g)
 #pragma unroll

@@ -5,9 +5,10 @@ own formulas, and every index it forms is checked against the buffer it
 addresses, before any of it runs on a GPU:
 
   * permute (count_kernel + scatter_kernel, reframework_amd/csrc/permute.hip):
-    the scatter's LDS tables (`total`, `base`, the per-wave `wave_cnt`) are
-    replayed per block, round and wave with every LDS word poisoned at kernel
-    start, so a read of a word the kernel never wrote fails; the ballot ranking
+    the scatter's LDS tables (`total`, `base`, the per-wave `wave_cnt`, the
+    per-part prefix sums over the count table) are replayed per block, round
+    and wave with every LDS word poisoned at kernel start, so a read of a word
+    the kernel never wrote fails; the ballot ranking
     is replayed bit by bit. Every slot_to_row / row_src write must stay in
     bounds, every row must be written once, and the result must equal the
     oracle's stable grouping. A planted mistake (the per-round zeroing of
@@ -62,6 +63,38 @@ def _routed(ids_flat, emap, E):
     return out
 
 
+def _emulate_prefix(counts, b, E, parts_overrun=False):
+    """The scatter's per-block prefix over the count table: thread tid sums
+    expert tid % E over block part tid // E of P = min(256 // E, 8) parts,
+    and the parts are added in LDS. Checks every count-table read and LDS
+    index."""
+    n_blocks = counts.shape[0]
+    table = counts.reshape(-1)
+    P = min(THREADS // E, 8)
+    ptot = np.full(THREADS, POISON, np.int64)
+    ppre = np.full(THREADS, POISON, np.int64)
+    for tid in range(THREADS):
+        e, p = tid % E, tid // E
+        tot = pre = 0
+        if p < P:
+            per = -(-n_blocks // P)
+            for bb in range(p * per, min(n_blocks, (p + 1) * per)):
+                idx = bb * E + e
+                assert 0 <= idx < table.size, f"count-table read {idx} outside [0, {table.size})"
+                tot += int(table[idx])
+                pre += int(table[idx]) if bb < b else 0
+        ptot[tid], ppre[tid] = tot, pre
+    total = np.zeros(E, np.int64)
+    base = np.zeros(E, np.int64)
+    for x in range(E):
+        for q in range(P + 1 if parts_overrun else P):
+            i = q * E + x
+            assert 0 <= i < THREADS and ptot[i] != POISON, f"LDS part {i} unwritten or out of range"
+            total[x] += ptot[i]
+            base[x] += ppre[i]
+    return total, base
+
+
 def emulate_permute(ids, E, tile_rows, max_tiles, emap=None, zero_first_row_only=False):
     """Replays count_kernel / scatter_kernel. Returns (offsets, slot_to_row,
     row_src, tile_map); raises AssertionError on an out-of-bounds index, a
@@ -78,8 +111,10 @@ def emulate_permute(ids, E, tile_rows, max_tiles, emap=None, zero_first_row_only
     row_src = np.full(R, POISON, np.int64)
     offsets = tile_map = None
     for b in range(n_blocks):
-        total = counts.sum(0) if n_blocks > 1 else counts[0].copy()
-        base = counts[:b].sum(0).astype(np.int64)
+        if n_blocks > 1:
+            total, base = _emulate_prefix(counts, b, E)
+        else:
+            total, base = counts[0].copy(), np.zeros(E, np.int64)
         start = np.concatenate([[0], np.cumsum(total)])
         tiles = -(-total // tile_rows)
         tile_start = np.concatenate([[0], np.cumsum(tiles)])
@@ -156,6 +191,8 @@ PERMUTE_CASES = [
     ("mixtral_t4096", lambda: _mixtral_ids(4096), 8, None),
     ("phi35_t2048", lambda: skewed_ids(2048, 2, 16, seed=3, skew=1.1), 16, None),
     ("finegrained_t8", lambda: _finegrained_ids(8), 66, None),
+    ("finegrained_t4096", lambda: _finegrained_ids(4096), 66, None),
+    ("experts256_t1500_k8", lambda: skewed_ids(1500, 8, 256, seed=5, skew=0.8), 256, None),
     ("finegrained_t700_dropped", lambda: _finegrained_ids(700, 1), 66,
      [(-1 if e % 5 == 3 else e) for e in range(66)]),
 ]
@@ -183,6 +220,16 @@ def test_permute_emulation_catches_partial_wave_table_zeroing():
     ids = _finegrained_ids(700, 1)
     with pytest.raises(AssertionError):
         emulate_permute(ids, 66, 256, 10_000, zero_first_row_only=True)
+
+
+def test_permute_prefix_emulation_catches_part_overrun():
+    """Planted mistake: summing one part too many reads past the 256 LDS
+    partial sums for 32 experts (8 parts)."""
+    counts = np.ones((40, 32), np.int64)
+    assert _emulate_prefix(counts, 3, 32)[0].tolist() == [40] * 32
+    assert _emulate_prefix(counts, 3, 32)[1].tolist() == [3] * 32
+    with pytest.raises(AssertionError):
+        _emulate_prefix(counts, 3, 32, parts_overrun=True)
 
 
 # ------------------------------------------------------------- tiled GEMM
