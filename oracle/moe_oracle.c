@@ -12,6 +12,8 @@
  *   oracle_topk           reframework/moe/fused.py:32-46 (+ moe_layer.py:326-342 entropy branch)
  *   oracle_permute        reframework/moe/fused.py:70-80, moe_layer.py:477-511 (remap/drop)
  *   oracle_fused_experts  reframework/moe/fused.py:49-87, reframework/layers/activation.py:15-59
+ *   oracle_fused_experts_bound  the same, plus the tests' per-element bound for
+ *                         fp32 evaluation (a checker bound, no reference counterpart)
  *   oracle_add_rmsnorm    reframework/layers/norm.py:27-53 (RMSNorm._forward, forward_add_residual)
  *
  * Inputs are given in their storage type (fp32, or raw bf16/f16 bits) and are
@@ -290,6 +292,130 @@ int oracle_fused_experts(const void* x, int x_type, const void* const* w1, const
     }
     free(xr);
     free(inter);
+  }
+  return 0;
+}
+
+/* ------------------------------------------- rounding-aware checker bound */
+/* Spacing of storage values (bf16: 8 significant bits; f16: 11, with the
+ * subnormal spacing 2^-24 below 2^-14) around |d|, and the distance from d to
+ * the nearest boundary between two neighbouring storage values. */
+static double storage_spacing(double d, int mode) {
+  const double a = fabs(d);
+  int e = 0;
+  if (a > 0.0) frexp(a, &e); /* a = m 2^e, m in [0.5, 1) */
+  if (mode == 1) return ldexp(1.0, (a > 0.0 ? e : -125) - 8);
+  int q = (a > 0.0 ? e : -14) - 11;
+  return ldexp(1.0, q < -24 ? -24 : q);
+}
+
+static double to_boundary(double d, int mode) {
+  const double s = storage_spacing(d, mode);
+  const double f = fabs(d) / s;
+  return fabs(f - floor(f) - 0.5) * s;
+}
+
+/* d/dg of gate_act, for the error propagation of the bound. */
+static double gate_act_slope(int act, double g) {
+  if (act == 0) {
+    const double sg = 1.0 / (1.0 + exp(-g));
+    return sg * (1.0 + g * (1.0 - sg));
+  }
+  if (act == 1) return 0.5 * (1.0 + erf(g / sqrt(2.0))) + g * exp(-0.5 * g * g) / sqrt(2.0 * M_PI);
+  const double c = sqrt(2.0 / M_PI), z = c * (g + 0.044715 * g * g * g), t = tanh(z);
+  return 0.5 * (1.0 + t) + 0.5 * g * (1.0 - t * t) * c * (1.0 + 3.0 * 0.044715 * g * g);
+}
+
+/* sum_i base[off + i] * v[i] and sum_i |base[off + i] * v[i]|. */
+static double dot_row_l1(const void* base, size_t off, int type, const double* v, int n,
+                         double* l1) {
+  double acc = 0.0, a1 = 0.0;
+  for (int i = 0; i < n; ++i) {
+    const double p = load_elem(base, off + (size_t)i, type) * v[i];
+    acc += p;
+    a1 += fabs(p);
+  }
+  *l1 = a1;
+  return acc;
+}
+
+/* oracle_fused_experts with inter_round / y_round given, plus, per output
+ * element, how far a correct fp32 evaluation may land from it beyond the
+ * output's own rounding: allow[t,h] = sum over the token's slots of |w| times
+ * (a) the fp32 accumulation error of y (6 sigma of a random walk of roundings
+ * of 2^-24 relative: 3 * 2^-24 * sum_i |inter_i w2_hi|), (b) for every
+ * intermediate whose value v may lie on either side of a rounding boundary
+ * once evaluated in fp32, the gap between its two candidate roundings times
+ * |w2_hi|, and (c) the same for y itself where y is rounded. "May lie on
+ * either side": the distance from v to the nearest boundary is within v's
+ * fp32 error estimate, |gate_act'(g)| |u| e_g + |gate_act(g)| e_u + 2^-21 |v|
+ * with e_g = 3 * 2^-24 * sum_k |x_k w1_gk| (likewise e_u), the last term for
+ * the rounding of the activation (the hardware exp2 / rcp). Only bf16 and
+ * f16 roundings (modes 1, 2) are bounded this way. A checker bound
+ * for the tests, derived from fp32 arithmetic; not the reference's algorithm. */
+int oracle_fused_experts_bound(const void* x, int x_type, const void* const* w1,
+                               const void* const* w2, int w_type, const float* topk_w,
+                               const int64_t* ids, int T, int H, int I, int E, int K, int act,
+                               int inter_round, int y_round, const int32_t* tokens, int n_tokens,
+                               double* out, double* allow) {
+  const int n = tokens ? n_tokens : T;
+  const double u24 = ldexp(1.0, -24);
+  init_half_table();
+#pragma omp parallel
+  {
+    double* xr = (double*)malloc(sizeof(double) * (size_t)H);
+    double* inter = (double*)malloc(sizeof(double) * (size_t)I);
+    double* gap = (double*)malloc(sizeof(double) * (size_t)I);
+    int* flagged = (int*)malloc(sizeof(int) * (size_t)I);
+#pragma omp for schedule(dynamic, 1)
+    for (int j = 0; j < n; ++j) {
+      const int t = tokens ? tokens[j] : j;
+      double* o = out + (size_t)t * H;
+      double* a = allow + (size_t)t * H;
+      for (int h = 0; h < H; ++h) {
+        xr[h] = load_elem(x, (size_t)t * H + h, x_type);
+        o[h] = 0.0;
+        a[h] = 0.0;
+      }
+      for (int k = 0; k < K; ++k) {
+        const int64_t e = ids[(size_t)t * K + k];
+        if (e < 0 || e >= E) continue;
+        const double wt = (double)topk_w[(size_t)t * K + k];
+        int nf = 0;
+        for (int i = 0; i < I; ++i) {
+          double lg, lu;
+          const double g = dot_row_l1(w1[e], (size_t)i * H, w_type, xr, H, &lg);
+          const double u = dot_row_l1(w1[e], (size_t)(I + i) * H, w_type, xr, H, &lu);
+          const double ag = gate_act(act, g), v = ag * u;
+          inter[i] = round_to(v, inter_round);
+          gap[i] = 0.0;
+          if (inter_round == 1 || inter_round == 2) {
+            const double err = fabs(gate_act_slope(act, g) * u) * 3.0 * u24 * lg +
+                               fabs(ag) * 3.0 * u24 * lu + 2.0 * u24 * 4.0 * fabs(v);
+            if (to_boundary(v, inter_round) <= err) {
+              gap[i] = storage_spacing(v, inter_round);
+              flagged[nf++] = i;
+            }
+          }
+        }
+        for (int h = 0; h < H; ++h) {
+          double ly;
+          const double y = dot_row_l1(w2[e], (size_t)h * I, w_type, inter, I, &ly);
+          double flip = 0.0;
+          for (int f = 0; f < nf; ++f)
+            flip += gap[flagged[f]] * fabs(load_elem(w2[e], (size_t)h * I + flagged[f], w_type));
+          double dy = 3.0 * u24 * ly + flip;
+          if ((y_round == 1 || y_round == 2) && to_boundary(y, y_round) <= dy)
+            dy += storage_spacing(y, y_round);
+          o[h] += wt * round_to(y, y_round);
+          a[h] += fabs(wt) * dy;
+        }
+      }
+    }
+    free(xr);
+    free(inter);
+    free(gap);
+    free(flagged);
   }
   return 0;
 }

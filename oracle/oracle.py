@@ -45,6 +45,9 @@ def lib() -> ctypes.CDLL:
         h.oracle_fused_experts.argtypes = [P, I, ctypes.POINTER(P), ctypes.POINTER(P), I, P, P,
                                            I, I, I, I, I, I, I, I, P, I, P]
         h.oracle_fused_experts.restype = I
+        h.oracle_fused_experts_bound.argtypes = [P, I, ctypes.POINTER(P), ctypes.POINTER(P), I, P,
+                                                 P, I, I, I, I, I, I, I, I, P, I, P, P]
+        h.oracle_fused_experts_bound.restype = I
         h.oracle_round.argtypes = [P, ctypes.c_size_t, I]
         h.oracle_round.restype = None
         h.oracle_add_rmsnorm.argtypes = [P, P, I, P, P, ctypes.c_double, I, I, P, P]
@@ -142,6 +145,40 @@ def fused_experts(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torc
                                None if tok is None else tok.ctypes.data,
                                0 if tok is None else len(tok), out.ctypes.data)
     return out
+
+
+def fused_experts_bound(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch.Tensor],
+                        topk_w: np.ndarray, ids: np.ndarray, activation: int, inter_round: int,
+                        y_round: int = ROUND_NONE, tokens: Optional[Sequence[int]] = None):
+    """(out, allow): fused_experts with the given roundings, and per output
+    element how far a correct fp32 evaluation may land from ``out`` beyond
+    the output's own rounding — the fp32 accumulation error of each slot's y
+    plus, for every intermediate (and y, where rounded) that may round to the
+    neighbouring storage value once computed in fp32, the effect of that other
+    rounding (moe_oracle.c: oracle_fused_experts_bound). A checker bound for
+    the tests, not part of the reference's algorithm."""
+    xt, tx = _raw(x)
+    w1c = [_raw(w)[0] for w in w1]
+    w2c = [_raw(w)[0] for w in w2]
+    tw = _TYPES[w1c[0].dtype]
+    T, H = xt.shape
+    I = w1c[0].shape[0] // 2
+    E = len(w1c)
+    tw_arr = np.ascontiguousarray(topk_w, dtype=np.float32)
+    id_arr = np.ascontiguousarray(ids, dtype=np.int64)
+    K = id_arr.shape[1]
+    P = ctypes.c_void_p
+    p1 = (P * E)(*[w.data_ptr() for w in w1c])
+    p2 = (P * E)(*[w.data_ptr() for w in w2c])
+    out = np.zeros((T, H), dtype=np.float64)
+    allow = np.zeros((T, H), dtype=np.float64)
+    tok = None if tokens is None else np.ascontiguousarray(tokens, dtype=np.int32)
+    lib().oracle_fused_experts_bound(xt.data_ptr(), tx, p1, p2, tw, tw_arr.ctypes.data,
+                                     id_arr.ctypes.data, T, H, I, E, K, activation, inter_round,
+                                     y_round, None if tok is None else tok.ctypes.data,
+                                     0 if tok is None else len(tok), out.ctypes.data,
+                                     allow.ctypes.data)
+    return out, allow
 
 
 def add_rmsnorm(x: torch.Tensor, residual: Optional[torch.Tensor], weight, bias, eps: float):

@@ -119,16 +119,17 @@ def _sample_tokens(ids, n_random, seed):
 def _check_sampled(out, x, w1, w2, w, ids, tokens, act=0, path=-1):
     """Sampled tokens against the fp64 oracle (<= 2e-2) and against the oracle
     that rounds the intermediate, and y where the plan's kernels do (each
-    element within its output rounding plus 1e-3 / 5e-4 of the largest);
-    plus which rounding of y the output follows."""
+    element within its output rounding plus the oracle's fp32 bound); plus
+    which rounding of y the output follows."""
     dt = w1[0].dtype
     plan = _capi.make_plan(x.shape[0], x.shape[1], w1[0].shape[0] // 2, len(w1), ids.shape[1],
                            _capi.dtype_code(dt), path)
     yr = y_round_of(plan, dt)
     got = out.float().cpu().numpy().astype(np.float64)[tokens]
     exact = oracle.fused_experts(x, w1, w2, w, ids, activation=act, tokens=tokens)[tokens]
-    rounded = oracle.fused_experts(x, w1, w2, w, ids, activation=act, inter_round=ROUND[dt],
-                                   y_round=yr, tokens=tokens)[tokens]
+    rounded, allow = oracle.fused_experts_bound(x, w1, w2, w, ids, act, ROUND[dt], y_round=yr,
+                                                tokens=tokens)
+    rounded, allow = rounded[tokens], allow[tokens]
     other = oracle.fused_experts(x, w1, w2, w, ids, activation=act, inter_round=ROUND[dt],
                                  y_round=0 if yr else ROUND[dt], tokens=tokens)[tokens]
     e1 = oracle.max_rel(got, exact)
@@ -136,7 +137,7 @@ def _check_sampled(out, x, w1, w2, w, ids, tokens, act=0, path=-1):
     print(f"  {len(tokens)} tokens, path {plan.path} splits {plan.down_splits}: max_rel vs fp64 "
           f"{e1:.2e}, vs the oracle rounding inter{' and y' if yr else ''} {e2:.2e}", flush=True)
     assert e1 <= 2e-2
-    assert_matches_rounded(got, rounded, dt, y_rounded=bool(yr))
+    assert_matches_rounded(got, rounded, allow, dt)
     assert_y_rounding(got, rounded, other, dt)
 
 
@@ -380,11 +381,14 @@ def test_finegrained_t8_layer_forward(dev):
                 + oracle.fused_experts(x, sh1, sh2, ones, zeros, inter_round=inter_round,
                                        y_round=y_round))
 
-    exact, rounded, other = ref(0, 0), ref(ROUND[torch.bfloat16], 0), ref(ROUND[torch.bfloat16], 1)
+    exact, other = ref(0, 0), ref(ROUND[torch.bfloat16], 1)
+    r1, a1 = oracle.fused_experts_bound(x, w1, w2, wn, idn, 0, ROUND[torch.bfloat16])
+    r2, a2 = oracle.fused_experts_bound(x, sh1, sh2, ones, zeros, 0, ROUND[torch.bfloat16])
+    rounded, allow = r1 + r2, a1 + a2
     e1, e2 = oracle.max_rel(got, exact), oracle.max_rel(got, rounded)
     print(f"  max_rel vs fp64 {e1:.2e}, vs the oracle rounding inter {e2:.2e}", flush=True)
     assert e1 <= 2e-2
-    assert_matches_rounded(got, rounded, torch.bfloat16)
+    assert_matches_rounded(got, rounded, allow, torch.bfloat16)
     assert_y_rounding(got, rounded, other, torch.bfloat16)
     # the shared experts are really in: the routed sum alone is far off
     assert oracle.max_rel(got, oracle.fused_experts(x, w1, w2, wn, idn)) > 0.1

@@ -76,8 +76,9 @@ def test_rmsnorm_layer_surface(dev):
     norm = RMSNorm(H, 1e-6).to(dev)
     with torch.no_grad():
         norm.weight.copy_(torch.linspace(0.5, 1.5, H))
-    x = torch.randn(6, H).to(torch.bfloat16)
-    r = torch.randn(6, H).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(47)
+    x = torch.randn(6, H, generator=g).to(torch.bfloat16)
+    r = torch.randn(6, H, generator=g).to(torch.bfloat16)
     xd, rd = x.to(dev), r.to(dev)
     f, new_r = norm.forward_add_residual(xd, rd)
     torch.cuda.synchronize()
@@ -108,8 +109,9 @@ def test_forward_with_norm_equals_norm_then_layer(T, dev):
     norm = RMSNorm(H, 1e-5).to(dev)
     with torch.no_grad():
         norm.weight.uniform_(0.5, 1.5)
-    h = torch.randn(T, H, device=dev).to(torch.bfloat16)
-    res = torch.randn(T, H, device=dev).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(53)
+    h = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    res = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
     out, new_res = moe.forward_with_norm(h, res, norm)
     f, want_res = norm.forward_add_residual(h, res)
     want = moe(f)
