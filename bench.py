@@ -156,6 +156,7 @@ def measure(layer, T, steps, warmup):
     torch.cuda.synchronize()
     stage_ms = {name: sum(e[j].elapsed_time(e[j + 1]) for e in ev) / steps
                 for j, name in enumerate(STAGES)}
+    stage_ms.update(small_stage_ms(layer, x, bufs))
     ids = bufs[3].cpu().numpy()
     routed = sorted(set(int(v) for v in ids.reshape(-1)))
     plan, ws = bufs[0], bufs[1]
@@ -164,6 +165,39 @@ def measure(layer, T, steps, warmup):
             "stage_ms": stage_ms, "layer_ev_ms": sum(stage_ms.values()),
             "routed_experts": len(routed), "plan_path": plan.path,
             "down_splits": plan.down_splits, "token_tiles": tiles}
+
+
+def small_stage_ms(layer, x, bufs, reps=20):
+    """ms per launch of the short stages (router, permute, combine): `reps`
+    back-to-back launches of one stage between two events on the kernels'
+    stream, queued behind three layer steps so the GPU never waits for the
+    host. Each launch rewrites its outputs from unchanged inputs. Recording an
+    event beside every launch of a 5-20 us kernel adds a few us of queue
+    overhead per launch that the kernel itself does not spend."""
+    import torch
+
+    from reframework_amd import _capi
+
+    plan, ws, w, ids, out = bufs
+    s = _capi.stream_handle(x.device)
+    fns = {
+        "router": lambda: _capi.router_topk(x, layer.gate, layer.bias, layer.K, True, True, 0,
+                                            w, ids, stream=s),
+        "permute": lambda: _capi.permute(plan, ids, ws, stream=s),
+        "combine": lambda: _capi.combine(plan, w, out, False, ws, stream=s),
+    }
+    res = {}
+    for name, fn in fns.items():
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(3):
+            run_layer(layer, x, bufs)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        b.synchronize()
+        res[name] = a.elapsed_time(b) / reps
+    return res
 
 
 def rotating_pairs(layer, steps, warmup, rotate=True):
@@ -205,7 +239,8 @@ def rotating_pairs(layer, steps, warmup, rotate=True):
 
 
 def stage_rates(layer, T, m):
-    """Algorithmic bytes and achieved GB/s of the HBM-bound stages: the
+    """Algorithmic bytes and achieved GB/s of the HBM-bound stages (times per
+    launch from small_stage_ms): the
     router (x and the gate read, T*K weights and ids written), the permute
     (it moves indices only: T*K ids read, slot_to_row / row_src and the
     per-block counts written; token rows are gathered by gate_up), and the
