@@ -30,7 +30,9 @@
 // tile's pipeline fill overlaps the previous tile's epilogue. The items left
 // for a last, mostly idle round are split along K over the idle CUs
 // (work_split); their fp32 partial tiles are summed (and, for gate_up,
-// activated) by gate_up_tail_fixup / down_tail_fixup.
+// activated) by gate_up_tail_fixup / down_tail_fixup. 128-row token tiles run
+// ffn_tiled_half_kernel, the same scheme with its loads split between waves
+// (described there).
 #include "dma_pipe.h"
 
 namespace moe355 {
@@ -59,21 +61,10 @@ __device__ __forceinline__ uint32_t swz8(int c, int r) {
   return static_cast<uint32_t>(c ^ ((r >> 1) & 7));
 }
 
-// Half tiles (the kernel instance for 128-row token tiles, chosen for groups
-// of about 128 rows or fewer, where 256-row tiles would be mostly padding):
-// token rows 0-63 go to LDS rows 0-63 and rows 64-127 to LDS rows 128-191, so
-// each wave of the 2x2 arrangement keeps its operand rows and multiplies only
-// its first two 32-row token blocks (8 MFMAs per sub-step instead of 16).
-// Weight loads, the pipeline and the barriers are those of full tiles.
-
-// Token row (offset in the tile) held by LDS row r; kTileT for none.
-__device__ __forceinline__ int tile_row_of(bool half, int r) {
-  if (!half) return r;
-  return r < 64 ? r : (r >= 128 && r < 192 ? r - 64 : kTileT);
-}
-
 // Token row (offset in the tile) of lane row lr of token block j of a wave
-// with token half wave_t; kTileT when the block is unused (half tiles).
+// with token half wave_t, on 256-row tiles or on the 128-row tiles of
+// ffn_tiled_half_kernel (two 32-row blocks per wave); kTileT when the block is
+// unused (the fix-up kernels serve both).
 __device__ __forceinline__ int tile_row_of_block(bool half, int wave_t, int j, int lr) {
   return half ? (j < 2 ? wave_t * 64 + j * 32 + lr : kTileT) : wave_t * 128 + j * 32 + lr;
 }
@@ -129,7 +120,7 @@ __device__ __forceinline__ Work decode_work(const FfnArgs& a, const WorkSplit& w
 // and X_{s+1} to (2s + 3) % 5, which held W_{s-1}. Weights thus have about
 // two steps to land and tokens one. Other vector-memory operations issued in
 // between (row_src prefetch, epilogue stores) only make the waits stricter.
-template <typename T, bool kGateUp, bool kHalf>
+template <typename T, bool kGateUp>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void ffn_tiled_kernel(const FfnArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kBufs * kBufBytes];
@@ -154,7 +145,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
   const uint32_t pitch = static_cast<uint32_t>(ld * 2);
 
   auto decode = [&](int L) {
-    return decode_work(a, ws, L, per_split, n_t, nk, kHalf ? kTileT / 2 : kTileT);
+    return decode_work(a, ws, L, per_split, n_t, nk, kTileT);
   };
 
   // An operand buffer is 32 loads of 1 KB, 8 rows x 128 B each; wave w issues
@@ -193,10 +184,8 @@ void ffn_tiled_kernel(const FfnArgs a) {
   int grow[kLoadsPerOp];
   auto fetch_rows = [&](const Tile& t) {
     const int ln = opaque(lane);
-    constexpr bool half = kHalf;
 #pragma unroll
-    for (int q = 0; q < kLoadsPerOp; ++q)
-      grow[q] = a.row_src[min(t.row0 + tile_row_of(half, op_row(q, ln)), t.row_end - 1)];
+    for (int q = 0; q < kLoadsPerOp; ++q) grow[q] = a.row_src[min(t.row0 + op_row(q, ln), t.row_end - 1)];
   };
   auto setup_x = [&](const Work& w) {
     const Tile& t = w.t;
@@ -204,19 +193,17 @@ void ffn_tiled_kernel(const FfnArgs a) {
     xke = w.ke;
     const int ln = opaque(lane);
     const size_t kbeg = static_cast<size_t>(t.split) * a.k_per_split;
-    // Rows past the group's end (and unused LDS rows of a half tile) load
-    // zeros: their offsets get bit 31 set (valid offsets stay below 2^31, so
+    // Rows past the group's end load zeros: their offsets get bit 31 set (valid offsets stay below 2^31, so
     // no step of K wraps them back). The bit is OR-ed into an offset computed
     // for every row alike: a select between the row offset and a constant
     // became a branch per row, and in gate_up each branch waited for all
     // loads in flight (the offset depends on the loaded row_src).
-    constexpr bool half = kHalf;
     if (kGateUp) {
       xsrc = lds_rsrc(static_cast<const char*>(a.x) + kbeg * 2);
 #pragma unroll
       for (int q = 0; q < kLoadsPerOp; ++q) {
         const int r = op_row(q, ln);
-        const uint32_t pad = t.row0 + tile_row_of(half, r) < t.row_end ? 0u : kPadOffset;
+        const uint32_t pad = t.row0 + r < t.row_end ? 0u : kPadOffset;
         xoff[q] = (static_cast<uint32_t>(grow[q]) * pitch + swz8(ln & 7, r) * 16) | pad;
       }
     } else {
@@ -224,9 +211,9 @@ void ffn_tiled_kernel(const FfnArgs a) {
                       (static_cast<size_t>(t.row0) * ld + kbeg) * 2);
 #pragma unroll
       for (int q = 0; q < kLoadsPerOp; ++q) {
-        const int r = op_row(q, ln), tr = tile_row_of(half, r);
-        const uint32_t pad = t.row0 + tr < t.row_end ? 0u : kPadOffset;
-        xoff[q] = (static_cast<uint32_t>(tr) * pitch + swz8(ln & 7, r) * 16) | pad;
+        const int r = op_row(q, ln);
+        const uint32_t pad = t.row0 + r < t.row_end ? 0u : kPadOffset;
+        xoff[q] = (static_cast<uint32_t>(r) * pitch + swz8(ln & 7, r) * 16) | pad;
       }
     }
   };
@@ -320,16 +307,14 @@ void ffn_tiled_kernel(const FfnArgs a) {
   // bw/bx) and 4 loads (issue(0..3)) are spread over the first 12 MFMAs
   // (3 MFMA : 2 LDS reads : 1 load), so neither the LDS nor the texture unit
   // sees a burst from all four waves and the last read still has 4 MFMAs to
-  // land. Half tiles multiply and read token blocks 0-1 only (8 MFMAs and 6
-  // operand reads per sub-step).
+  // land.
   auto sub = [&](const u32x4* af, const u32x4* bf, int bw, int bx, int j, u32x4* na, u32x4* nb,
                  auto issue) {
-    constexpr int NJ = kHalf ? 2 : 4, NB = NJ;
     wait_lgkm0();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int jj = 0; jj < NJ; ++jj) acc[i][jj] = Mfma32<T>::mma(af[i], bf[jj], acc[i][jj]);
+      for (int jj = 0; jj < 4; ++jj) acc[i][jj] = Mfma32<T>::mma(af[i], bf[jj], acc[i][jj]);
     // Memory operations in the order of the schedule below: the compiler keeps
     // LDS reads and direct-to-LDS loads in program order (it cannot tell that
     // they touch different buffers).
@@ -339,29 +324,18 @@ void ffn_tiled_kernel(const FfnArgs a) {
     for (int i = 0; i < 4; ++i) {
       na[i] = *reinterpret_cast<const u32x4*>(sw + arow[i] + coff[j]);
       issue(i);
-      if (i < NB) nb[i] = *reinterpret_cast<const u32x4*>(sx + brow[i] + coff[j]);
+      nb[i] = *reinterpret_cast<const u32x4*>(sx + brow[i] + coff[j]);
     }
-    if (!kHalf) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global -> LDS load
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        if (i < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      }
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global -> LDS load
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -392,7 +366,6 @@ void ffn_tiled_kernel(const FfnArgs a) {
   Work cw = decode(Lc);
   while (true) {
     const Tile& ct = cw.t;
-    constexpr bool half = kHalf;
     for (int kt = cw.kb; kt < cw.ke; ++kt) {
       const int bx = ring_add(bw, 1);
       const int nbw = ring_add(bw, 2), nbx = ring_add(bw, 3);  // step s+1
@@ -440,7 +413,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
         for (int b = 0; b < 2; ++b) {
   #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const int prow = ct.row0 + tile_row_of_block(half, wave_t, j, elr);
+            const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
             if (prow < ct.row_end) {
   #pragma unroll
               for (int q = 0; q < 4; ++q) {
@@ -474,7 +447,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
       for (int b = 0; b < 4; ++b) {
   #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int prow = ct.row0 + tile_row_of_block(half, wave_t, j, elr);
+          const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
           if (prow < ct.row_end) {
   #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -500,6 +473,386 @@ void ffn_tiled_kernel(const FfnArgs a) {
   // No direct-to-LDS write may still be in flight when the workgroup's LDS is
   // released.
   wait_vmcnt<0>();
+}
+
+// 128-row token tiles (groups of about 128 rows or fewer). Few tokens meet
+// each weight slab, so a step carries a quarter of a full tile's MFMA work
+// (~256 cycles per sub-step) and the loads' latency shows. Token rows are
+// mostly not in L2 (the weight stream evicts them) and come from the
+// Infinity Cache, ~1 us away: issued one step ahead, as in the full-tile
+// pipeline, they arrive after the barrier that waits for them. And in one
+// wave's counter loads retire in order, so waiting for tokens also waits for
+// every weight load issued before them.
+//
+// Here waves 0-1 issue all weight loads and waves 2-3 all token loads (every
+// wave still multiplies), so each wave's counter holds one kind of load only.
+// The LDS holds a ring of three 32 KB weight buffers and four 16 KB token
+// buffers (128 rows, compact), 160 KB in all: weights are issued two steps
+// ahead of their use (a plain stream reaches ~6.3 TB/s with 32 KB in flight
+// per CU), tokens three.
+//   step s, weight buffer s % 3, token buffer s % 4; sub-step j (16 k each):
+//   sub-step 0: MFMAs (s, 0), read (s, 1); W_{s+2} loads 4-7, X_{s+3} loads 4-7
+//   sub-step 1: MFMAs (s, 1), read (s, 2); W_{s+2} loads 8-11
+//   sub-step 2: MFMAs (s, 2), read (s, 3); W_{s+2} loads 12-15
+//   barrier B_s: weight waves wait until at most their 16 loads of W_{s+2} are
+//                in flight (so W_{s+1} has landed), token waves until at most
+//                their 16 of X_{s+2} and X_{s+3} (so X_{s+1} has).
+//   sub-step 3: MFMAs (s, 3), read (s+1, 0); W_{s+3} loads 0-3 into the buffer
+//               of W_s, X_{s+4} loads 0-3 into the buffer of X_s (both freed
+//               by B_s).
+// Each wave multiplies its 128 weight rows against its two 32-row token
+// blocks (token half wave_t: tile rows 64 wave_t ..); the lane layout of the
+// accumulators, the epilogue and the K-split partial tiles are those of the
+// full-tile kernel with token blocks 0-1.
+constexpr int kHalfRows = kTileT / 2;
+constexpr int kXBufBytes = kHalfRows * kSRowBytes;        // 16 KB
+constexpr int kWBufs = 3, kXBufs = 4;                      // 3 x 32 KB + 4 x 16 KB = 160 KB
+constexpr int kWLoadsPerWave = kBufBytes / 1024 / 2;       // 16 x 1 KB per weight wave
+constexpr int kXLoadsPerWave = kXBufBytes / 1024 / 2;      // 8 x 1 KB per token wave
+static_assert(kWBufs * kBufBytes + kXBufs * kXBufBytes == kBufs * kBufBytes, "LDS budget");
+
+template <typename T, bool kGateUp, bool kWeightWave>
+__device__ __forceinline__ void half_tile_waves(const FfnArgs& a, uint8_t* lds, int wave,
+                                                int lane, int Lc) {
+  const int wave_w = wave >> 1, wave_t = wave & 1;
+  const int lw = wave & 1;  // this wave's share of its kind of load
+  const int n_t = a.tile_map[0];
+  const int per_split = a.n_wtiles * n_t;
+  const int G = gridDim.x;
+  const int nk = a.k_per_split / kSK;
+  const WorkSplit ws = work_split(a.splits * per_split, G, nk, a.part_units);
+  const int n_seq = ws.n_full + ws.n_units;
+  const int ld = kGateUp ? a.H : a.I;
+  const uint32_t pitch = static_cast<uint32_t>(ld * 2);
+  auto decode = [&](int L) { return decode_work(a, ws, L, per_split, n_t, nk, kHalfRows); };
+  auto wbuf = [&](int b) { return lds + b * kBufBytes; };
+  auto xbuf = [&](int b) { return lds + kWBufs * kBufBytes + b * kXBufBytes; };
+
+  // Weight cursor (weight waves): rows (16 lw + q) * 8 + lane / 8, q < 16.
+  int wL = Lc, wkt = 0, wke = 0;
+  __amdgpu_buffer_rsrc_t wsrc;
+  uint32_t woff[kWLoadsPerWave];
+  auto w_row = [&](int q, int ln) { return (lw * kWLoadsPerWave + q) * 8 + (ln >> 3); };
+  auto setup_w = [&](const Work& w) {
+    const Tile& t = w.t;
+    wkt = w.kb;
+    wke = w.ke;
+    const int ln = opaque(lane);
+    wsrc = lds_rsrc(static_cast<const char*>(a.w[t.e]) + static_cast<size_t>(t.split) * a.k_per_split * 2,
+                    -1);
+#pragma unroll
+    for (int q = 0; q < kWLoadsPerWave; ++q) {
+      const int r = w_row(q, ln);
+      const int wr = kGateUp ? (r < kTileW / 2 ? t.wtile * (kTileW / 2) + r
+                                               : a.I + t.wtile * (kTileW / 2) + (r - kTileW / 2))
+                             : t.wtile * kTileW + r;
+      woff[q] = static_cast<uint32_t>(wr) * pitch + swz8(ln & 7, r) * 16;
+    }
+  };
+  auto advance_w = [&]() {
+    if (++wkt < wke) return;
+    if (wL + G < n_seq) {
+      wL += G;
+      setup_w(decode(wL));
+    } else {
+      wkt = wke - 1;
+    }
+  };
+  auto issue_w = [&](int b, int q0, int n) {
+    uint8_t* dst = wbuf(b) + lw * kWLoadsPerWave * 1024;
+#pragma unroll
+    for (int q = q0; q < q0 + n; ++q) dma16_rsrc(wsrc, woff[q], wkt * kSRowBytes, dst + q * 1024);
+  };
+
+  // Token cursor (token waves): tile rows (8 lw + q) * 8 + lane / 8, q < 8;
+  // gate_up rows come through row_src, fetched one item ahead.
+  int xL = Lc, xkt = 0, xke = 0;
+  __amdgpu_buffer_rsrc_t xsrc;
+  uint32_t xoff[kXLoadsPerWave];
+  int grow[kXLoadsPerWave];
+  auto x_row = [&](int q, int ln) { return (lw * kXLoadsPerWave + q) * 8 + (ln >> 3); };
+  auto fetch_rows = [&](const Tile& t) {
+    const int ln = opaque(lane);
+#pragma unroll
+    for (int q = 0; q < kXLoadsPerWave; ++q)
+      grow[q] = a.row_src[min(t.row0 + x_row(q, ln), t.row_end - 1)];
+  };
+  auto setup_x = [&](const Work& w) {
+    const Tile& t = w.t;
+    xkt = w.kb;
+    xke = w.ke;
+    const int ln = opaque(lane);
+    const size_t kbeg = static_cast<size_t>(t.split) * a.k_per_split;
+    // Rows past the group's end load zeros (offsets with bit 31 set, as in the
+    // full-tile kernel).
+    if (kGateUp) {
+      xsrc = lds_rsrc(static_cast<const char*>(a.x) + kbeg * 2);
+#pragma unroll
+      for (int q = 0; q < kXLoadsPerWave; ++q) {
+        const int r = x_row(q, ln);
+        const uint32_t pad = t.row0 + r < t.row_end ? 0u : kPadOffset;
+        xoff[q] = (static_cast<uint32_t>(grow[q]) * pitch + swz8(ln & 7, r) * 16) | pad;
+      }
+    } else {
+      xsrc = lds_rsrc(static_cast<const char*>(a.x) +
+                      (static_cast<size_t>(t.row0) * ld + kbeg) * 2);
+#pragma unroll
+      for (int q = 0; q < kXLoadsPerWave; ++q) {
+        const int r = x_row(q, ln);
+        const uint32_t pad = t.row0 + r < t.row_end ? 0u : kPadOffset;
+        xoff[q] = (static_cast<uint32_t>(r) * pitch + swz8(ln & 7, r) * 16) | pad;
+      }
+    }
+  };
+  auto prefetch_next_rows = [&]() {
+    if (kGateUp) fetch_rows(decode(xL + G < n_seq ? xL + G : xL).t);
+  };
+  auto advance_x = [&]() {
+    if (++xkt < xke) return;
+    if (xL + G < n_seq) {
+      xL += G;
+      setup_x(decode(xL));
+      prefetch_next_rows();
+    } else {
+      xkt = xke - 1;
+    }
+  };
+  auto issue_x = [&](int b, int q0, int n) {
+    uint8_t* dst = xbuf(b) + lw * kXLoadsPerWave * 1024;
+#pragma unroll
+    for (int q = q0; q < q0 + n; ++q) dma16_rsrc(xsrc, xoff[q], xkt * kSRowBytes, dst + q * 1024);
+  };
+
+  // MFMA operand rows of this wave: weight blocks as in the full-tile kernel,
+  // token blocks 64 wave_t + 32 b (b < 2) of the compact token buffer.
+  const int lr = lane & 31, kh = lane >> 5;
+  uint32_t arow[4], brow[2];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int rb = kGateUp ? (b < 2 ? wave_w * 64 + b * 32 : kTileW / 2 + wave_w * 64 + (b - 2) * 32)
+                           : wave_w * 128 + b * 32;
+    arow[b] = (rb + lr) * kSRowBytes;
+  }
+#pragma unroll
+  for (int b = 0; b < 2; ++b) brow[b] = (wave_t * 64 + b * 32 + lr) * kSRowBytes;
+  uint32_t coff[kSK / 16];
+#pragma unroll
+  for (int j = 0; j < kSK / 16; ++j) coff[j] = swz8(2 * j + kh, lr) << 4;
+
+  f32x16 acc[4][2];
+  auto acc_read = [](float x) {
+    float r;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(r) : "a"(x));
+    return r;
+  };
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  };
+  auto read_frags = [&](int bw, int bx, int j, u32x4* af, u32x4* bf) {
+    const uint8_t* sw = wbuf(bw);
+    const uint8_t* sx = xbuf(bx);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) af[b] = *reinterpret_cast<const u32x4*>(sw + arow[b] + coff[j]);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) bf[b] = *reinterpret_cast<const u32x4*>(sx + brow[b] + coff[j]);
+  };
+
+  // One sub-step: wait for its operands, 8 MFMAs; the next sub-step's 6
+  // operand reads and NL loads spread over them.
+  auto sub = [&](const u32x4* af, const u32x4* bf, int bw, int bx, int j, u32x4* na, u32x4* nb,
+                 auto issue, auto nl) {
+    constexpr int NL = decltype(nl)::value;
+    wait_lgkm0();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Mfma32<T>::mma(af[i], bf[jj], acc[i][jj]);
+    const uint8_t* sw = wbuf(bw);
+    const uint8_t* sx = xbuf(bx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      na[i] = *reinterpret_cast<const u32x4*>(sw + arow[i] + coff[j]);
+      if (i < NL) issue(i);
+      if (i < 2) nb[i] = *reinterpret_cast<const u32x4*>(sx + brow[i] + coff[j]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // LDS read
+      if (i < NL) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global -> LDS load
+      if (i < 2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  using L4 = std::integral_constant<int, 4>;
+  using L0 = std::integral_constant<int, 0>;
+  auto none = [](int) {};
+
+  // Prologue: weight waves W_0, W_1 and loads 0-3 of W_2 (wait for W_0);
+  // token waves X_0, X_1, X_2 and loads 0-3 of X_3 (wait for X_0).
+  {
+    const Work w0 = decode(Lc);
+    if (kWeightWave) {
+      setup_w(w0);
+      issue_w(0, 0, kWLoadsPerWave);
+      advance_w();
+      issue_w(1, 0, kWLoadsPerWave);
+      advance_w();
+      issue_w(2, 0, 4);
+      wait_vmcnt<kWLoadsPerWave + 4>();
+    } else {
+      if (kGateUp) fetch_rows(w0.t);
+      setup_x(w0);
+      prefetch_next_rows();
+      issue_x(0, 0, kXLoadsPerWave);
+      advance_x();
+      issue_x(1, 0, kXLoadsPerWave);
+      advance_x();
+      issue_x(2, 0, kXLoadsPerWave);
+      advance_x();
+      issue_x(3, 0, 4);
+      wait_vmcnt<2 * kXLoadsPerWave + 4>();
+    }
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+
+  zero_acc();
+  u32x4 fa[2][4], fb[2][2];
+  read_frags(0, 0, 0, fa[0], fb[0]);
+
+  int bw = 0, bx = 0;  // buffers of W_s and X_s
+  Work cw = decode(Lc);
+  while (true) {
+    const Tile& ct = cw.t;
+    for (int kt = cw.kb; kt < cw.ke; ++kt) {
+      const int nbw = bw == kWBufs - 1 ? 0 : bw + 1, nbx = (bx + 1) & (kXBufs - 1);  // step s+1
+      const int bw2 = nbw == kWBufs - 1 ? 0 : nbw + 1;                             // W_{s+2}
+      const int bx3 = (bx + 3) & (kXBufs - 1);                                     // X_{s+3}
+      if (kWeightWave) {
+        sub(fa[0], fb[0], bw, bx, 1, fa[1], fb[1], [&](int i) { issue_w(bw2, 4 + i, 1); }, L4{});
+        sub(fa[1], fb[1], bw, bx, 2, fa[0], fb[0], [&](int i) { issue_w(bw2, 8 + i, 1); }, L4{});
+        sub(fa[0], fb[0], bw, bx, 3, fa[1], fb[1], [&](int i) { issue_w(bw2, 12 + i, 1); }, L4{});
+        advance_w();
+        wait_lgkm0();
+        wait_vmcnt<kWLoadsPerWave>();
+      } else {
+        sub(fa[0], fb[0], bw, bx, 1, fa[1], fb[1], [&](int i) { issue_x(bx3, 4 + i, 1); }, L4{});
+        advance_x();
+        sub(fa[1], fb[1], bw, bx, 2, fa[0], fb[0], none, L0{});
+        sub(fa[0], fb[0], bw, bx, 3, fa[1], fb[1], none, L0{});
+        wait_lgkm0();
+        wait_vmcnt<2 * kXLoadsPerWave>();
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (kWeightWave)
+        sub(fa[1], fb[1], nbw, nbx, 0, fa[0], fb[0], [&](int i) { issue_w(bw, i, 1); }, L4{});
+      else
+        sub(fa[1], fb[1], nbw, nbx, 0, fa[0], fb[0], [&](int i) { issue_x(bx, i, 1); }, L4{});
+      bw = nbw;
+      bx = nbx;
+    }
+
+    // Epilogue, as the full-tile kernel's for token blocks 0-1.
+    const int eln = opaque(lane), elr = eln & 31, ekh = eln >> 5;
+    if (cw.unit >= 0) {
+      f32x4* pp = reinterpret_cast<f32x4*>(a.part) +
+                  static_cast<size_t>(cw.unit * 4 + wave) * kPartVecsPerWave + eln;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            pp[((i * 4 + j) * 4 + q) * kWave] =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                      acc[i][j][4 * q + 3]};
+      zero_acc();
+    } else if (kGateUp) {
+      T* inter = static_cast<T*>(a.out);
+      auto epilogue = [&](auto silu) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int prow = ct.row0 + wave_t * 64 + j * 32 + elr;
+            if (prow < ct.row_end) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int col = ct.wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * ekh;
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  v[r] = gate_act_16<decltype(silu)::value>(a.act, acc_read(acc[b][j][4 * q + r])) *
+                         acc_read(acc[b + 2][j][4 * q + r]);
+                store4<T>(inter + static_cast<size_t>(prow) * a.I + col, v[0], v[1], v[2], v[3]);
+              }
+            }
+            acc[b][j] = f32x16{};
+            acc[b + 2][j] = f32x16{};
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      };
+      if (a.act == MOE355_ACT_SILU)
+        epilogue(std::true_type{});
+      else
+        epilogue(std::false_type{});
+    } else {
+      T* y16 = static_cast<T*>(a.out);
+      float* y32 = static_cast<float*>(a.out) + static_cast<size_t>(ct.split) * a.R * a.H;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int prow = ct.row0 + wave_t * 64 + j * 32 + elr;
+          if (prow < ct.row_end) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int h = ct.wtile * kTileW + wave_w * 128 + b * 32 + 8 * q + 4 * ekh;
+              const size_t o = static_cast<size_t>(prow) * a.H + h;
+              const float v0 = acc_read(acc[b][j][4 * q]), v1 = acc_read(acc[b][j][4 * q + 1]);
+              const float v2 = acc_read(acc[b][j][4 * q + 2]), v3 = acc_read(acc[b][j][4 * q + 3]);
+              if (a.y16)
+                store4<T>(y16 + o, v0, v1, v2, v3);
+              else
+                store4<float>(y32 + o, v0, v1, v2, v3);
+            }
+          }
+          acc[b][j] = f32x16{};
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    Lc += G;
+    if (Lc >= n_seq) break;
+    cw = decode(Lc);
+  }
+  wait_vmcnt<0>();
+}
+
+template <typename T, bool kGateUp>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void ffn_tiled_half_kernel(const FfnArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kBufs * kBufBytes];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int n_t = a.tile_map[0];
+  const int n_work = a.splits * a.n_wtiles * n_t;
+  const WorkSplit ws = work_split(n_work, gridDim.x, a.k_per_split / kSK, a.part_units);
+  const int Lc = xcd_remap(blockIdx.x, gridDim.x);
+  if (Lc >= ws.n_full + ws.n_units) return;
+  if (wave < 2)
+    half_tile_waves<T, kGateUp, true>(a, lds, wave, lane, Lc);
+  else
+    half_tile_waves<T, kGateUp, false>(a, lds, wave, lane, Lc);
 }
 
 // Sums the S partial tiles of each split tail item of the tiled gate_up and
@@ -592,11 +945,11 @@ hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   a.grid = static_cast<int>(work < device_cu_count() ? work : device_cu_count());
   if (!a.part) a.part_units = 0;
   if (dtype == MOE355_BF16)
-    a.tile_rows < kTileT ? ffn_tiled_kernel<bf16, kGateUp, true><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
-                         : ffn_tiled_kernel<bf16, kGateUp, false><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    a.tile_rows < kTileT ? ffn_tiled_half_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
+                         : ffn_tiled_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else
-    a.tile_rows < kTileT ? ffn_tiled_kernel<f16, kGateUp, true><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
-                         : ffn_tiled_kernel<f16, kGateUp, false><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    a.tile_rows < kTileT ? ffn_tiled_half_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
+                         : ffn_tiled_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.part_units == 0) return err;
   // The split depends on the device-side tile count; without a tail the

@@ -19,10 +19,10 @@ addresses, before any of it runs on a GPU:
     must cover every (K-split, permuted row, weight tile) exactly once, by a
     whole item or by all S K-parts of a split item, whose partial tiles stay
     within the workspace; every token row the MFMAs read (all 256 rows of a
-    256-row tile; on 128-row tiles the two 64-row halves that sit in LDS rows
-    0-63 and 128-191) is a loaded row of the tile or a zero-filled padding
-    row, and every valid row is read; token and weight offsets stay in their
-    32-bit buffer ranges.
+    256-row tile; on 128-row tiles the 128 rows of the compact token buffer
+    that the two token-loading waves fill) is a loaded row of the tile or a
+    zero-filled padding row, and every valid row is read; token and weight
+    offsets stay in their 32-bit buffer ranges.
   * the weight-streaming kernel's in-kernel grouping (ffn_skinny.hip,
     group_small): its outputs must equal the permute's, and every tile it
     hands a workgroup must lie inside one expert's rows.
@@ -314,15 +314,22 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
             n = r1 - r0
             assert 1 <= n <= tile_rows
             half = tile_rows < 256
-            # tile row held by each LDS row (tile_row_of): 256 = none
-            held = np.where(~half | (lds_rows < 64), lds_rows,
-                            np.where((lds_rows >= 128) & (lds_rows < 192), lds_rows - 64, 256))
-            # tile rows the MFMAs read (tile_row_of_block over both token halves)
+            # tile row held by each row of the token buffer: 256 rows of the
+            # full-tile buffer; the 128 rows of the compact half-tile buffer
+            # (ffn_tiled_half_kernel), which its two token waves fill, 8 loads
+            # of 8 rows each: rows (8 w + q) * 8 + lane / 8
+            if half:
+                held = np.array(sorted((8 * w + q) * 8 + ln // 8 for w in range(2)
+                                       for q in range(8) for ln in range(0, 64, 8)))
+                assert np.array_equal(held, np.arange(128))
+            else:
+                held = lds_rows
+            # tile rows the MFMAs read: token half h (64 or 128 rows), blocks j
             nblk = 2 if half else 4
             read = {h * (64 if half else 128) + j * 32 + lr for h in range(2)
                     for j in range(nblk) for lr in range(32)}
             assert set(range(n)) <= read and max(read) < tile_rows
-            assert read <= set(held[held < 256].tolist())
+            assert read <= set(held.tolist())
             # every LDS row is loaded from a valid row or zero-filled
             valid = r0 + held < r1
             src_rows = np.minimum(r0 + np.minimum(held, tile_rows - 1), r1 - 1)
