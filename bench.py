@@ -41,9 +41,11 @@ def parse():
                     help="comma-separated token counts reported beside the headline ('' = none)")
     ap.add_argument("--configs", type=str, default="phi35moe,finegrained,offload,norm_router",
                     help="other workloads reported beside the headline ('' = none)")
-    ap.add_argument("--offload-layers", type=int, default=4)
-    ap.add_argument("--offload-steps", type=int, default=48)
+    ap.add_argument("--offload-layers", type=int, default=32)
+    ap.add_argument("--offload-steps", type=int, default=256)
     ap.add_argument("--offload-tokens", type=int, default=8)
+    ap.add_argument("--offload-host-pools", type=int, default=4,
+                    help="distinct layers' experts staged in pinned memory; deeper layers reuse them")
     ap.add_argument("--offload-modes", type=str,
                     default="max_pack_2_per_layer_lru,max_pack_2_shared_pool,exact_per_layer_lru,"
                             "exact_shared_pool",
@@ -429,15 +431,19 @@ def _progress(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, thrash_steps=32,
+def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, thrash_steps=16,
                           modes=("max_pack_2_per_layer_lru", "max_pack_2_shared_pool",
-                                 "exact_per_layer_lru", "exact_shared_pool")):
+                                 "exact_per_layer_lru", "exact_shared_pool"), host_pools=4):
     """Decode through expert offload: a stack of Mixtral-shape layers (8
     experts each, 352 MB per expert in bf16) whose experts live in pinned host
     memory, with HBM room for 2 experts per layer (64 of 256 experts for 32
     layers). Synthetic routing (bypasses the router): per layer and token,
     p=0.7 the previous step's pair again, else two experts from Zipf(1.2).
-    Misses stream host->HBM on the caches' copy streams.
+    Misses stream host->HBM on the caches' copy streams. ``host_pools``
+    distinct layers' experts are staged in pinned memory (2.8 GB each); a layer
+    l >= host_pools uses layer l mod host_pools's pool (share_host), so a
+    32-layer stack pins 4 pools instead of 32 while every layer keeps its own
+    routing, HBM slots and LRU, and each miss still copies 352 MB over PCIe.
 
     Forwards: the reference's default truncation to RE_MAX_PACK=2 experts per
     layer, and the exact streaming forward (every routed expert). Residency,
@@ -460,15 +466,21 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, thrash_step
     t_setup = time.perf_counter()
     g = torch.Generator(device=dev).manual_seed(0)
     layers = []
+    host_pools = max(1, min(host_pools, n_layers))
     for li in range(n_layers):
-        moe = FusedMoE(e, k, h, i, dtype=torch.bfloat16).to(dev)
-        with torch.no_grad():
-            for prm in moe.parameters():
-                prm.copy_(torch.randn(prm.shape, generator=g, device=dev) * 0.02)
-        moe.build_offload_cache(dev, lru_capacity=2)
+        if li < host_pools:
+            moe = FusedMoE(e, k, h, i, dtype=torch.bfloat16).to(dev)
+            with torch.no_grad():
+                for prm in moe.parameters():
+                    prm.copy_(torch.randn(prm.shape, generator=g, device=dev) * 0.02)
+            moe.build_offload_cache(dev, lru_capacity=2)
+        else:
+            moe = FusedMoE(e, k, h, i, dtype=torch.bfloat16)
+            moe.build_offload_cache(dev, lru_capacity=2, host_from=layers[li % host_pools]._cache)
+            moe = moe.to(dev)
         layers.append(moe)
     torch.cuda.synchronize()
-    _progress(f"offload decode: {n_layers} layers staged in pinned host memory "
+    _progress(f"offload decode: {n_layers} layers on {host_pools} pinned host pools "
               f"({time.perf_counter() - t_setup:.0f} s)")
     # peak pinned H2D on this host: one 1 GiB copy through the same entry point
     n = 1 << 30
@@ -538,7 +550,7 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, thrash_step
 
     res = {"workload": f"offload decode, {n_layers} mixtral-shape layers, {2 * n_layers} of "
                        f"{e * n_layers} experts in HBM", "layers": n_layers, "tokens": T,
-           "peak_pinned_h2d_gb_s": round(peak_h2d, 2)}
+           "host_pools": host_pools, "peak_pinned_h2d_gb_s": round(peak_h2d, 2)}
     for mode in modes:
         exact = mode.startswith("exact")
         shared = mode.endswith("shared_pool")
@@ -664,6 +676,7 @@ def main():
     if "offload" in names:
         configs["offload_decode"] = config_offload_decode(
             dev, args.offload_layers, args.offload_steps, T=args.offload_tokens,
+            host_pools=args.offload_host_pools,
             modes=tuple(m for m in args.offload_modes.split(",") if m))
 
     cpu = None

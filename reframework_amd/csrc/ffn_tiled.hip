@@ -311,10 +311,15 @@ void ffn_tiled_kernel(const FfnArgs a) {
   auto sub = [&](const u32x4* af, const u32x4* bf, int bw, int bx, int j, u32x4* na, u32x4* nb,
                  auto issue) {
     wait_lgkm0();
+    // Serpentine block order: consecutive MFMAs share an operand (the weight
+    // fragment along a row, the token fragment at a row change).
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) acc[i][jj] = Mfma32<T>::mma(af[i], bf[jj], acc[i][jj]);
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const int jj = (i & 1) ? 3 - j4 : j4;
+        acc[i][jj] = Mfma32<T>::mma(af[i], bf[jj], acc[i][jj]);
+      }
     // Memory operations in the order of the schedule below: the compiler keeps
     // LDS reads and direct-to-LDS loads in program order (it cannot tell that
     // they touch different buffers).

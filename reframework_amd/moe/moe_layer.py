@@ -172,16 +172,26 @@ class FusedMoE(BaseOP):
 
     # ----------------------------------------------------------- offload setup
     def build_offload_cache(self, device: torch.device, lru_capacity: int,
-                            source=None, pool=None) -> ExpertOffloadCache:
+                            source=None, pool=None,
+                            host_from: Optional[ExpertOffloadCache] = None) -> ExpertOffloadCache:
         """Stage this layer's experts into a pinned-host cache on ``device``
         and drop the per-expert parameters. ``source(e) -> (gate [I,H], up
         [I,H], down [H,I])``, when given, supplies the experts instead of the
         parameters (e.g. straight from a checkpoint). ``pool`` (an
         ExpertPool) shares one HBM slot pool and LRU with other layers
-        instead of a per-layer window of ``lru_capacity`` experts."""
+        instead of a per-layer window of ``lru_capacity`` experts.
+        ``host_from`` (another layer's cache with the same expert shapes)
+        lends its staged host pool instead: this layer's experts are then
+        that layer's weights."""
         self._cache = ExpertOffloadCache(device=device, lru_capacity=lru_capacity, dtype=self.dtype,
                                          pool=pool)
-        if source is None:
+        if host_from is not None:
+            w1_shape = (2 * self.intermediate_size, self.hidden_size)
+            if host_from.num_experts != self.num_experts or \
+                    tuple(host_from._host[0][0].shape) != w1_shape:
+                raise ValueError("host_from holds experts of another count or shape")
+            self._cache.share_host(host_from)
+        elif source is None:
             self._cache.load([{"w1": self.experts_w1[e], "w2": self.experts_w2[e]}
                               for e in range(self.num_experts)])
         else:

@@ -301,6 +301,24 @@ class ExpertOffloadCache:
             v2.copy_(d)
         self._loaded()
 
+    def share_host(self, other: "ExpertOffloadCache") -> None:
+        """Use ``other``'s staged host pool instead of staging a copy: layers
+        whose experts hold the same weights keep one pinned pool between
+        them (and a deep offload stack can be built on a host that cannot
+        pin every layer's experts). HBM slots, LRU and statistics stay this
+        cache's own; the pool stays alive while either cache holds it."""
+        if not other._host:
+            raise ValueError("the other cache has no staged experts")
+        if other.dtype != self.dtype:
+            raise ValueError(f"host pool dtype {other.dtype} != cache dtype {self.dtype}")
+        self._host_buf = other._host_buf
+        self._host = list(other._host)
+        self._host_off = list(other._host_off)
+        self._pinned = other._pinned
+        self._int8_host = []
+        self._cpu_split = False
+        self._loaded()
+
     def _alloc_pool(self, shapes) -> torch.Tensor:
         """One host buffer holding every expert's w1 then w2; pinned
         (hipHostMalloc through torch) when a GPU is present, else pageable."""

@@ -61,3 +61,26 @@ def test_reserve_respects_the_shared_capacity():
     n = A.reserve([2, 3], protect_current=[0])
     # loading 2 evicts B0 (oldest); loading 3 evicts B1; capacity is never exceeded
     assert n == 2 and set(A._lru) == {0, 2, 3} and set(B._lru) == set() and len(pool) == 3
+
+
+def test_share_host_reuses_the_pool_with_separate_residency():
+    A = _cache(None)
+    B = ExpertOffloadCache("cpu", lru_capacity=1, dtype=torch.float32)
+    B.share_host(A)
+    assert B._host_buf is A._host_buf and B.num_experts == A.num_experts
+    w1, w2, idx = B.prefetch([3])
+    assert idx == {3: 0} and torch.all(w1[0] == 3.0) and torch.all(w2[0] == 3.0)
+    assert set(B._lru) == {3} and set(A._lru) == set()
+    assert (B.stats.misses, A.stats.misses) == (1, 0)
+    A.prefetch([2])
+    assert set(A._lru) == {2} and set(B._lru) == {3}
+
+
+def test_share_host_rejects_empty_or_other_dtype():
+    import pytest
+
+    empty = ExpertOffloadCache("cpu", lru_capacity=1, dtype=torch.float32)
+    with pytest.raises(ValueError):
+        ExpertOffloadCache("cpu", lru_capacity=1, dtype=torch.float32).share_host(empty)
+    with pytest.raises(ValueError):
+        ExpertOffloadCache("cpu", lru_capacity=1, dtype=torch.float16).share_host(_cache(None))

@@ -89,3 +89,19 @@ def test_available_is_false_without_a_gpu_or_library(monkeypatch):
     monkeypatch.setattr(_capi, "LIB_PATH", "/nonexistent/libmoe355.so")
     monkeypatch.setattr(_capi, "_lib", None)
     assert moe.available() is False
+
+
+def test_offload_cache_host_from_shares_the_pool():
+    a = FusedMoE(4, 2, 32, 16, dtype=torch.float32)
+    with torch.no_grad():
+        for e, p in enumerate(a.experts_w1):
+            p.fill_(float(e))
+    ca = a.build_offload_cache(torch.device("cpu"), lru_capacity=2)
+    b = FusedMoE(4, 2, 32, 16, dtype=torch.float32)
+    cb = b.build_offload_cache(torch.device("cpu"), lru_capacity=2, host_from=ca)
+    assert cb is not ca and cb._host_buf is ca._host_buf and len(b.experts_w1) == 0
+    w1, _, idx = cb.prefetch([3])
+    assert torch.all(w1[idx[3]] == 3.0) and set(ca._lru) == set()
+    other = FusedMoE(4, 2, 32, 24, dtype=torch.float32)
+    with pytest.raises(ValueError):
+        other.build_offload_cache(torch.device("cpu"), lru_capacity=2, host_from=ca)
