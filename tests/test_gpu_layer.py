@@ -348,6 +348,46 @@ def test_shared_pool_across_layers_matches_resident(dev, monkeypatch):
     assert ev > 0 and pool.n_slots <= 3 + 2 and len(pool) <= 3 + 2
 
 
+def test_layers_sharing_host_pools_match_resident(dev, monkeypatch):
+    """Four offloaded layers on two staged host pools (layers 2 and 3 borrow
+    the pools of layers 0 and 1 through host_from, each with its own router and
+    HBM window): a chained decode equals resident layers that hold the pool
+    owners' experts and their own gates."""
+    monkeypatch.delenv("RE_CHUNK_SIZE", raising=False)
+    monkeypatch.setenv("RE_MAX_PACK", "8")
+    banner("offloaded layers sharing host pools")
+    E, K, H, I = 8, 2, 256, 256
+    refs, layers = [], []
+    for li in range(4):
+        owner = li % 2
+        r = _build(E, K, H, I, torch.bfloat16, seed=20 + owner, gate_sigma=0.2)
+        r.gate.data = _build(E, K, H, I, torch.bfloat16, seed=30 + li, gate_sigma=0.2).gate.data
+        refs.append(r.to(dev))
+        if li < 2:
+            m = _build(E, K, H, I, torch.bfloat16, seed=20 + owner, gate_sigma=0.2)
+            m.build_offload_cache(dev, lru_capacity=2)
+        else:
+            m = FusedMoE(num_experts=E, top_k=K, hidden_size=H, intermediate_size=I,
+                         dtype=torch.bfloat16)
+            m.build_offload_cache(dev, lru_capacity=2, host_from=layers[owner]._cache)
+        m.gate.data = refs[li].gate.data.clone()
+        layers.append(m)
+    assert layers[2]._cache._host_buf is layers[0]._cache._host_buf
+    outs, wants = [], []
+    for step in range(6):
+        x = synth.make_tokens(2, H, torch.bfloat16, seed=200 + step).to(dev)
+        y, z = x, x
+        for m, r in zip(layers, refs):
+            y = m(y)
+            z = r(z)
+        outs.append(y)
+        wants.append(z)
+    torch.cuda.synchronize()
+    for o, w in zip(outs, wants):
+        assert torch.allclose(o.float(), w.float(), rtol=0, atol=2e-3 * w.float().abs().max().item())
+    assert all(m._cache.stats.misses > 0 for m in layers)
+
+
 def test_substitute_aliases_hbm_slot_then_refills(dev, monkeypatch):
     """Similarity substitution on HBM slots (reference: offload_cache.py:713-
     732): a miss served by the most similar resident expert makes the kernels
