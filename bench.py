@@ -643,7 +643,7 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                 "traffic": measured_traffic(T),
-                "kernel": "ffn_tiled_kernel<bf16, gate_up>",
+                "kernel": "ffn_tiled16_kernel<bf16, gate_up>",
                 "flops_per_launch": gemm1_flops, "avg_launch_ms": round(head["gate_up_ms"], 4)}
 
     decode = {}

@@ -92,6 +92,25 @@ struct Mfma32<f16> {
   }
 };
 
+template <typename T>
+struct Mfma16;
+
+template <>
+struct Mfma16<bf16> {
+  __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma16<f16> {
+  __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
 // One work item of the persistent grouped-GEMM kernels.
 struct Tile {
   int split, wtile, e, row0, row_end;

@@ -7,7 +7,7 @@
 // sizes.
 //
 // Tile: 256 weight rows x 256 token rows, 4 waves in a 2x2 arrangement, each
-// wave owning 4x4 blocks of v_mfma_f32_32x32x16 (a 128x128 sub-tile, 256 fp32
+// wave owning 8x8 blocks of v_mfma_f32_16x16x32 (a 128x128 sub-tile, 256 fp32
 // accumulators). Weight rows are the MFMA M side and tokens the N side, so each
 // lane ends up holding 4 consecutive output features of one token and stores
 // them as one vector.
@@ -30,9 +30,9 @@
 // tile's pipeline fill overlaps the previous tile's epilogue. The items left
 // for a last, mostly idle round are split along K over the idle CUs
 // (work_split); their fp32 partial tiles are summed (and, for gate_up,
-// activated) by gate_up_tail_fixup / down_tail_fixup. 128-row token tiles run
-// ffn_tiled_half_kernel, the same scheme with its loads split between waves
-// (described there).
+// activated) by the fix-up kernels. 128-row token tiles run
+// ffn_tiled_half_kernel, the same scheme on v_mfma_f32_32x32x16 with its loads
+// split between waves (described there).
 #include "dma_pipe.h"
 
 namespace moe355 {
@@ -104,25 +104,43 @@ __device__ __forceinline__ Work decode_work(const FfnArgs& a, const WorkSplit& w
 // continuous stream; two load cursors (weights, tokens) walk it ahead of the
 // MFMAs and cross into the next item while the current one is still being
 // multiplied, so no workgroup launch or pipeline fill is paid per tile.
+// Operand W_s (weights of step s) sits in LDS buffer (2s) % 5, X_s (tokens) in
+// (2s + 1) % 5; W_{s+2} goes to the buffer of X_{s-1} and X_{s+2} to that of
+// W_s, so weights have about two steps to land and tokens one.
 //
-// Pipeline, step s (64 k = four 16-k sub-steps of 16 MFMAs per wave). Operand
-// W_s (weights) sits in LDS buffer (2s) % 5, X_s (tokens) in (2s + 1) % 5.
-//   sub-step 0: MFMAs of (s, 0); read operands (s, 1); issue X_{s+1} loads 4-7
-//   sub-step 1: MFMAs of (s, 1); read operands (s, 2); issue W_{s+2} loads 0-3
-//   sub-step 2: MFMAs of (s, 2); read operands (s, 3); issue W_{s+2} loads 4-7
-//   barrier B_s: each wave waits until at most its 8 W_{s+2} loads are in
-//                flight, so W_{s+1} and X_{s+1} have landed; after it no wave
-//                reads the buffers of step s again (the operands of (s, 3) are
-//                in registers).
-//   sub-step 3: MFMAs of (s, 3); read operands (s+1, 0); issue X_{s+2} loads
-//               0-3 into the buffer of W_s, freed by B_s.
-// W_{s+2} goes to buffer (2s + 4) % 5, which held X_{s-1} (freed by B_{s-1}),
-// and X_{s+1} to (2s + 3) % 5, which held W_{s-1}. Weights thus have about
-// two steps to land and tokens one. Other vector-memory operations issued in
-// between (row_src prefetch, epilogue stores) only make the waits stricter.
+// Each wave's 128x128 sub-tile is 8x8 blocks of v_mfma_f32_16x16x32 (64
+// accumulators of 4 fp32). On random bf16 operands this MFMA does 15 % more
+// FLOPs per joule than v_mfma_f32_32x32x16 (a probe with every SIMD busy on
+// either: 2.13 against 1.85 PFLOP/s at the power limit), and the kernel is
+// power bound (Mixtral shape, 4096 tokens: gate_up 1.64 -> 1.52 ms). A step is
+// two 32-k sub-steps of 64 MFMAs per wave:
+//   sub-step 0: MFMAs (s, 0); read (s, 1); issue X_{s+1} loads 4-7, then
+//               W_{s+2} loads 0-3
+//   barrier B_s: at most those 4 W_{s+2} loads in flight (vmcnt(4)), so
+//               W_{s+1} and X_{s+1} have landed; step s's buffers are no
+//               longer read
+//   sub-step 1: MFMAs (s, 1); read (s+1, 0); issue W_{s+2} loads 4-7, then
+//               X_{s+2} loads 0-3 into the buffer of W_s
+// Operand fragments: lane l reads row (l & 15) of a 16-row block at logical
+// chunk 4h + (l >> 4) of the 128-byte row (k 32h + 8 (l >> 4) .. +7); 16 lanes
+// of one chunk hit 16 distinct bank groups under swz8. Lane l of output block
+// (bi, bj) holds features 4 (l >> 4) + 0..3 of weight block bi and token
+// (l & 15) of token block bj.
+// c += a * b on v_mfma_f32_16x16x32 with the accumulator pinned to AGPRs and
+// tied to the result (compiled MFMAs on 64 f32x4 accumulators came out with
+// results in other registers than their accumulators and AGPR copies between
+// them).
+template <typename T>
+__device__ __forceinline__ void mfma16_agpr(f32x4& c, const u32x4& a, const u32x4& b) {
+  if constexpr (std::is_same<T, bf16>::value)
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
 template <typename T, bool kGateUp>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void ffn_tiled_kernel(const FfnArgs a) {
+void ffn_tiled16_kernel(const FfnArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kBufs * kBufBytes];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -134,28 +152,16 @@ void ffn_tiled_kernel(const FfnArgs a) {
   const int n_work = a.splits * per_split;
   const int G = gridDim.x;
   const int nk = a.k_per_split / kSK;
-  // Work sequence L0, L0 + G, ...: whole items below ws.n_full, then at most
-  // one tail unit per workgroup.
   const WorkSplit ws = work_split(n_work, G, nk, a.part_units);
   const int n_seq = ws.n_full + ws.n_units;
-  int Lc = xcd_remap(blockIdx.x, G);  // work item being multiplied
+  int Lc = xcd_remap(blockIdx.x, G);
   if (Lc >= n_seq) return;
 
-  const int ld = kGateUp ? a.H : a.I;  // elements per weight row and per token row
+  const int ld = kGateUp ? a.H : a.I;
   const uint32_t pitch = static_cast<uint32_t>(ld * 2);
-
-  auto decode = [&](int L) {
-    return decode_work(a, ws, L, per_split, n_t, nk, kTileT);
-  };
-
-  // An operand buffer is 32 loads of 1 KB, 8 rows x 128 B each; wave w issues
-  // loads q = 0..7, covering rows 8 (8 w + q) + i / 8 for lane i. Lane i writes
-  // physical chunk i % 8 of its row, so it fetches that row's logical chunk
-  // swz8(i % 8, row) (the swizzle is an involution) from global memory.
+  auto decode = [&](int L) { return decode_work(a, ws, L, per_split, n_t, nk, kTileT); };
   auto op_row = [&](int q, int ln) { return (wave * kLoadsPerOp + q) * 8 + (ln >> 3); };
 
-  // Weight cursor: work item wL, step wkt of [.., wke); source base and
-  // per-load offsets.
   int wL = Lc, wkt = 0, wke = 0;
   __amdgpu_buffer_rsrc_t wsrc;
   uint32_t woff[kLoadsPerOp];
@@ -176,8 +182,6 @@ void ffn_tiled_kernel(const FfnArgs a) {
     }
   };
 
-  // Token cursor: work item xL, step xkt of [.., xke). gate_up token rows come
-  // through row_src; they are fetched one item ahead.
   int xL = Lc, xkt = 0, xke = 0;
   __amdgpu_buffer_rsrc_t xsrc;
   uint32_t xoff[kLoadsPerOp];
@@ -193,11 +197,7 @@ void ffn_tiled_kernel(const FfnArgs a) {
     xke = w.ke;
     const int ln = opaque(lane);
     const size_t kbeg = static_cast<size_t>(t.split) * a.k_per_split;
-    // Rows past the group's end load zeros: their offsets get bit 31 set (valid offsets stay below 2^31, so
-    // no step of K wraps them back). The bit is OR-ed into an offset computed
-    // for every row alike: a select between the row offset and a constant
-    // became a branch per row, and in gate_up each branch waited for all
-    // loads in flight (the offset depends on the loaded row_src).
+    // Rows past the group's end load zeros (offsets with bit 31 set).
     if (kGateUp) {
       xsrc = lds_rsrc(static_cast<const char*>(a.x) + kbeg * 2);
 #pragma unroll
@@ -217,15 +217,9 @@ void ffn_tiled_kernel(const FfnArgs a) {
       }
     }
   };
-  // Unconditional (past the last item it fetches the current item's rows
-  // again): a conditional load leaves two values of grow to merge, and the
-  // register copies that merge them wait for the loads to land (vmcnt(0)).
   auto prefetch_next_rows = [&]() {
     if (kGateUp) fetch_rows(decode(xL + G < n_seq ? xL + G : xL).t);
   };
-  // Step a cursor to its next step; past the last work item it stays on its
-  // final step, so the tail keeps issuing (harmless, in-bounds) loads into
-  // buffers nobody reads and the vmcnt accounting of the pipeline stays fixed.
   auto advance_w = [&]() {
     if (++wkt < wke) return;
     if (wL + G < n_seq) {
@@ -245,108 +239,88 @@ void ffn_tiled_kernel(const FfnArgs a) {
       xkt = xke - 1;
     }
   };
-  // Loads q0 .. q0+n-1 of a cursor's current step into LDS buffer b.
-  auto issue_w = [&](int b, int q0, int n) {
-    uint8_t* dst = lds + b * kBufBytes + wave * kLoadsPerOp * 1024;
-#pragma unroll
-    for (int q = q0; q < q0 + n; ++q) dma16_rsrc(wsrc, woff[q], wkt * kSRowBytes, dst + q * 1024);
+  auto issue_w = [&](int b, int q) {
+    dma16_rsrc(wsrc, woff[q], wkt * kSRowBytes, lds + b * kBufBytes + (wave * kLoadsPerOp + q) * 1024);
   };
-  auto issue_x = [&](int b, int q0, int n) {
-    uint8_t* dst = lds + b * kBufBytes + wave * kLoadsPerOp * 1024;
-#pragma unroll
-    for (int q = q0; q < q0 + n; ++q) dma16_rsrc(xsrc, xoff[q], xkt * kSRowBytes, dst + q * 1024);
+  auto issue_x = [&](int b, int q) {
+    dma16_rsrc(xsrc, xoff[q], xkt * kSRowBytes, lds + b * kBufBytes + (wave * kLoadsPerOp + q) * 1024);
   };
 
-  // MFMA operand rows of this wave inside a buffer.
-  const int lr = lane & 31, kh = lane >> 5;
-  uint32_t arow[4], brow[4];
+  // MFMA operand rows of this wave: weight blocks bi (gate_up: 0-3 gate rows
+  // 64 wave_w + 16 bi, 4-7 the matching up rows), token blocks 128 wave_t + 16 bj.
+  const int lr = lane & 15, kq = lane >> 4;
+  uint32_t arow[8], brow[8];
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    int rb;
-    if (kGateUp)
-      rb = b < 2 ? wave_w * 64 + b * 32 : kTileW / 2 + wave_w * 64 + (b - 2) * 32;
-    else
-      rb = wave_w * 128 + b * 32;
+  for (int b = 0; b < 8; ++b) {
+    const int rb = kGateUp ? (b < 4 ? wave_w * 64 + b * 16 : kTileW / 2 + wave_w * 64 + (b - 4) * 16)
+                           : wave_w * 128 + b * 16;
     arow[b] = (rb + lr) * kSRowBytes;
-    brow[b] = (wave_t * 128 + b * 32 + lr) * kSRowBytes;
+    brow[b] = (wave_t * 128 + b * 16 + lr) * kSRowBytes;
   }
-  // Operand rows start at multiples of 32, so the swizzle bits are lr's.
-  uint32_t coff[kSK / 16];
+  // Block rows start at multiples of 16, so the swizzle bits are lr's.
+  uint32_t coff[2];
 #pragma unroll
-  for (int j = 0; j < kSK / 16; ++j) coff[j] = swz8(2 * j + kh, lr) << 4;
+  for (int h = 0; h < 2; ++h) coff[h] = swz8(4 * h + kq, lr) << 4;
 
-  f32x16 acc[4][4];
-
-  // Accumulator element to a VGPR at the point of use. Read all at once at
-  // the loop exit, the 256 accumulators would need 256 VGPRs next to the
-  // AGPRs that hold them and spill.
+  f32x4 acc[8][8];
   auto acc_read = [](float x) {
     float r;
     asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(r) : "a"(x));
     return r;
   };
-  auto zero_acc = [&]() {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  };
-
-  auto read_frags = [&](int bw, int bx, int j, u32x4* af, u32x4* bf) {
-    const uint8_t* sw = lds + bw * kBufBytes;
-    const uint8_t* sx = lds + bx * kBufBytes;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      af[b] = *reinterpret_cast<const u32x4*>(sw + arow[b] + coff[j]);
-      bf[b] = *reinterpret_cast<const u32x4*>(sx + brow[b] + coff[j]);
-    }
-  };
-
-  // One sub-step: wait for its operands (read during the previous sub-step),
-  // then 16 MFMAs; the next sub-step's 8 operand reads (sub-step j of buffers
-  // bw/bx) and 4 loads (issue(0..3)) are spread over the first 12 MFMAs
-  // (3 MFMA : 2 LDS reads : 1 load), so neither the LDS nor the texture unit
-  // sees a burst from all four waves and the last read still has 4 MFMAs to
-  // land.
-  auto sub = [&](const u32x4* af, const u32x4* bf, int bw, int bx, int j, u32x4* na, u32x4* nb,
-                 auto issue) {
-    wait_lgkm0();
-    // Serpentine block order: consecutive MFMAs share an operand (the weight
-    // fragment along a row, the token fragment at a row change).
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        const int jj = (i & 1) ? 3 - j4 : j4;
-        acc[i][jj] = Mfma32<T>::mma(af[i], bf[jj], acc[i][jj]);
-      }
-    // Memory operations in the order of the schedule below: the compiler keeps
-    // LDS reads and direct-to-LDS loads in program order (it cannot tell that
-    // they touch different buffers).
-    const uint8_t* sw = lds + bw * kBufBytes;
-    const uint8_t* sx = lds + bx * kBufBytes;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      na[i] = *reinterpret_cast<const u32x4*>(sw + arow[i] + coff[j]);
-      issue(i);
-      nb[i] = *reinterpret_cast<const u32x4*>(sx + brow[i] + coff[j]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global -> LDS load
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  // The MFMAs are assembly, out of the compiler's hazard checks: an MFMA
+  // reading as accumulator an AGPR that a VALU op wrote needs 2 wait states
+  // (after zeroing), and a read of an MFMA result needs up to 11 for these
+  // 4-pass MFMAs (before the epilogue); mfma_nops() gives 24.
+  auto mfma_nops = []() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n s_nop 7\n s_nop 7");
     __builtin_amdgcn_sched_barrier(0);
   };
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{};
+    mfma_nops();
+  };
+  auto read_frags = [&](int bw, int bx, int h, u32x4* af, u32x4* bf) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      af[b] = *reinterpret_cast<const u32x4*>(lds + bw * kBufBytes + arow[b] + coff[h]);
+      bf[b] = *reinterpret_cast<const u32x4*>(lds + bx * kBufBytes + brow[b] + coff[h]);
+    }
+  };
 
-  // Prologue: W_0, X_0, W_1 and the first half of X_1 (the loads sub-step 3
-  // of step -1 would issue), then wait for W_0 and X_0 and read the operands
-  // of (0, 0).
+  // One sub-step: wait for its operands, then 64 MFMAs with the next
+  // sub-step's 16 operand reads after MFMAs 1, 4, .., 46 and its NL loads after
+  // MFMAs 2, 5, ..; the last 16 MFMAs give the last reads time to land. The
+  // MFMAs are volatile assembly, so this program order is the issue order (the
+  // reads and loads cannot move across them).
+  auto sub = [&](const u32x4* af, const u32x4* bf, int bw, int bx, int h, u32x4* na, u32x4* nb,
+                 auto issue, auto nl) {
+    constexpr int NL = decltype(nl)::value;
+    wait_lgkm0();
+    const uint8_t* sw = lds + bw * kBufBytes;
+    const uint8_t* sx = lds + bx * kBufBytes;
+#pragma unroll
+    for (int m = 0; m < 64; ++m) {
+      const int i = m >> 3, j = m & 7;
+      mfma16_agpr<T>(acc[i][j], af[i], bf[j]);
+      if (m % 3 == 1 && m / 3 < 16) {
+        const int r = m / 3;  // reads A0 B0 A1 B1 ..
+        if (r & 1)
+          nb[r >> 1] = *reinterpret_cast<const u32x4*>(sx + brow[r >> 1] + coff[h]);
+        else
+          na[r >> 1] = *reinterpret_cast<const u32x4*>(sw + arow[r >> 1] + coff[h]);
+      }
+      if (m % 3 == 2 && m / 3 < NL) issue(m / 3);
+    }
+  };
+  using L8 = std::integral_constant<int, 8>;
+
+  // Prologue: W_0, X_0, W_1 and the first half of X_1 (the loads sub-step 1
+  // of step -1 would issue), then wait for W_0 and X_0 and read (0, 0).
   {
     const Work w0 = decode(Lc);
     if (kGateUp) fetch_rows(w0.t);
@@ -354,17 +328,21 @@ void ffn_tiled_kernel(const FfnArgs a) {
     setup_x(w0);
     prefetch_next_rows();
   }
-  issue_w(0, 0, kLoadsPerOp);
+#pragma unroll
+  for (int q = 0; q < kLoadsPerOp; ++q) issue_w(0, q);
   advance_w();
-  issue_x(1, 0, kLoadsPerOp);
+#pragma unroll
+  for (int q = 0; q < kLoadsPerOp; ++q) issue_x(1, q);
   advance_x();
-  issue_w(2, 0, kLoadsPerOp);
+#pragma unroll
+  for (int q = 0; q < kLoadsPerOp; ++q) issue_w(2, q);
   advance_w();
-  issue_x(3, 0, kLoadsPerOp / 2);
+#pragma unroll
+  for (int q = 0; q < kLoadsPerOp / 2; ++q) issue_x(3, q);
   dma_barrier<kLoadsPerOp + kLoadsPerOp / 2>();  // W_0 and X_0 landed
 
   zero_acc();
-  u32x4 fa[2][4], fb[2][4];
+  u32x4 fa[2][8], fb[2][8];
   read_frags(0, 1, 0, fa[0], fb[0]);
 
   int bw = 0;  // buffer of W_s (X_s is in the next one)
@@ -375,108 +353,103 @@ void ffn_tiled_kernel(const FfnArgs a) {
       const int bx = ring_add(bw, 1);
       const int nbw = ring_add(bw, 2), nbx = ring_add(bw, 3);  // step s+1
       const int bw2 = ring_add(bw, 4);                          // W_{s+2}
-      // X_{s+1} loads 4-7 (its buffer is nbx), then its cursor moves to X_{s+2}.
+      // X_{s+1} loads 4-7 (its buffer is nbx), then its cursor moves on;
+      // W_{s+2} loads 0-3.
       sub(fa[0], fb[0], bw, bx, 1, fa[1], fb[1],
-          [&](int i) { issue_x(nbx, kLoadsPerOp / 2 + i, 1); });
+          [&](int i) {
+            if (i < 4)
+              issue_x(nbx, kLoadsPerOp / 2 + i);
+            else
+              issue_w(bw2, i - 4);
+          },
+          L8{});
       advance_x();
-      sub(fa[1], fb[1], bw, bx, 2, fa[0], fb[0], [&](int i) { issue_w(bw2, i, 1); });
-      sub(fa[0], fb[0], bw, bx, 3, fa[1], fb[1],
-          [&](int i) { issue_w(bw2, kLoadsPerOp / 2 + i, 1); });
-      advance_w();
-      // W_{s+1} and X_{s+1} landed (only W_{s+2} may be in flight) and every
-      // wave has read its last operands of step s.
+      // W_{s+1} and X_{s+1} landed (only W_{s+2} loads 0-3 may be in flight)
+      // and every wave has read its last operands of step s.
       wait_lgkm0();
-      dma_barrier<kLoadsPerOp>();
-      // X_{s+2} loads 0-3 into the buffer of W_s.
-      sub(fa[1], fb[1], nbw, nbx, 0, fa[0], fb[0], [&](int i) { issue_x(bw, i, 1); });
+      dma_barrier<kLoadsPerOp / 2>();
+      // W_{s+2} loads 4-7, then X_{s+2} loads 0-3 into the buffer of W_s.
+      sub(fa[1], fb[1], nbw, nbx, 0, fa[0], fb[0],
+          [&](int i) {
+            if (i < 4)
+              issue_w(bw2, kLoadsPerOp / 2 + i);
+            else
+              issue_x(bw, i - 4);
+          },
+          L8{});
+      advance_w();
       bw = nbw;
     }
 
-    // Epilogue. Lane (lr, kh) of block (i, j) holds, for q = 0..3, features
-    // 8q + 4kh + 0..3 of the 32-row weight block and token lr of the token block.
-    const int eln = opaque(lane), elr = eln & 31, ekh = eln >> 5;
+    mfma_nops();
+    const int eln = opaque(lane), elr = eln & 15, ekq = eln >> 4;
     if (cw.unit >= 0) {
-      // K-part of a split tail item: raw fp32 accumulators to its partial slot.
+      // K-part of a split tail item: raw fp32 accumulators to its partial slot,
+      // block by block (each store 1 KB contiguous).
       f32x4* pp = reinterpret_cast<f32x4*>(a.part) +
                   static_cast<size_t>(cw.unit * 4 + wave) * kPartVecsPerWave + eln;
-  #pragma unroll
-      for (int i = 0; i < 4; ++i)
-  #pragma unroll
-        for (int j = 0; j < 4; ++j)
-  #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            pp[((i * 4 + j) * 4 + q) * kWave] =
-                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                      acc[i][j][4 * q + 3]};
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pp[(i * 8 + j) * kWave] = acc[i][j];
       zero_acc();
     } else if (kGateUp) {
       T* inter = static_cast<T*>(a.out);
-      // The activation is chosen once per tile, so the SiLU epilogue has no
-      // per-element branch.
       auto epilogue = [&](auto silu) {
-  #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-  #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
-            if (prow < ct.row_end) {
-  #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const int col = ct.wtile * (kTileW / 2) + wave_w * 64 + b * 32 + 8 * q + 4 * ekh;
-                float v[4];
-  #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                  v[r] = gate_act_16<decltype(silu)::value>(a.act, acc_read(acc[b][j][4 * q + r])) *
-                         acc_read(acc[b + 2][j][4 * q + r]);
-                store4<T>(inter + static_cast<size_t>(prow) * a.I + col, v[0], v[1], v[2], v[3]);
-              }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int prow = ct.row0 + wave_t * 128 + j * 16 + elr;
+          if (prow < ct.row_end) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int col = ct.wtile * (kTileW / 2) + wave_w * 64 + i * 16 + 4 * ekq;
+              float v[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                v[r] = gate_act_16<decltype(silu)::value>(a.act, acc_read(acc[i][j][r])) *
+                       acc_read(acc[i + 4][j][r]);
+              store4<T>(inter + static_cast<size_t>(prow) * a.I + col, v[0], v[1], v[2], v[3]);
             }
-            // One (b, j) pair at a time, its accumulators cleared in place:
-            // keeps the epilogue's temporaries within the register file.
-            acc[b][j] = f32x16{};
-            acc[b + 2][j] = f32x16{};
-            __builtin_amdgcn_sched_barrier(0);
           }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i][j] = f32x4{};
+          __builtin_amdgcn_sched_barrier(0);
         }
       };
       if (a.act == MOE355_ACT_SILU)
         epilogue(std::true_type{});
       else
         epilogue(std::false_type{});
+      mfma_nops();
     } else {
-      // y rows: fp32 partials of this item's K-split, or (y16: one split) the
-      // layer dtype, as the reference's bf16 `inter @ w2[e].t()` returns.
       T* y16 = static_cast<T*>(a.out);
       float* y32 = static_cast<float*>(a.out) + static_cast<size_t>(ct.split) * a.R * a.H;
-  #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-  #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int prow = ct.row0 + wave_t * 128 + j * 32 + elr;
-          if (prow < ct.row_end) {
-  #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int h = ct.wtile * kTileW + wave_w * 128 + b * 32 + 8 * q + 4 * ekh;
-              const size_t o = static_cast<size_t>(prow) * a.H + h;
-              const float v0 = acc_read(acc[b][j][4 * q]), v1 = acc_read(acc[b][j][4 * q + 1]);
-              const float v2 = acc_read(acc[b][j][4 * q + 2]), v3 = acc_read(acc[b][j][4 * q + 3]);
-              if (a.y16)
-                store4<T>(y16 + o, v0, v1, v2, v3);
-              else
-                store4<float>(y32 + o, v0, v1, v2, v3);
-            }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int prow = ct.row0 + wave_t * 128 + j * 16 + elr;
+        if (prow < ct.row_end) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int h = ct.wtile * kTileW + wave_w * 128 + i * 16 + 4 * ekq;
+            const size_t o = static_cast<size_t>(prow) * a.H + h;
+            const float v0 = acc_read(acc[i][j][0]), v1 = acc_read(acc[i][j][1]);
+            const float v2 = acc_read(acc[i][j][2]), v3 = acc_read(acc[i][j][3]);
+            if (a.y16)
+              store4<T>(y16 + o, v0, v1, v2, v3);
+            else
+              store4<float>(y32 + o, v0, v1, v2, v3);
           }
-          acc[b][j] = f32x16{};
-          __builtin_amdgcn_sched_barrier(0);
         }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i][j] = f32x4{};
+        __builtin_amdgcn_sched_barrier(0);
       }
+      mfma_nops();
     }
     Lc += G;
     if (Lc >= n_seq) break;
     cw = decode(Lc);
   }
-  // No direct-to-LDS write may still be in flight when the workgroup's LDS is
-  // released.
   wait_vmcnt<0>();
 }
 
@@ -934,6 +907,65 @@ __global__ __launch_bounds__(kThreads) void down_tail_fixup(const FfnArgs a) {
   }
 }
 
+// The fix-ups for ffn_tiled16_kernel's partial tiles (8x8 blocks of 16x16 per
+// wave, block (i, j) at vectors (i * 8 + j) * 64 + lane). gate_up: task (item,
+// i < 4, j) sums gate block i and up block i + 4 against token block j;
+// down: task (item, i, j).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void gate_up_tail_fixup16(const FfnArgs a) {
+  const int n_t = a.tile_map[0];
+  const int per_split = a.n_wtiles * n_t;
+  const int nk = a.k_per_split / kSK;
+  const WorkSplit ws = work_split(a.splits * per_split, a.grid, nk, a.part_units);
+  const int tasks = ws.n_units / ws.S * 32;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int wave_w = wave >> 1, wave_t = wave & 1, lr = lane & 15, kq = lane >> 4;
+  T* inter = static_cast<T*>(a.out);
+  for (int task = blockIdx.x; task < tasks; task += gridDim.x) {
+    const int it = task >> 5, i = (task >> 3) & 3, j = task & 7;
+    const Tile t = decode_tile(a, ws.n_full + it, per_split, n_t, a.tile_rows);
+    const int prow = t.row0 + wave_t * 128 + j * 16 + lr;
+    if (prow >= t.row_end) continue;
+    f32x4 g = {}, u = {};
+    for (int p = 0; p < ws.S; ++p) {
+      const f32x4* pp = reinterpret_cast<const f32x4*>(a.part) +
+                        static_cast<size_t>((it * ws.S + p) * 4 + wave) * kPartVecsPerWave + lane;
+      g += pp[(i * 8 + j) * kWave];
+      u += pp[((i + 4) * 8 + j) * kWave];
+    }
+    const int col = t.wtile * (kTileW / 2) + wave_w * 64 + i * 16 + 4 * kq;
+    store4<T>(inter + static_cast<size_t>(prow) * a.I + col, gate_act_fast(a.act, g[0]) * u[0],
+              gate_act_fast(a.act, g[1]) * u[1], gate_act_fast(a.act, g[2]) * u[2],
+              gate_act_fast(a.act, g[3]) * u[3]);
+  }
+}
+
+template <typename Y>
+__global__ __launch_bounds__(kThreads) void down_tail_fixup16(const FfnArgs a) {
+  const int n_t = a.tile_map[0];
+  const int per_split = a.n_wtiles * n_t;
+  const int nk = a.k_per_split / kSK;
+  const WorkSplit ws = work_split(a.splits * per_split, a.grid, nk, a.part_units);
+  const int tasks = ws.n_units / ws.S * 64;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int wave_w = wave >> 1, wave_t = wave & 1, lr = lane & 15, kq = lane >> 4;
+  for (int task = blockIdx.x; task < tasks; task += gridDim.x) {
+    const int it = task >> 6, i = (task >> 3) & 7, j = task & 7;
+    const Tile t = decode_tile(a, ws.n_full + it, per_split, n_t, a.tile_rows);
+    const int prow = t.row0 + wave_t * 128 + j * 16 + lr;
+    if (prow >= t.row_end) continue;
+    f32x4 v = {};
+    for (int p = 0; p < ws.S; ++p) {
+      const f32x4* pp = reinterpret_cast<const f32x4*>(a.part) +
+                        static_cast<size_t>((it * ws.S + p) * 4 + wave) * kPartVecsPerWave + lane;
+      v += pp[(i * 8 + j) * kWave];
+    }
+    Y* y = static_cast<Y*>(a.out) + static_cast<size_t>(t.split) * a.R * a.H;
+    const int h = t.wtile * kTileW + wave_w * 128 + i * 16 + 4 * kq;
+    store4<Y>(y + static_cast<size_t>(prow) * a.H + h, v[0], v[1], v[2], v[3]);
+  }
+}
+
 template <bool kGateUp>
 hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   const long work = static_cast<long>(args.n_wtiles) * args.max_tiles * args.splits;
@@ -949,16 +981,30 @@ hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   a.group_t = -1;
   a.grid = static_cast<int>(work < device_cu_count() ? work : device_cu_count());
   if (!a.part) a.part_units = 0;
+  const bool half = a.tile_rows < kTileT;
   if (dtype == MOE355_BF16)
-    a.tile_rows < kTileT ? ffn_tiled_half_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
-                         : ffn_tiled_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    half ? ffn_tiled_half_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
+         : ffn_tiled16_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else
-    a.tile_rows < kTileT ? ffn_tiled_half_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
-                         : ffn_tiled_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    half ? ffn_tiled_half_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
+         : ffn_tiled16_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.part_units == 0) return err;
   // The split depends on the device-side tile count; without a tail the
   // fix-up finds no task and exits.
+  if (!half) {
+    if (!kGateUp && !a.y16)
+      down_tail_fixup16<float><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    else if (!kGateUp && dtype == MOE355_BF16)
+      down_tail_fixup16<bf16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    else if (!kGateUp)
+      down_tail_fixup16<f16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    else if (dtype == MOE355_BF16)
+      gate_up_tail_fixup16<bf16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    else
+      gate_up_tail_fixup16<f16><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+    return hipGetLastError();
+  }
   if (!kGateUp && !a.y16)
     down_tail_fixup<float><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else if (!kGateUp && dtype == MOE355_BF16)

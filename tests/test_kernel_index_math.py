@@ -325,9 +325,12 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
             else:
                 held = lds_rows
             # tile rows the MFMAs read: token half h (64 or 128 rows), blocks j
-            nblk = 2 if half else 4
-            read = {h * (64 if half else 128) + j * 32 + lr for h in range(2)
-                    for j in range(nblk) for lr in range(32)}
+            # (two 32-row blocks of v_mfma_f32_32x32x16 on half tiles, eight
+            # 16-row blocks of v_mfma_f32_16x16x32 on full tiles)
+            if half:
+                read = {h * 64 + j * 32 + lr for h in range(2) for j in range(2) for lr in range(32)}
+            else:
+                read = {h * 128 + j * 16 + lr for h in range(2) for j in range(8) for lr in range(16)}
             assert set(range(n)) <= read and max(read) < tile_rows
             assert read <= set(held.tolist())
             # every LDS row is loaded from a valid row or zero-filled
@@ -351,9 +354,11 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
         split, wt, e, r0, r1 = decode_tile(it)
         whole[split, r0:r1, wt] += 1
     assert (whole == 1).all(), "a (split, row, weight tile) is not covered exactly once"
-    # fix-up tasks cover the split items' rows once
-    tasks = n_units // S * (8 if gate_up else 16)
-    assert tasks == len(parts) * (8 if gate_up else 16)
+    # fix-up tasks cover the split items' rows once: per item, gate blocks x
+    # token blocks (gate_up) or weight blocks x token blocks (down)
+    per_item = (8 if gate_up else 16) if tile_rows < 256 else (32 if gate_up else 64)
+    tasks = n_units // S * per_item
+    assert tasks == len(parts) * per_item
     return n_seq
 
 
