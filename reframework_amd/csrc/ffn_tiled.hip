@@ -106,7 +106,7 @@ __device__ __forceinline__ Work decode_work(const FfnArgs& a, const WorkSplit& w
 // multiplied, so no workgroup launch or pipeline fill is paid per tile.
 // Operand W_s (weights of step s) sits in LDS buffer (2s) % 5, X_s (tokens) in
 // (2s + 1) % 5; W_{s+2} goes to the buffer of X_{s-1} and X_{s+2} to that of
-// W_s, so weights have about two steps to land and tokens one.
+// W_s.
 //
 // Each wave's 128x128 sub-tile is 8x8 blocks of v_mfma_f32_16x16x32 (64
 // accumulators of 4 fp32). On random bf16 operands this MFMA does 15 % more
@@ -114,13 +114,13 @@ __device__ __forceinline__ Work decode_work(const FfnArgs& a, const WorkSplit& w
 // either: 2.13 against 1.85 PFLOP/s at the power limit), and the kernel is
 // power bound (Mixtral shape, 4096 tokens: gate_up 1.64 -> 1.52 ms). A step is
 // two 32-k sub-steps of 64 MFMAs per wave:
-//   sub-step 0: MFMAs (s, 0); read (s, 1); issue X_{s+1} loads 4-7, then
-//               W_{s+2} loads 0-3
-//   barrier B_s: at most those 4 W_{s+2} loads in flight (vmcnt(4)), so
-//               W_{s+1} and X_{s+1} have landed; step s's buffers are no
-//               longer read
-//   sub-step 1: MFMAs (s, 1); read (s+1, 0); issue W_{s+2} loads 4-7, then
-//               X_{s+2} loads 0-3 into the buffer of W_s
+//   sub-step 0: MFMAs (s, 0); read (s, 1); issue W_{s+2}
+//   barrier B_s: at most the 8 W_{s+2} loads in flight (vmcnt(8)), so W_{s+1}
+//               and X_{s+1} have landed; step s's buffers are no longer read
+//   sub-step 1: MFMAs (s, 1); read (s+1, 0); issue X_{s+2} into the buffer of
+//               W_s
+// Tokens thus get ~1.5 sub-steps of lead and weights ~3 (a token tile is
+// mostly not in L2 when its first CU of an XCD asks for it).
 // Operand fragments: lane l reads row (l & 15) of a 16-row block at logical
 // chunk 4h + (l >> 4) of the 128-byte row (k 32h + 8 (l >> 4) .. +7); 16 lanes
 // of one chunk hit 16 distinct bank groups under swz8. Lane l of output block
@@ -319,8 +319,8 @@ void ffn_tiled16_kernel(const FfnArgs a) {
   };
   using L8 = std::integral_constant<int, 8>;
 
-  // Prologue: W_0, X_0, W_1 and the first half of X_1 (the loads sub-step 1
-  // of step -1 would issue), then wait for W_0 and X_0 and read (0, 0).
+  // Prologue: W_0, X_0, W_1 and X_1 (the loads sub-step 1 of step -1 would
+  // issue), then wait for W_0 and X_0 and read (0, 0).
   {
     const Work w0 = decode(Lc);
     if (kGateUp) fetch_rows(w0.t);
@@ -338,8 +338,9 @@ void ffn_tiled16_kernel(const FfnArgs a) {
   for (int q = 0; q < kLoadsPerOp; ++q) issue_w(2, q);
   advance_w();
 #pragma unroll
-  for (int q = 0; q < kLoadsPerOp / 2; ++q) issue_x(3, q);
-  dma_barrier<kLoadsPerOp + kLoadsPerOp / 2>();  // W_0 and X_0 landed
+  for (int q = 0; q < kLoadsPerOp; ++q) issue_x(3, q);
+  advance_x();
+  dma_barrier<2 * kLoadsPerOp>();  // W_0 and X_0 landed
 
   zero_acc();
   u32x4 fa[2][8], fb[2][8];
@@ -353,31 +354,16 @@ void ffn_tiled16_kernel(const FfnArgs a) {
       const int bx = ring_add(bw, 1);
       const int nbw = ring_add(bw, 2), nbx = ring_add(bw, 3);  // step s+1
       const int bw2 = ring_add(bw, 4);                          // W_{s+2}
-      // X_{s+1} loads 4-7 (its buffer is nbx), then its cursor moves on;
-      // W_{s+2} loads 0-3.
-      sub(fa[0], fb[0], bw, bx, 1, fa[1], fb[1],
-          [&](int i) {
-            if (i < 4)
-              issue_x(nbx, kLoadsPerOp / 2 + i);
-            else
-              issue_w(bw2, i - 4);
-          },
-          L8{});
-      advance_x();
-      // W_{s+1} and X_{s+1} landed (only W_{s+2} loads 0-3 may be in flight)
-      // and every wave has read its last operands of step s.
-      wait_lgkm0();
-      dma_barrier<kLoadsPerOp / 2>();
-      // W_{s+2} loads 4-7, then X_{s+2} loads 0-3 into the buffer of W_s.
-      sub(fa[1], fb[1], nbw, nbx, 0, fa[0], fb[0],
-          [&](int i) {
-            if (i < 4)
-              issue_w(bw2, kLoadsPerOp / 2 + i);
-            else
-              issue_x(bw, i - 4);
-          },
-          L8{});
+      // W_{s+2} (its buffer held X_{s-1}, freed by B_{s-1}).
+      sub(fa[0], fb[0], bw, bx, 1, fa[1], fb[1], [&](int i) { issue_w(bw2, i); }, L8{});
       advance_w();
+      // W_{s+1} and X_{s+1} landed (only W_{s+2} may be in flight) and every
+      // wave has read its last operands of step s.
+      wait_lgkm0();
+      dma_barrier<kLoadsPerOp>();
+      // X_{s+2} into the buffer of W_s.
+      sub(fa[1], fb[1], nbw, nbx, 0, fa[0], fb[0], [&](int i) { issue_x(bw, i); }, L8{});
+      advance_x();
       bw = nbw;
     }
 
