@@ -138,6 +138,16 @@ __device__ __forceinline__ void mfma16_agpr(f32x4& c, const u32x4& a, const u32x
     asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
 }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Four values rounded to T (bf16 or f16), packed in two dwords.
+template <typename T>
+__device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  const T4 v = {from_f32<T>(a), from_f32<T>(b), from_f32<T>(c), from_f32<T>(d)};
+  return __builtin_bit_cast(u32x2, v);
+}
+
 template <typename T, bool kGateUp>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void ffn_tiled16_kernel(const FfnArgs a) {
@@ -408,28 +418,55 @@ void ffn_tiled16_kernel(const FfnArgs a) {
         epilogue(std::false_type{});
       mfma_nops();
     } else {
-      T* y16 = static_cast<T*>(a.out);
-      float* y32 = static_cast<float*>(a.out) + static_cast<size_t>(ct.split) * a.R * a.H;
+      // y: the 4 lanes holding one token row's features of a block (lanes
+      // r, r + 16, r + 32, r + 48) are far apart, so a store straight from
+      // the MFMA layout reaches memory as 64 separate 8-byte pieces. A lane
+      // permutation first (lane 4 r + q takes lane r + 16 q's values) puts each
+      // row's 32 bytes in 4 consecutive lanes; the stores then coalesce into
+      // 16 row pieces (down at 1408-wide K: epilogue 11.7 -> 6.8 k cycles).
+      const int pr = eln >> 2, pq = eln & 3;
+      const int psrc = (pr + 16 * pq) << 2;
+      auto perm = [&](uint32_t v) {
+        return static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(psrc, static_cast<int>(v)));
+      };
+      auto store_y = [&](auto* y) {
+        using O = typename std::remove_pointer<decltype(y)>::type;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int prow = ct.row0 + wave_t * 128 + j * 16 + elr;
-        if (prow < ct.row_end) {
+        for (int j = 0; j < 8; ++j) {
+          const int prow = ct.row0 + wave_t * 128 + j * 16 + pr;
+          O* yr = y + static_cast<size_t>(prow) * a.H + (ct.wtile * kTileW + wave_w * 128 + 4 * pq);
+          if constexpr (sizeof(O) == 4) {
+            u32x4 q[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int h = ct.wtile * kTileW + wave_w * 128 + i * 16 + 4 * ekq;
-            const size_t o = static_cast<size_t>(prow) * a.H + h;
-            const float v0 = acc_read(acc[i][j][0]), v1 = acc_read(acc[i][j][1]);
-            const float v2 = acc_read(acc[i][j][2]), v3 = acc_read(acc[i][j][3]);
-            if (a.y16)
-              store4<T>(y16 + o, v0, v1, v2, v3);
-            else
-              store4<float>(y32 + o, v0, v1, v2, v3);
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) q[i][r] = perm(__builtin_bit_cast(uint32_t, acc_read(acc[i][j][r])));
+            if (prow < ct.row_end) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(yr + i * 16) = q[i];
+            }
+          } else {
+            u32x2 q[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const u32x2 pk = pack4<O>(acc_read(acc[i][j][0]), acc_read(acc[i][j][1]),
+                                        acc_read(acc[i][j][2]), acc_read(acc[i][j][3]));
+              q[i] = u32x2{perm(pk[0]), perm(pk[1])};
+            }
+            if (prow < ct.row_end) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x2*>(yr + i * 16) = q[i];
+            }
           }
-        }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i][j] = f32x4{};
-        __builtin_amdgcn_sched_barrier(0);
-      }
+          for (int i = 0; i < 8; ++i) acc[i][j] = f32x4{};
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      if (a.y16)
+        store_y(static_cast<T*>(a.out));
+      else
+        store_y(static_cast<float*>(a.out) + static_cast<size_t>(ct.split) * a.R * a.H);
       mfma_nops();
     }
     Lc += G;
