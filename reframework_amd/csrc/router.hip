@@ -9,6 +9,7 @@
 #include <climits>
 
 #include "common.h"
+#include "dma_pipe.h"
 
 namespace moe355 {
 namespace {
@@ -340,76 +341,99 @@ struct Mfma16R<f16> {
 
 // Prefill-sized router on MFMA: 16 tokens per workgroup, the 4 waves splitting
 // H in quarters. Each wave multiplies its 16 token rows (A, 16 x 32 per step)
-// by 16-expert groups of gate rows (B) with v_mfma_f32_16x16x32, operands
-// loaded straight from global memory in MFMA layout (lane l: row l % 16, k
-// chunk l / 16); the 4 quarter sums are added in fixed order through LDS.
-// Lane l then holds logits of tokens 4 (l / 16) + 0..3 for expert l % 16 of
-// each group. A group of 16 lanes per token does the softmax and top-k
-// (group16_topk).
+// by 16-expert groups of gate rows (B) with v_mfma_f32_16x16x32; the 4
+// quarter sums are added in fixed order through LDS. Lane l then holds logits
+// of tokens 4 (l / 16) + 0..3 for expert l % 16 of each group. A group of 16
+// lanes per token does the softmax and top-k (group16_topk).
+// Operands go through the LDS: a wave streams its quarter of the token and
+// gate rows in batches of 64 k (128 bytes of each row) with direct-to-LDS
+// loads of 8 whole rows each, up to 7 batches in flight in its own ring, and reads them
+// back in MFMA layout (16-byte chunks XOR-swizzled by row, conflict free).
+// Loading the MFMA layout straight from memory put the 4 lanes of a row 16
+// lanes apart, so every load left as 64 separate 16-byte pieces, and the
+// kernel took ~10 us at 8 experts and ~17 us at 64 whatever the token count
+// (now 8.5 and 12.3 us at 4096 tokens, H = 4096 and 2048).
 // The fp32 VALU router re-reads the gate per 8 tokens and spends E*H FMAs per
 // token on the VALU: at 4096 tokens, 64 experts and H = 2048 it took 54 us.
 template <typename T, int NG>
 __global__ __launch_bounds__(kThreads) void router_mfma_kernel(const RouterArgs a) {
-  constexpr int kTok = 16, EP = 16 * NG;
-  __shared__ float part[kThreads / kWave][kTok][EP];
-  __shared__ float lg[kTok][EP];
+  constexpr int kTok = 16, EP = 16 * NG, kRows = kTok + EP;
+  constexpr int kLoads = kRows / 8;  // direct-to-LDS loads per batch
+  constexpr int kBuf = kRows * 128;  // bytes per batch buffer
+  constexpr int kWaves = kThreads / kWave;
+  // Buffers per wave: as many as 160 KB hold (a workgroup has a CU to itself
+  // at these token counts), all but one in flight: ~110 KB per CU, what a
+  // CU needs at ~1.5 us of load latency.
+  constexpr int kNB = NG == 1 ? 8 : NG == 2 ? 6 : 4;
+  static_assert(kWaves * kNB * kBuf <= 160 * 1024, "LDS");
+  static_assert((kNB - 1) * kLoads < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) uint8_t stage[kWaves][kNB][kBuf];
+  // After the K loop the ring holds the quarter sums and the logits.
+  typedef float Part[kWaves][kTok][EP];
+  typedef float Lg[kTok][EP];
+  static_assert(sizeof(Part) + sizeof(Lg) <= sizeof(stage), "LDS reuse");
+  Part& part = *reinterpret_cast<Part*>(&stage[0][0][0]);
+  Lg& lg = *reinterpret_cast<Lg*>(&stage[0][0][0] + sizeof(Part));
   const int t0 = blockIdx.x * kTok;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int r = lane & 15, kq = lane >> 4;
-  const int hq = a.H / 4;
-  const T* xr = static_cast<const T*>(a.x) + static_cast<size_t>(min(t0 + r, a.T - 1)) * a.H +
-                wave * hq + kq * 8;
-  // Lanes past the last expert load the last expert's row again (the same
-  // addresses as its own lanes, so no extra traffic); those logits are never
-  // read. A per-lane condition on the load made each one wait in turn.
-  const T* gr[NG];
+  const int hq = a.H / kWaves;
+  const uint32_t pitch = static_cast<uint32_t>(a.H) * sizeof(T);
+  // Load q covers batch rows 8 q .. 8 q + 7 (rows 0-15 tokens t0.., then gate
+  // rows): lane l takes row 8 q + l / 8 and lands in its LDS chunk l % 8,
+  // which holds logical chunk (l % 8) ^ ((row >> 1) & 7). Token rows past T
+  // and gate rows past E load the last row again (never read back).
+  const __amdgpu_buffer_rsrc_t xsrc =
+      pipe::lds_rsrc(static_cast<const T*>(a.x) + static_cast<size_t>(t0) * a.H + wave * hq);
+  const __amdgpu_buffer_rsrc_t gsrc = pipe::lds_rsrc(static_cast<const T*>(a.gate) + wave * hq);
+  uint32_t voff[kLoads];
 #pragma unroll
-  for (int g = 0; g < NG; ++g)
-    gr[g] = static_cast<const T*>(a.gate) + static_cast<size_t>(min(16 * g + r, a.E - 1)) * a.H +
-            wave * hq + kq * 8;
+  for (int q = 0; q < kLoads; ++q) {
+    const int row = 8 * q + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+    const int src = row < kTok ? min(t0 + row, a.T - 1) - t0 : min(row - kTok, a.E - 1);
+    voff[q] = static_cast<uint32_t>(src) * pitch + c * 16;
+  }
+  auto issue = [&](int b) {
+    uint8_t* dst = &stage[wave][b % kNB][0];
+#pragma unroll
+    for (int q = 0; q < kLoads; ++q)
+      pipe::dma16_rsrc(q < kTok / 8 ? xsrc : gsrc, voff[q], b * 128, dst + q * 1024);
+  };
+  // Fragment of batch row `row`, step u (32 k) of the batch: lane (r, kq) reads
+  // logical chunk 4 u + kq.
+  auto frag = [&](const uint8_t* buf, int row, int u) {
+    return *reinterpret_cast<const u32x4*>(buf + row * 128 + (((4 * u + kq) ^ ((row >> 1) & 7)) << 4));
+  };
   f32x4 acc[NG];
 #pragma unroll
   for (int g = 0; g < NG; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Batches of U k-steps in two register sets: batch b + 1's loads are issued
-  // before batch b's MFMAs, so two batches of loads are in flight and a wave
-  // pays about one memory round trip for its whole quarter of H instead of
-  // one per batch (Mixtral shape, 4096 tokens: four batches of 8 steps per
-  // wave). No exit inside a batch: a conditional exit let the compiler wait
-  // for each step's loads in turn. The remainder runs one step at a time.
-  constexpr int U = NG == 1 ? 8 : 4;
-  u32x4 av[2][U], bv[2][U][NG];
-  auto issue = [&](u32x4 (&ab)[U], u32x4 (&bb)[U][NG], int k) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      ab[u] = *reinterpret_cast<const u32x4*>(xr + k + 32 * u);
-#pragma unroll
-      for (int g = 0; g < NG; ++g)
-        bb[u][g] = *reinterpret_cast<const u32x4*>(gr[g] + k + 32 * u);
+  const int nb = hq / 64;
+  for (int b = 0; b < kNB - 1 && b < nb; ++b) issue(b);
+  for (int b = 0; b < nb; ++b) {
+    // The buffer of batch b + kNB - 1 held batch b - 1, whose reads have
+    // completed. Then wait until only the batches after b are in flight.
+    if (b + kNB - 1 < nb) issue(b + kNB - 1);
+    switch (min(nb - 1 - b, kNB - 1)) {
+      case 0: pipe::wait_vmcnt<0>(); break;
+      case 1: pipe::wait_vmcnt<kLoads>(); break;
+      case 2: pipe::wait_vmcnt<2 * kLoads>(); break;
+      case 3: pipe::wait_vmcnt<3 * kLoads>(); break;
+      case 4: pipe::wait_vmcnt<4 * kLoads>(); break;
+      case 5: pipe::wait_vmcnt<(kNB > 5 ? 5 : 1) * kLoads>(); break;
+      case 6: pipe::wait_vmcnt<(kNB > 6 ? 6 : 1) * kLoads>(); break;
+      default: pipe::wait_vmcnt<(kNB > 7 ? 7 : 1) * kLoads>(); break;
     }
-  };
-  auto compute = [&](const u32x4 (&ab)[U], const u32x4 (&bb)[U][NG]) {
+    const uint8_t* buf = &stage[wave][b % kNB][0];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < 2; ++u) {
+      const u32x4 av = frag(buf, r, u);
 #pragma unroll
-      for (int g = 0; g < NG; ++g) acc[g] = Mfma16R<T>::mma(ab[u], bb[u][g], acc[g]);
-  };
-  const int nb = hq / (32 * U);
-  if (nb > 0) issue(av[0], bv[0], 0);
-  int b = 0;
-  for (; b + 2 <= nb; b += 2) {
-    issue(av[1], bv[1], (b + 1) * 32 * U);
-    compute(av[0], bv[0]);
-    if (b + 2 < nb) issue(av[0], bv[0], (b + 2) * 32 * U);
-    compute(av[1], bv[1]);
-  }
-  if (b < nb) compute(av[0], bv[0]);
-  for (int k = nb * 32 * U; k < hq; k += 32) {
-    const u32x4 a1 = *reinterpret_cast<const u32x4*>(xr + k);
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      acc[g] = Mfma16R<T>::mma(a1, *reinterpret_cast<const u32x4*>(gr[g] + k), acc[g]);
+      for (int g = 0; g < NG; ++g) acc[g] = Mfma16R<T>::mma(av, frag(buf, kTok + 16 * g + r, u), acc[g]);
     }
+    pipe::wait_lgkm0();
   }
+  __syncthreads();
 #pragma unroll
   for (int g = 0; g < NG; ++g)
 #pragma unroll
@@ -517,7 +541,7 @@ hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
     // the smaller sizes, where one workgroup per 1-8 tokens has the lowest
     // latency (256-768 tokens: 7.8 against 9.5 us at 8 experts; at 64
     // experts MFMA wins from 256 tokens, 17 against 23 us).
-    if ((a.T >= 1024 || (a.T >= 256 && a.E > 16)) && a.K <= 8 && a.E <= 64 && a.H % 128 == 0) {
+    if ((a.T >= 1024 || (a.T >= 256 && a.E > 16)) && a.K <= 8 && a.E <= 64 && a.H % 256 == 0) {
       const dim3 grid((a.T + 15) / 16);
       if (a.E <= 16)
         router_mfma_kernel<T, 1><<<grid, block, 0, s>>>(a);
