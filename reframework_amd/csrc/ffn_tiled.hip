@@ -33,6 +33,7 @@
 // activated) by the fix-up kernels. 128-row token tiles run
 // ffn_tiled_half_kernel, the same scheme on v_mfma_f32_32x32x16 with its loads
 // split between waves (described there).
+#include "acc_regs.h"
 #include "dma_pipe.h"
 
 namespace moe355 {
@@ -126,16 +127,27 @@ __device__ __forceinline__ Work decode_work(const FfnArgs& a, const WorkSplit& w
 // of one chunk hit 16 distinct bank groups under swz8. Lane l of output block
 // (bi, bj) holds features 4 (l >> 4) + 0..3 of weight block bi and token
 // (l & 15) of token block bj.
-// c += a * b on v_mfma_f32_16x16x32 with the accumulator pinned to AGPRs and
-// tied to the result (compiled MFMAs on 64 f32x4 accumulators came out with
-// results in other registers than their accumulators and AGPR copies between
-// them).
-template <typename T>
-__device__ __forceinline__ void mfma16_agpr(f32x4& c, const u32x4& a, const u32x4& b) {
+// c += a * b on v_mfma_f32_16x16x32 for accumulator block n, pinned to
+// a[4n .. 4n+3] (acc_regs.h). The compiler holds no accumulator values (with
+// compiled MFMAs on 64 f32x4 accumulators it had put results in other
+// registers than their accumulators and copied between them).
+template <typename T, int n>
+__device__ __forceinline__ void mfma16_acc(u32x4 a, u32x4 b) {
   if constexpr (std::is_same<T, bf16>::value)
-    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    accr::mfma_bf16<n>(a, b);
   else
-    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    accr::mfma_f16<n>(a, b);
+}
+
+// f(std::integral_constant<int, k>) for k = B .. E-1, expanded at compile
+// time (accumulator registers are named by literal strings, so every index
+// that reaches them must be a constant).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -272,12 +284,15 @@ void ffn_tiled16_kernel(const FfnArgs a) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) coff[h] = swz8(4 * h + kq, lr) << 4;
 
-  f32x4 acc[8][8];
-  auto acc_read = [](float x) {
-    float r;
-    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(r) : "a"(x));
-    return r;
+  // Accumulator block (i, j) is AGPR block 8 i + j (a[4 (8 i + j) ..]); the
+  // indices are integral constants.
+  auto acc_at = [](auto i, auto j, auto r) {
+    return accr::get<4 * (8 * decltype(i)::value + decltype(j)::value) + decltype(r)::value>();
   };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
   // The MFMAs are assembly, out of the compiler's hazard checks: an MFMA
   // reading as accumulator an AGPR that a VALU op wrote needs 2 wait states
   // (after zeroing), and a read of an MFMA result needs up to 11 for these
@@ -288,10 +303,7 @@ void ffn_tiled16_kernel(const FfnArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   };
   auto zero_acc = [&]() {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{};
+    accr::zero_all();
     mfma_nops();
   };
   auto read_frags = [&](int bw, int bx, int h, u32x4* af, u32x4* bf) {
@@ -313,19 +325,18 @@ void ffn_tiled16_kernel(const FfnArgs a) {
     wait_lgkm0();
     const uint8_t* sw = lds + bw * kBufBytes;
     const uint8_t* sx = lds + bx * kBufBytes;
-#pragma unroll
-    for (int m = 0; m < 64; ++m) {
-      const int i = m >> 3, j = m & 7;
-      mfma16_agpr<T>(acc[i][j], af[i], bf[j]);
-      if (m % 3 == 1 && m / 3 < 16) {
-        const int r = m / 3;  // reads A0 B0 A1 B1 ..
-        if (r & 1)
+    static_for<0, 64>([&](auto mc) {
+      constexpr int m = decltype(mc)::value, i = m >> 3, j = m & 7;
+      mfma16_acc<T, 8 * i + j>(af[i], bf[j]);
+      if constexpr (m % 3 == 1 && m / 3 < 16) {
+        constexpr int r = m / 3;  // reads A0 B0 A1 B1 ..
+        if constexpr (r & 1)
           nb[r >> 1] = *reinterpret_cast<const u32x4*>(sx + brow[r >> 1] + coff[h]);
         else
           na[r >> 1] = *reinterpret_cast<const u32x4*>(sw + arow[r >> 1] + coff[h]);
       }
-      if (m % 3 == 2 && m / 3 < NL) issue(m / 3);
-    }
+      if constexpr (m % 3 == 2 && m / 3 < NL) issue(m / 3);
+    });
   };
   using L8 = std::integral_constant<int, 8>;
 
@@ -384,33 +395,33 @@ void ffn_tiled16_kernel(const FfnArgs a) {
       // block by block (each store 1 KB contiguous).
       f32x4* pp = reinterpret_cast<f32x4*>(a.part) +
                   static_cast<size_t>(cw.unit * 4 + wave) * kPartVecsPerWave + eln;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pp[(i * 8 + j) * kWave] = acc[i][j];
+      static_for<0, 8>([&](auto i) {
+        static_for<0, 8>([&](auto j) {
+          pp[(i * 8 + j) * kWave] = f32x4{acc_at(i, j, I0{}), acc_at(i, j, I1{}), acc_at(i, j, I2{}),
+                                          acc_at(i, j, I3{})};
+        });
+      });
       zero_acc();
     } else if (kGateUp) {
       T* inter = static_cast<T*>(a.out);
       auto epilogue = [&](auto silu) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        static_for<0, 8>([&](auto j) {
           const int prow = ct.row0 + wave_t * 128 + j * 16 + elr;
           if (prow < ct.row_end) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            static_for<0, 4>([&](auto i) {
+              using IU = std::integral_constant<int, decltype(i)::value + 4>;
               const int col = ct.wtile * (kTileW / 2) + wave_w * 64 + i * 16 + 4 * ekq;
               float v[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                v[r] = gate_act_16<decltype(silu)::value>(a.act, acc_read(acc[i][j][r])) *
-                       acc_read(acc[i + 4][j][r]);
+              static_for<0, 4>([&](auto r) {
+                v[decltype(r)::value] =
+                    gate_act_16<decltype(silu)::value>(a.act, acc_at(i, j, r)) * acc_at(IU{}, j, r);
+              });
               store4<T>(inter + static_cast<size_t>(prow) * a.I + col, v[0], v[1], v[2], v[3]);
-            }
+            });
           }
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i][j] = f32x4{};
+          static_for<0, 8>([&](auto i) { accr::zero_block<8 * decltype(i)::value + decltype(j)::value>(); });
           __builtin_amdgcn_sched_barrier(0);
-        }
+        });
       };
       if (a.act == MOE355_ACT_SILU)
         epilogue(std::true_type{});
@@ -431,37 +442,35 @@ void ffn_tiled16_kernel(const FfnArgs a) {
       };
       auto store_y = [&](auto* y) {
         using O = typename std::remove_pointer<decltype(y)>::type;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        static_for<0, 8>([&](auto j) {
           const int prow = ct.row0 + wave_t * 128 + j * 16 + pr;
           O* yr = y + static_cast<size_t>(prow) * a.H + (ct.wtile * kTileW + wave_w * 128 + 4 * pq);
           if constexpr (sizeof(O) == 4) {
             u32x4 q[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) q[i][r] = perm(__builtin_bit_cast(uint32_t, acc_read(acc[i][j][r])));
+            static_for<0, 8>([&](auto i) {
+              static_for<0, 4>([&](auto r) {
+                q[i][decltype(r)::value] = perm(__builtin_bit_cast(uint32_t, acc_at(i, j, r)));
+              });
+            });
             if (prow < ct.row_end) {
 #pragma unroll
               for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(yr + i * 16) = q[i];
             }
           } else {
             u32x2 q[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const u32x2 pk = pack4<O>(acc_read(acc[i][j][0]), acc_read(acc[i][j][1]),
-                                        acc_read(acc[i][j][2]), acc_read(acc[i][j][3]));
+            static_for<0, 8>([&](auto i) {
+              const u32x2 pk = pack4<O>(acc_at(i, j, I0{}), acc_at(i, j, I1{}), acc_at(i, j, I2{}),
+                                        acc_at(i, j, I3{}));
               q[i] = u32x2{perm(pk[0]), perm(pk[1])};
-            }
+            });
             if (prow < ct.row_end) {
 #pragma unroll
               for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x2*>(yr + i * 16) = q[i];
             }
           }
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i][j] = f32x4{};
+          static_for<0, 8>([&](auto i) { accr::zero_block<8 * decltype(i)::value + decltype(j)::value>(); });
           __builtin_amdgcn_sched_barrier(0);
-        }
+        });
       };
       if (a.y16)
         store_y(static_cast<T*>(a.out));
