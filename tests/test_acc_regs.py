@@ -26,11 +26,26 @@ def test_acc_regs_header_matches_generator():
         assert f.read() == out
 
 
+def _tiled_flags():
+    """The extra flags the Makefile gives ffn_tiled.hip."""
+    with open(os.path.join(CSRC, "Makefile")) as f:
+        m = re.search(r"^TILED_FLAGS := (.*)$", f.read(), re.M)
+    assert m, "Makefile lost TILED_FLAGS"
+    return m.group(1).split()
+
+
+def test_makefile_forbids_vgpr_spills_to_agprs():
+    flags = _tiled_flags()
+    assert "-amdgpu-spill-vgpr-to-agpr=0" in flags
+    with open(os.path.join(CSRC, "Makefile")) as f:
+        assert "$(OBJDIR)/ffn_tiled.o: HIPFLAGS += $(TILED_FLAGS)" in f.read()
+
+
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
 def test_tiled16_accumulators_stay_in_their_agprs(tmp_path):
     asm = tmp_path / "ffn_tiled.s"
     subprocess.run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
-                    "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",
+                    "-Xclang", "-packed-fp32-ops", *_tiled_flags(), "--cuda-device-only", "-S",
                     os.path.join(CSRC, "ffn_tiled.hip"), "-o", str(asm)],
                    check=True, capture_output=True, cwd=CSRC)
     lines = asm.read_text().splitlines()
