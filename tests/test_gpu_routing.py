@@ -69,7 +69,11 @@ def _router(x, gate, bias, K, renorm, round_logits, kmin=0):
                                      (33, 1024, 16, 2), (5, 8192, 256, 8),
                                      # 4 and 8 tokens per workgroup, 8 or 16 experts per pass
                                      (300, 4096, 8, 2), (300, 2048, 64, 6), (1100, 1024, 8, 2),
-                                     (1100, 512, 64, 6)])
+                                     (1100, 512, 64, 6),
+                                     # MFMA router: one 64-k batch per wave, a partial last
+                                     # workgroup and 20 experts in two 16-row groups; an odd
+                                     # batch count; 5 batches through a 4-buffer ring
+                                     (1037, 1024 // 4, 20, 3), (1100, 768, 8, 2), (257, 1280, 40, 4)])
 def test_router_topk(dtype, T, H, E, K, dev):
     banner(f"router dtype={dtype} T={T} H={H} E={E} K={K}")
     dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
