@@ -940,42 +940,41 @@ __global__ __launch_bounds__(kThreads) void down_tail_fixup(const FfnArgs a) {
 }
 
 // The fix-ups for ffn_tiled16_kernel's partial tiles (8x8 blocks of 16x16 per
-// wave, block (i, j) at vectors (i * 8 + j) * 64 + lane). A task covers four
-// token blocks 4 jq .. 4 jq + 3 (four independent loads per part in flight per
-// lane): gate_up task (item, i < 4, jq) sums gate block i and up block i + 4;
-// down task (item, i, jq).
+// wave, block (i, j) at vectors (i * 8 + j) * 64 + lane). gate_up task (item,
+// i < 4, j) sums gate block i and up block i + 4 of token block j over the
+// parts (its tail is cut into up to 16 parts of few items: the parts' loads go
+// out together); down task (item, i, jq) covers four token blocks 4 jq ..
+// 4 jq + 3 (four independent loads per part in flight per lane; its tail has
+// more items and fewer parts).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void gate_up_tail_fixup16(const FfnArgs a) {
   const int n_t = a.tile_map[0];
   const int per_split = a.n_wtiles * n_t;
   const int nk = a.k_per_split / kSK;
   const WorkSplit ws = work_split(a.splits * per_split, a.grid, nk, a.part_units);
-  const int tasks = ws.n_units / ws.S * 8;
+  const int tasks = ws.n_units / ws.S * 32;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int wave_w = wave >> 1, wave_t = wave & 1, lr = lane & 15, kq = lane >> 4;
   T* inter = static_cast<T*>(a.out);
   for (int task = blockIdx.x; task < tasks; task += gridDim.x) {
-    const int it = task >> 3, i = (task >> 1) & 3, jq = task & 1;
+    const int it = task >> 5, i = (task >> 3) & 3, j = task & 7;
     const Tile t = decode_tile(a, ws.n_full + it, per_split, n_t, a.tile_rows);
-    f32x4 g[4] = {}, u[4] = {};
+    const f32x4* pp = reinterpret_cast<const f32x4*>(a.part) +
+                      static_cast<size_t>(it * ws.S * 4 + wave) * kPartVecsPerWave + lane;
+    f32x4 g = {}, u = {};
+    // The parts of one block are independent loads: unrolled, up to 16 of
+    // them are in flight per lane (the gate_up tail often splits 8 ways).
+#pragma unroll 8
     for (int p = 0; p < ws.S; ++p) {
-      const f32x4* pp = reinterpret_cast<const f32x4*>(a.part) +
-                        static_cast<size_t>((it * ws.S + p) * 4 + wave) * kPartVecsPerWave + lane;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        g[q] += pp[(i * 8 + 4 * jq + q) * kWave];
-        u[q] += pp[((i + 4) * 8 + 4 * jq + q) * kWave];
-      }
+      g += pp[static_cast<size_t>(p) * 4 * kPartVecsPerWave + (i * 8 + j) * kWave];
+      u += pp[static_cast<size_t>(p) * 4 * kPartVecsPerWave + ((i + 4) * 8 + j) * kWave];
     }
     const int col = t.wtile * (kTileW / 2) + wave_w * 64 + i * 16 + 4 * kq;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int prow = t.row0 + wave_t * 128 + (4 * jq + q) * 16 + lr;
-      if (prow < t.row_end)
-        store4<T>(inter + static_cast<size_t>(prow) * a.I + col, gate_act_fast(a.act, g[q][0]) * u[q][0],
-                  gate_act_fast(a.act, g[q][1]) * u[q][1], gate_act_fast(a.act, g[q][2]) * u[q][2],
-                  gate_act_fast(a.act, g[q][3]) * u[q][3]);
-    }
+    const int prow = t.row0 + wave_t * 128 + j * 16 + lr;
+    if (prow < t.row_end)
+      store4<T>(inter + static_cast<size_t>(prow) * a.I + col, gate_act_fast(a.act, g[0]) * u[0],
+                gate_act_fast(a.act, g[1]) * u[1], gate_act_fast(a.act, g[2]) * u[2],
+                gate_act_fast(a.act, g[3]) * u[3]);
   }
 }
 

@@ -355,8 +355,8 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
         whole[split, r0:r1, wt] += 1
     assert (whole == 1).all(), "a (split, row, weight tile) is not covered exactly once"
     # fix-up tasks cover the split items' rows once: per item, gate blocks x
-    # groups of token blocks (gate_up) or weight blocks x groups (down)
-    per_item = 8 if gate_up else 16
+    # token blocks (gate_up) or weight blocks x groups of 4 token blocks (down)
+    per_item = 32 if gate_up else 16
     tasks = n_units // S * per_item
     assert tasks == len(parts) * per_item
     return n_seq
