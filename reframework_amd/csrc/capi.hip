@@ -326,6 +326,18 @@ int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renorm
 
 namespace {
 
+// Whether the full-tile kernels multiply only the token blocks each item's
+// rows reach and rotate their XCD slots (ffn_tiled16_kernel): with 16 or more
+// experts holding on average two 256-row tiles or fewer, the padding of the
+// experts' last tiles is a large share of the work (Phi-3.5 2048 tokens,
+// fine-grained 4096 tokens: gate_up -3.5 and -4 %). With 8 experts the uneven
+// items cost about what the padding saves (Mixtral 1024 and 2048 tokens: gate_up
+// +0.6 and +1.1 %), and more at more rows per expert (4096 tokens: +4 %).
+bool ragged_tiles(const moe355_plan* p) {
+  const long long act = std::min<long long>(p->E, p->rows);
+  return act >= 16 && p->rows / act <= 2 * 256;
+}
+
 // Checks the permute's arguments and fills its kernel arguments (the caller
 // has checked the plan and that it has rows).
 int permute_args(const moe355_plan* p, const void* topk_ids, int ids_int64,
@@ -401,6 +413,7 @@ int gate_up_impl(const moe355_plan* p, const void* x, const void* const* w1, int
   if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_TILED128) {
     a.n_wtiles = p->I / 128;
     a.tile_rows = p->tile_rows;
+    a.ragged = ragged_tiles(p);
     // The y and part regions are free until the down projection: they hold
     // the partial tiles of the K-split tail items (256x256 fp32 each).
     a.part = at<float>(workspace, p->off_y);
@@ -511,6 +524,7 @@ int moe355_down(const moe355_plan* p, const void* const* w2, void* workspace, vo
   if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_TILED128) {
     a.n_wtiles = p->H / 256;
     a.tile_rows = p->tile_rows;
+    a.ragged = ragged_tiles(p);
     a.y16 = y_narrow(p);
     // Partial tiles of the K-split last-round items (256x256 fp32 each).
     a.part = at<float>(workspace, p->off_part);

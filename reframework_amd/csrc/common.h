@@ -221,6 +221,7 @@ struct FfnArgs {
   int group_t;             // token tiles per item group (0: all; -1: one group per expert; see decode_tile)
   int tile_rows;           // token rows per tile of the tile map (tiled kernels: 256, or 128 for half tiles)
   int y16;                 // tiled down with one K-split: y rounded to the layer dtype
+  int ragged;              // full-tile kernel: per-item token-block count and rotated XCD slots
   const void* w[kMaxExperts];  // w1[e] ([2I,H]) or w2[e] ([H,I])
   // Skinny gate_up only, when self_permute: every workgroup groups the <= 64
   // routed slots of perm itself (no permute launch), and workgroup 0 writes

@@ -160,8 +160,9 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
   return __builtin_bit_cast(u32x2, v);
 }
 
-template <typename T, bool kGateUp>
+template <typename T, bool kGateUp, bool kRagged>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__attribute__((amdgpu_num_vgpr(128)))
 void ffn_tiled16_kernel(const FfnArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kBufs * kBufBytes];
 
@@ -178,13 +179,40 @@ void ffn_tiled16_kernel(const FfnArgs a) {
   const int n_seq = ws.n_full + ws.n_units;
   int Lc = xcd_remap(blockIdx.x, G);
   if (Lc >= n_seq) return;
+  // Item sequence of this workgroup: slot s (its place on the XCD) of its
+  // XCD's block of n_x consecutive items in every round (items k G .. k G +
+  // G - 1). kRagged launches (experts holding few token tiles each) multiply
+  // only the token blocks an item's rows reach, so an expert's last-tile items
+  // are cheaper; they also take, in the rounds wholly made of full items, slot
+  // (s + 13 k) mod n_x instead of s, so that which CUs draw those cheaper items
+  // changes from round to round instead of falling on the same CUs every
+  // round. Both pay where experts hold few tiles (Phi-3.5 2048 tokens gate_up
+  // -4 %, fine-grained 4096 tokens -4 %) and cost where they hold many
+  // (Mixtral 4096 tokens +4 %: CUs that drew cheap items run into the next
+  // round early and no longer share its weight slabs in L2).
+  // A cursor is (item L, round k, rotated slot r); next() gives the next
+  // one without a division (it runs at item boundaries of the K loop).
+  const int xslot = blockIdx.x >> 3;
+  const int n_x = (G >> 3) + ((blockIdx.x & 7) < (G & 7) ? 1 : 0);
+  const int xbase = Lc - xslot, rstep = kRagged ? 13 % n_x : 0;
+  struct Seq {
+    int L, k, r;
+  };
+  auto next = [&](const Seq& c) {
+    if (!kRagged) return Seq{c.L + G, c.k + 1, c.r};
+    Seq n{0, c.k + 1, c.r + rstep};
+    if (n.r >= n_x) n.r -= n_x;
+    n.L = n.k * G + xbase + ((n.k + 1) * G <= ws.n_full ? n.r : xslot);
+    return n;
+  };
 
   const int ld = kGateUp ? a.H : a.I;
   const uint32_t pitch = static_cast<uint32_t>(ld * 2);
   auto decode = [&](int L) { return decode_work(a, ws, L, per_split, n_t, nk, kTileT); };
   auto op_row = [&](int q, int ln) { return (wave * kLoadsPerOp + q) * 8 + (ln >> 3); };
 
-  int wL = Lc, wkt = 0, wke = 0;
+  Seq wq{Lc, 0, xslot};
+  int wkt = 0, wke = 0;
   __amdgpu_buffer_rsrc_t wsrc;
   uint32_t woff[kLoadsPerOp];
   auto setup_w = [&](const Work& w) {
@@ -204,7 +232,8 @@ void ffn_tiled16_kernel(const FfnArgs a) {
     }
   };
 
-  int xL = Lc, xkt = 0, xke = 0;
+  Seq xq{Lc, 0, xslot};
+  int xkt = 0, xke = 0;
   __amdgpu_buffer_rsrc_t xsrc;
   uint32_t xoff[kLoadsPerOp];
   int grow[kLoadsPerOp];
@@ -240,22 +269,27 @@ void ffn_tiled16_kernel(const FfnArgs a) {
     }
   };
   auto prefetch_next_rows = [&]() {
-    if (kGateUp) fetch_rows(decode(xL + G < n_seq ? xL + G : xL).t);
+    if (kGateUp) {
+      const int n = next(xq).L;
+      fetch_rows(decode(n < n_seq ? n : xq.L).t);
+    }
   };
   auto advance_w = [&]() {
     if (++wkt < wke) return;
-    if (wL + G < n_seq) {
-      wL += G;
-      setup_w(decode(wL));
+    const Seq n = next(wq);
+    if (n.L < n_seq) {
+      wq = n;
+      setup_w(decode(wq.L));
     } else {
       wkt = wke - 1;
     }
   };
   auto advance_x = [&]() {
     if (++xkt < xke) return;
-    if (xL + G < n_seq) {
-      xL += G;
-      setup_x(decode(xL));
+    const Seq n = next(xq);
+    if (n.L < n_seq) {
+      xq = n;
+      setup_x(decode(xq.L));
       prefetch_next_rows();
     } else {
       xkt = xke - 1;
@@ -269,20 +303,29 @@ void ffn_tiled16_kernel(const FfnArgs a) {
   };
 
   // MFMA operand rows of this wave: weight blocks bi (gate_up: 0-3 gate rows
-  // 64 wave_w + 16 bi, 4-7 the matching up rows), token blocks 128 wave_t + 16 bj.
+  // 64 wave_w + 16 bi, 4-7 the matching up rows 128 + ..; down 128 wave_w +
+  // 16 bi), token blocks 16 (2 bj + wave_t): the two token waves interleave
+  // 16-row blocks, so the first 32 J rows of a tile are token blocks 0 .. J-1
+  // of both. A lane reads row (l & 15) of a block at logical chunk 4 h +
+  // (l >> 4); a block's place in the buffer is an immediate offset of the
+  // read, so one base address per operand and k-half serves all 8 blocks.
   const int lr = lane & 15, kq = lane >> 4;
-  uint32_t arow[8], brow[8];
+  const uint32_t lds0 =
+      static_cast<uint32_t>(reinterpret_cast<size_t>((const __attribute__((address_space(3))) uint8_t*)lds));
+  uint32_t abase[2], bbase[2];
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    const int rb = kGateUp ? (b < 4 ? wave_w * 64 + b * 16 : kTileW / 2 + wave_w * 64 + (b - 4) * 16)
-                           : wave_w * 128 + b * 16;
-    arow[b] = (rb + lr) * kSRowBytes;
-    brow[b] = (wave_t * 128 + b * 16 + lr) * kSRowBytes;
+  for (int h = 0; h < 2; ++h) {
+    // Block rows start at multiples of 16, so the swizzle bits are lr's.
+    const uint32_t coff = swz8(4 * h + kq, lr) << 4;
+    abase[h] = lds0 + ((kGateUp ? wave_w * 64 : wave_w * 128) + lr) * kSRowBytes + coff;
+    bbase[h] = lds0 + (wave_t * 16 + lr) * kSRowBytes + coff;
   }
-  // Block rows start at multiples of 16, so the swizzle bits are lr's.
-  uint32_t coff[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) coff[h] = swz8(4 * h + kq, lr) << 4;
+  // Byte offsets of weight block i and token block j from those bases.
+  auto a_off = [](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    return std::integral_constant<int, (16 * i + (kGateUp && i >= 4 ? 64 : 0)) * kSRowBytes>{};
+  };
+  auto b_off = [](auto jc) { return std::integral_constant<int, 32 * decltype(jc)::value * kSRowBytes>{}; };
 
   // Accumulator block (i, j) is AGPR block 8 i + j (a[4 (8 i + j) ..]); the
   // indices are integral constants.
@@ -306,39 +349,61 @@ void ffn_tiled16_kernel(const FfnArgs a) {
     accr::zero_all();
     mfma_nops();
   };
-  auto read_frags = [&](int bw, int bx, int h, u32x4* af, u32x4* bf) {
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      af[b] = *reinterpret_cast<const u32x4*>(lds + bw * kBufBytes + arow[b] + coff[h]);
-      bf[b] = *reinterpret_cast<const u32x4*>(lds + bx * kBufBytes + brow[b] + coff[h]);
-    }
+  // Operand fragments live in fixed VGPRs above the compiler's budget
+  // (acc_regs.h): set s holds weight block i at v[128 + 32 s + 4 i ..] and
+  // token block j at v[192 + 32 s + 4 j ..]. Reads and MFMAs are assembly,
+  // so the compiler keeps only addresses, and the K loop can exist in one copy
+  // per token-block count J without register pressure.
+  auto read_a = [&](auto sc, auto ic, uint32_t base) {
+    accr::Frag<128 + 32 * decltype(sc)::value + 4 * decltype(ic)::value>::template read<
+        decltype(a_off(ic))::value>(base);
   };
-
-  // One sub-step: wait for its operands, then 64 MFMAs with the next
-  // sub-step's 16 operand reads after MFMAs 1, 4, .., 46 and its NL loads after
-  // MFMAs 2, 5, ..; the last 16 MFMAs give the last reads time to land. The
-  // MFMAs are volatile assembly, so this program order is the issue order (the
-  // reads and loads cannot move across them).
-  auto sub = [&](const u32x4* af, const u32x4* bf, int bw, int bx, int h, u32x4* na, u32x4* nb,
-                 auto issue, auto nl) {
-    constexpr int NL = decltype(nl)::value;
-    wait_lgkm0();
-    const uint8_t* sw = lds + bw * kBufBytes;
-    const uint8_t* sx = lds + bx * kBufBytes;
-    static_for<0, 64>([&](auto mc) {
-      constexpr int m = decltype(mc)::value, i = m >> 3, j = m & 7;
-      mfma16_acc<T, 8 * i + j>(af[i], bf[j]);
-      if constexpr (m % 3 == 1 && m / 3 < 16) {
-        constexpr int r = m / 3;  // reads A0 B0 A1 B1 ..
-        if constexpr (r & 1)
-          nb[r >> 1] = *reinterpret_cast<const u32x4*>(sx + brow[r >> 1] + coff[h]);
-        else
-          na[r >> 1] = *reinterpret_cast<const u32x4*>(sw + arow[r >> 1] + coff[h]);
-      }
-      if constexpr (m % 3 == 2 && m / 3 < NL) issue(m / 3);
+  auto read_b = [&](auto sc, auto jc, uint32_t base) {
+    accr::Frag<192 + 32 * decltype(sc)::value + 4 * decltype(jc)::value>::template read<
+        decltype(b_off(jc))::value>(base);
+  };
+  auto read_frags = [&](int bw, int bx, int h, auto sc) {
+    const uint32_t av = abase[h] + bw * kBufBytes, bv = bbase[h] + bx * kBufBytes;
+    static_for<0, 8>([&](auto b) {
+      read_a(sc, b, av);
+      read_b(sc, b, bv);
     });
   };
-  using L8 = std::integral_constant<int, 8>;
+
+  // One sub-step on fragment set S: wait for its operands, then the 8 J
+  // MFMAs of weight blocks 0-7 x token blocks 0 .. J-1 (a tile of n rows
+  // needs J = ceil(n / 32)), with the next sub-step's 16 operand reads (into
+  // set 1 - S) and 8 loads spread over them: at J = 8 reads after MFMAs 1, 4,
+  // .., 46 and loads after MFMAs 2, 5, .., 23, the last 16 MFMAs giving the
+  // last reads time to land; at smaller J the same pattern compressed. All 8
+  // token blocks are read whatever J is, so the reads do not depend on the
+  // next item's J. The MFMAs are volatile assembly, so this program order is
+  // the issue order (the reads and loads cannot move across them).
+  auto sub = [&](auto sc, int bw, int bx, int h, auto issue, auto jc) {
+    constexpr int S = decltype(sc)::value, J = decltype(jc)::value, M = 8 * J;
+    using NS = std::integral_constant<int, 1 - S>;
+    wait_lgkm0();
+    const uint32_t av = abase[h] + bw * kBufBytes, bv = bbase[h] + bx * kBufBytes;
+    static_for<0, M>([&](auto mc) {
+      constexpr int m = decltype(mc)::value, i = m / J, j = m % J;
+      if constexpr (std::is_same<T, bf16>::value)
+        accr::mma_bf16<S, i, j>();
+      else
+        accr::mma_f16<S, i, j>();
+      static_for<0, 16>([&](auto rc) {  // reads A0 B0 A1 B1 ..
+        constexpr int r = decltype(rc)::value;
+        if constexpr ((3 * r + 1) * M / 64 == m) {
+          if constexpr (r & 1)
+            read_b(NS{}, std::integral_constant<int, (r >> 1)>{}, bv);
+          else
+            read_a(NS{}, std::integral_constant<int, (r >> 1)>{}, av);
+        }
+      });
+      static_for<0, kLoadsPerOp>([&](auto qc) {
+        if constexpr ((3 * decltype(qc)::value + 2) * M / 64 == m) issue(decltype(qc)::value);
+      });
+    });
+  };
 
   // Prologue: W_0, X_0, W_1 and X_1 (the loads sub-step 1 of step -1 would
   // issue), then wait for W_0 and X_0 and read (0, 0).
@@ -364,28 +429,48 @@ void ffn_tiled16_kernel(const FfnArgs a) {
   dma_barrier<2 * kLoadsPerOp>();  // W_0 and X_0 landed
 
   zero_acc();
-  u32x4 fa[2][8], fb[2][8];
-  read_frags(0, 1, 0, fa[0], fb[0]);
+  read_frags(0, 1, 0, std::integral_constant<int, 0>{});
 
   int bw = 0;  // buffer of W_s (X_s is in the next one)
+  Seq cq{Lc, 0, xslot};
   Work cw = decode(Lc);
   while (true) {
     const Tile& ct = cw.t;
-    for (int kt = cw.kb; kt < cw.ke; ++kt) {
-      const int bx = ring_add(bw, 1);
-      const int nbw = ring_add(bw, 2), nbx = ring_add(bw, 3);  // step s+1
-      const int bw2 = ring_add(bw, 4);                          // W_{s+2}
-      // W_{s+2} (its buffer held X_{s-1}, freed by B_{s-1}).
-      sub(fa[0], fb[0], bw, bx, 1, fa[1], fb[1], [&](int i) { issue_w(bw2, i); }, L8{});
-      advance_w();
-      // W_{s+1} and X_{s+1} landed (only W_{s+2} may be in flight) and every
-      // wave has read its last operands of step s.
-      wait_lgkm0();
-      dma_barrier<kLoadsPerOp>();
-      // X_{s+2} into the buffer of W_s.
-      sub(fa[1], fb[1], nbw, nbx, 0, fa[0], fb[0], [&](int i) { issue_x(bw, i); }, L8{});
-      advance_x();
-      bw = nbw;
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    auto kloop = [&](auto jc) {
+      for (int kt = cw.kb; kt < cw.ke; ++kt) {
+        const int bx = ring_add(bw, 1);
+        const int nbw = ring_add(bw, 2), nbx = ring_add(bw, 3);  // step s+1
+        const int bw2 = ring_add(bw, 4);                          // W_{s+2}
+        // W_{s+2} (its buffer held X_{s-1}, freed by B_{s-1}).
+        sub(S0{}, bw, bx, 1, [&](int i) { issue_w(bw2, i); }, jc);
+        advance_w();
+        // W_{s+1} and X_{s+1} landed (only W_{s+2} may be in flight) and every
+        // wave has read its last operands of step s.
+        wait_lgkm0();
+        dma_barrier<kLoadsPerOp>();
+        // X_{s+2} into the buffer of W_s.
+        sub(S1{}, nbw, nbx, 0, [&](int i) { issue_x(bw, i); }, jc);
+        advance_x();
+        bw = nbw;
+      }
+    };
+    // kRagged: the token blocks the item's rows need, rounded up to even
+    // (rows past the group's end are zero-filled in the LDS; blocks past them
+    // are not multiplied). Otherwise all 8.
+    if constexpr (kRagged) {
+      switch (min(8, (ct.row_end - ct.row0 + 31) >> 5)) {
+        case 1:
+        case 2: kloop(std::integral_constant<int, 2>{}); break;
+        case 3:
+        case 4: kloop(std::integral_constant<int, 4>{}); break;
+        case 5:
+        case 6: kloop(std::integral_constant<int, 6>{}); break;
+        default: kloop(std::integral_constant<int, 8>{}); break;
+      }
+    } else {
+      kloop(std::integral_constant<int, 8>{});
     }
 
     mfma_nops();
@@ -406,7 +491,7 @@ void ffn_tiled16_kernel(const FfnArgs a) {
       T* inter = static_cast<T*>(a.out);
       auto epilogue = [&](auto silu) {
         static_for<0, 8>([&](auto j) {
-          const int prow = ct.row0 + wave_t * 128 + j * 16 + elr;
+          const int prow = ct.row0 + (2 * j + wave_t) * 16 + elr;
           if (prow < ct.row_end) {
             static_for<0, 4>([&](auto i) {
               using IU = std::integral_constant<int, decltype(i)::value + 4>;
@@ -443,7 +528,7 @@ void ffn_tiled16_kernel(const FfnArgs a) {
       auto store_y = [&](auto* y) {
         using O = typename std::remove_pointer<decltype(y)>::type;
         static_for<0, 8>([&](auto j) {
-          const int prow = ct.row0 + wave_t * 128 + j * 16 + pr;
+          const int prow = ct.row0 + (2 * j + wave_t) * 16 + pr;
           O* yr = y + static_cast<size_t>(prow) * a.H + (ct.wtile * kTileW + wave_w * 128 + 4 * pq);
           if constexpr (sizeof(O) == 4) {
             u32x4 q[8];
@@ -478,9 +563,9 @@ void ffn_tiled16_kernel(const FfnArgs a) {
         store_y(static_cast<float*>(a.out) + static_cast<size_t>(ct.split) * a.R * a.H);
       mfma_nops();
     }
-    Lc += G;
-    if (Lc >= n_seq) break;
-    cw = decode(Lc);
+    cq = next(cq);
+    if (cq.L >= n_seq) break;
+    cw = decode(cq.L);
   }
   wait_vmcnt<0>();
 }
@@ -970,7 +1055,7 @@ __global__ __launch_bounds__(kThreads) void gate_up_tail_fixup16(const FfnArgs a
       u += pp[static_cast<size_t>(p) * 4 * kPartVecsPerWave + ((i + 4) * 8 + j) * kWave];
     }
     const int col = t.wtile * (kTileW / 2) + wave_w * 64 + i * 16 + 4 * kq;
-    const int prow = t.row0 + wave_t * 128 + j * 16 + lr;
+    const int prow = t.row0 + (2 * j + wave_t) * 16 + lr;
     if (prow < t.row_end)
       store4<T>(inter + static_cast<size_t>(prow) * a.I + col, gate_act_fast(a.act, g[0]) * u[0],
                 gate_act_fast(a.act, g[1]) * u[1], gate_act_fast(a.act, g[2]) * u[2],
@@ -1001,7 +1086,7 @@ __global__ __launch_bounds__(kThreads) void down_tail_fixup16(const FfnArgs a) {
     const int h = t.wtile * kTileW + wave_w * 128 + i * 16 + 4 * kq;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int prow = t.row0 + wave_t * 128 + (4 * jq + q) * 16 + lr;
+      const int prow = t.row0 + (2 * (4 * jq + q) + wave_t) * 16 + lr;
       if (prow < t.row_end)
         store4<Y>(y + static_cast<size_t>(prow) * a.H + h, v[q][0], v[q][1], v[q][2], v[q][3]);
     }
@@ -1026,10 +1111,12 @@ hipError_t launch_tiled(const FfnArgs& args, int dtype, hipStream_t s) {
   const bool half = a.tile_rows < kTileT;
   if (dtype == MOE355_BF16)
     half ? ffn_tiled_half_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
-         : ffn_tiled16_kernel<bf16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+         : a.ragged ? ffn_tiled16_kernel<bf16, kGateUp, true><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
+                          : ffn_tiled16_kernel<bf16, kGateUp, false><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   else
     half ? ffn_tiled_half_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
-         : ffn_tiled16_kernel<f16, kGateUp><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
+         : a.ragged ? ffn_tiled16_kernel<f16, kGateUp, true><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a)
+                          : ffn_tiled16_kernel<f16, kGateUp, false><<<dim3(a.grid), dim3(kThreads), 0, s>>>(a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.part_units == 0) return err;
   // The split depends on the device-side tile count; without a tail the

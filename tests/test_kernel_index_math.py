@@ -299,6 +299,24 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
     parts = {}
     n_seq = n_full + n_units
     lds_rows = np.arange(256)
+    # ragged launches (full tiles, >= 16 active experts, <= 512 routed rows
+    # per active expert): per-item token-block count and rotated XCD slots
+    act = min(E, plan.rows)
+    ragged = tile_rows == 256 and act >= 16 and plan.rows // act <= 512
+
+    def next_item(pid, L):
+        # the full-tile kernel's item sequence: in ragged launches rotated
+        # slots in whole rounds of full items, else (and in the other rounds)
+        # slot s; the 128-row kernel steps by G
+        if not ragged:
+            return L + G
+        slot = pid >> 3
+        n_x = (G >> 3) + (1 if (pid & 7) < (G & 7) else 0)
+        base = xcd_remap(pid, G) - slot
+        k = L // G + 1
+        rot = (slot + 13 * k) % n_x if (k + 1) * G <= n_full else slot
+        return k * G + base + rot
+
     for pid in range(G):
         L = xcd_remap(pid, G)
         while L < n_seq:
@@ -324,14 +342,21 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
                 assert np.array_equal(held, np.arange(128))
             else:
                 held = lds_rows
-            # tile rows the MFMAs read: token half h (64 or 128 rows), blocks j
-            # (two 32-row blocks of v_mfma_f32_32x32x16 on half tiles, eight
-            # 16-row blocks of v_mfma_f32_16x16x32 on full tiles)
+            # tile rows the MFMAs read: on half tiles token half h (64 rows),
+            # two 32-row blocks j of v_mfma_f32_32x32x16; on full tiles 16-row
+            # blocks of v_mfma_f32_16x16x32, interleaved between the token waves
             if half:
                 read = {h * 64 + j * 32 + lr for h in range(2) for j in range(2) for lr in range(32)}
+                used = read
             else:
-                read = {h * 128 + j * 16 + lr for h in range(2) for j in range(8) for lr in range(16)}
-            assert set(range(n)) <= read and max(read) < tile_rows
+                # token wave h's block j is tile rows 16 (2 j + h) ..; the
+                # LDS reads cover all 8 blocks, the MFMAs blocks j < J (ragged:
+                # J = ceil(n / 32) rounded up to even, else 8)
+                read = {(2 * j + h) * 16 + lr for h in range(2) for j in range(8) for lr in range(16)}
+                J = min(8, -(-n // 32)) if ragged else 8
+                J += J & 1
+                used = {(2 * j + h) * 16 + lr for h in range(2) for j in range(J) for lr in range(16)}
+            assert set(range(n)) <= used <= read and max(read) < tile_rows
             assert read <= set(held.tolist())
             # every LDS row is loaded from a valid row or zero-filled
             valid = r0 + held < r1
@@ -348,7 +373,7 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
             else:
                 wr = wt * 256 + np.arange(256)
                 assert wr.max() < H
-            L += G
+            L = next_item(pid, L)
     for it, ks in parts.items():
         assert sorted(ks) == list(range(S)), f"item {it}: K-parts {ks}"
         split, wt, e, r0, r1 = decode_tile(it)
