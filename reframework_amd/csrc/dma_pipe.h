@@ -114,6 +114,7 @@ struct Mfma16<f16> {
 // One work item of the persistent grouped-GEMM kernels.
 struct Tile {
   int split, wtile, e, row0, row_end;
+  int height;  // rows per token tile of this expert (row_end - row0 <= height)
 };
 
 // Work item L of (split, weight tile, token tile), token tiles of tile_rows
@@ -146,8 +147,20 @@ __device__ __forceinline__ Tile decode_tile(const FfnArgs& a, int L, int per_spl
     t.wtile = r2 / ne;
     const int tt = b + (r2 - t.wtile * ne);
     t.e = e;
-    t.row0 = tile_map[3 + 2 * tt];
-    t.row_end = min(t.row0 + tile_rows, ee);
+    if (tile_rows == 256) {
+      // Full tiles: the expert's ne tiles share its rows evenly, in heights
+      // rounded up to the 32-row token-block pair (the MFMAs then skip the
+      // padding rows past the height; 1085 rows: 5 tiles of 224 and 189 rows
+      // instead of 4 x 256 + 61).
+      const int h = (((ee - eb + ne - 1) / ne) + 31) & ~31;
+      t.height = h;
+      t.row0 = eb + (tt - b) * h;
+      t.row_end = min(t.row0 + h, ee);
+    } else {
+      t.height = tile_rows;
+      t.row0 = tile_map[3 + 2 * tt];
+      t.row_end = min(t.row0 + tile_rows, ee);
+    }
     return t;
   }
   // Items come in groups of gt token tiles x all weight tiles, the token tile
@@ -161,6 +174,7 @@ __device__ __forceinline__ Tile decode_tile(const FfnArgs& a, int L, int per_spl
   t.e = tile_map[2 + 2 * tt];
   t.row0 = tile_map[3 + 2 * tt];
   t.row_end = min(t.row0 + tile_rows, offsets[t.e + 1]);
+  t.height = tile_rows;
   return t;
 }
 

@@ -14,7 +14,7 @@ addresses, before any of it runs on a GPU:
     oracle's stable grouping. A planted mistake (the per-round zeroing of
     `wave_cnt` covering only wave 0's row, which once sent row_src out of
     bounds on the GPU) must be caught.
-  * the tiled grouped GEMM (ffn_tiled.hip): the persistent schedule (XCD
+  * the tiled grouped GEMM (ffn_tiled.h): the persistent schedule (XCD
     remap, work_split's K-split tail, decode_tile's per-expert item groups)
     must cover every (K-split, permuted row, weight tile) exactly once, by a
     whole item or by all S K-parts of a split item, whose partial tiles stay
@@ -291,9 +291,21 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
         r2 = rem - b * n_wt
         wt = r2 // ne
         tt = b + (r2 - wt * ne)
-        row0 = tiles[tt][1]
         assert tiles[tt][0] == e
+        if tile_rows == 256:
+            row0 = eb + (tt - b) * height(e)
+            return split, wt, e, row0, min(row0 + height(e), ee)
+        row0 = tiles[tt][1]
         return split, wt, e, row0, min(row0 + tile_rows, ee)
+
+    def height(e):
+        # full tiles share the expert's rows evenly, in heights rounded up to
+        # 32 rows (1085 rows: 5 tiles of 224 and 189 rows)
+        n = int(counts[e])
+        if tile_rows < 256 or n == 0:
+            return tile_rows
+        ne = -(-n // tile_rows)
+        return -(-(-(-n // ne)) // 32) * 32
 
     whole = np.zeros((S_d, R, n_wt), np.int64)
     parts = {}
@@ -351,10 +363,10 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
             else:
                 # token wave h's block j is tile rows 16 (2 j + h) ..; the
                 # LDS reads cover all 8 blocks, the MFMAs blocks j < J (ragged:
-                # J = ceil(n / 32) rounded up to even, else 8)
+                # J = ceil(n / 32), else the expert's tile height / 32)
                 read = {(2 * j + h) * 16 + lr for h in range(2) for j in range(8) for lr in range(16)}
-                J = min(8, -(-n // 32)) if ragged else 8
-                J += J & 1
+                J = min(8, -(-(n if ragged else height(e)) // 32))
+                assert n <= height(e) <= tile_rows
                 used = {(2 * j + h) * 16 + lr for h in range(2) for j in range(J) for lr in range(16)}
             assert set(range(n)) <= used <= read and max(read) < tile_rows
             assert read <= set(held.tolist())
