@@ -250,6 +250,35 @@ def test_tile_boundary_group_sizes(m, path, dev):
     _check(gpu_fused(x, w1, w2, w, ids, path=path), x, w1, w2, w, ids, path=path)
 
 
+def _tile_blocks(n):
+    """Token-block pairs J the 256-row kernel multiplies for every tile of an
+    expert of n rows: its rows shared evenly over ceil(n / 256) tiles, the
+    height rounded up to 32 rows (J = height / 32)."""
+    nt = -(-n // 256)
+    return -(-(-(-n // nt)) // 32)
+
+
+@pytest.mark.parametrize("counts,I", [
+    # 8 experts (all-blocks instance): J = 5, 5, 6, 8, 7, 1, 1, 8; a K-split tail
+    ([257, 300, 513, 700, 1025, 1, 32, 255], 2048),
+    # 16 experts of <= 512 rows on average (ragged instance, rotated slots)
+    ([29, 94, 140, 187, 257, 281, 369, 514, 1, 33, 64, 97, 128, 160, 224, 500], 1536),
+], ids=["e8", "e16"])
+def test_balanced_tile_heights(counts, I, dev):
+    E, H = len(counts), 512
+    assert sorted({min(8, _tile_blocks(n)) for n in counts if n}) == (
+        [1, 5, 6, 7, 8] if E == 8 else [1, 2, 3, 4, 5, 6, 7, 8])
+    T = sum(counts)
+    ids = np.repeat(np.arange(E), counts)[np.random.default_rng(E).permutation(T)][:, None]
+    plan = _capi.make_plan(T, H, I, E, 1, _capi.BF16, _capi.PATH_MFMA_TILED)
+    banner(f"balanced tiles E={E} T={T} I={I} tiles<={plan.max_tiles}")
+    w1, w2 = make_bank(E, H, I, torch.bfloat16, seed=E + 40)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(E + 41)).to(torch.bfloat16)
+    w = np.random.default_rng(E + 42).random((T, 1)).astype(np.float32)
+    out = gpu_fused(x, w1, w2, w, ids.astype(np.int64), path=_capi.PATH_MFMA_TILED)
+    _check(out, x, w1, w2, w, ids.astype(np.int64), path=_capi.PATH_MFMA_TILED)
+
+
 def test_dropped_slots_and_expert_map(dev):
     banner("expert_map drop/rename")
     T, K, Eg, H, I = 200, 2, 8, 256, 256

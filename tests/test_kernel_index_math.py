@@ -410,7 +410,15 @@ TILED_CASES = [
     ("phi35_t2048", 2048, 4096, 6400, 16, lambda: skewed_ids(2048, 2, 16, seed=3, skew=1.1)),
     ("finegrained_t4096", 4096, 2048, 1408, 66, lambda: _finegrained_ids(4096)),
     ("ragged_e64", 1000, 4096, 256, 64, lambda: skewed_ids(1000, 1, 64, seed=5, skew=1.5)),
+    # the counts of the GPU balanced-tile-height tests (every token-block count)
+    ("balanced_e8", 3083, 512, 2048, 8, lambda: _ids_of([257, 300, 513, 700, 1025, 1, 32, 255])),
+    ("balanced_e16", 3078, 512, 1536, 16,
+     lambda: _ids_of([29, 94, 140, 187, 257, 281, 369, 514, 1, 33, 64, 97, 128, 160, 224, 500])),
 ]
+
+
+def _ids_of(counts):
+    return np.repeat(np.arange(len(counts)), counts)[:, None]
 
 
 @pytest.mark.parametrize("gate_up", [True, False], ids=["gate_up", "down"])
