@@ -327,15 +327,15 @@ int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renorm
 namespace {
 
 // Whether the full-tile kernels multiply only the token blocks each item's
-// rows reach and rotate their XCD slots (ffn_tiled16_kernel): with 16 or more
-// experts holding on average two 256-row tiles or fewer, the padding of the
-// experts' last tiles is a large share of the work (Phi-3.5 2048 tokens,
-// fine-grained 4096 tokens: gate_up -3.5 and -4 %). With 8 experts the uneven
-// items cost about what the padding saves (Mixtral 1024 and 2048 tokens: gate_up
-// +0.6 and +1.1 %), and more at more rows per expert (4096 tokens: +4 %).
+// rows reach and rotate their XCD slots (the kRagged instance of
+// ffn_tiled16_kernel) instead of the blocks of each expert's tile height:
+// where experts hold on average two 256-row tiles or fewer (Mixtral 2048
+// tokens gate_up 831 -> 822 us, fine-grained 4096 tokens 319 -> 314 us,
+// Phi-3.5 2048 tokens 507 -> 504 us); at more rows per expert the uneven items
+// cost about what they save (Mixtral 4096 tokens 1464 -> 1470 us).
 bool ragged_tiles(const moe355_plan* p) {
   const long long act = std::min<long long>(p->E, p->rows);
-  return act >= 16 && p->rows / act <= 2 * 256;
+  return act > 0 && p->rows / act <= 2 * 256;
 }
 
 // Checks the permute's arguments and fills its kernel arguments (the caller

@@ -311,10 +311,10 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
     parts = {}
     n_seq = n_full + n_units
     lds_rows = np.arange(256)
-    # ragged launches (full tiles, >= 16 active experts, <= 512 routed rows
-    # per active expert): per-item token-block count and rotated XCD slots
+    # ragged launches (full tiles, <= 512 routed rows per active expert):
+    # per-item token-block count and rotated XCD slots
     act = min(E, plan.rows)
-    ragged = tile_rows == 256 and act >= 16 and plan.rows // act <= 512
+    ragged = tile_rows == 256 and act > 0 and plan.rows // act <= 512
 
     def next_item(pid, L):
         # the full-tile kernel's item sequence: in ragged launches rotated
@@ -412,6 +412,8 @@ TILED_CASES = [
     ("ragged_e64", 1000, 4096, 256, 64, lambda: skewed_ids(1000, 1, 64, seed=5, skew=1.5)),
     # the counts of the GPU balanced-tile-height tests (every token-block count)
     ("balanced_e8", 3083, 512, 2048, 8, lambda: _ids_of([257, 300, 513, 700, 1025, 1, 32, 255])),
+    ("balanced_e11", 6683, 512, 2048, 11,
+     lambda: _ids_of([257, 300, 513, 700, 1025, 1, 32, 255, 1200, 1200, 1200])),
     ("balanced_e16", 3078, 512, 1536, 16,
      lambda: _ids_of([29, 94, 140, 187, 257, 281, 369, 514, 1, 33, 64, 97, 128, 160, 224, 500])),
 ]
