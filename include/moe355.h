@@ -74,7 +74,9 @@ typedef struct moe355_plan {
   size_t off_offsets;      /* int32 [E+1]    expert_offsets: rows of expert e are [off[e], off[e+1]) */
   size_t off_slot_to_row;  /* int32 [T*K]    permuted row of slot (t,k), -1 when dropped */
   size_t off_row_src;      /* int32 [T*K]    source token of each permuted row */
-  size_t off_tile_map;     /* int32 [2 + 2*max_tiles]: count, 0, then (expert, first_row) pairs */
+  size_t off_tile_map;     /* int32 [2 + 2*max_tiles]: count, tile_rows, then (expert, first_row)
+                              pairs; an expert's tiles lie its tile height apart (tile_rows, or on
+                              256-row maps its rows over its tiles rounded up to 32) */
   size_t off_inter;        /* dtype [T*K, I] silu(gate)*up per permuted row */
   size_t off_y;            /* fp32  [down_splits, T*K, H] down-projection partials; for the
                               tiled paths with down_splits == 1, dtype [T*K, H] (rounded to

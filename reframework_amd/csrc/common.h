@@ -157,6 +157,18 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Rows per token tile of an expert of n rows in a tile map of tile_rows-row
+// tiles. 256-row tiles share the expert's rows evenly over its ceil(n / 256)
+// tiles, the height rounded up to the 32-row token-block pair the 256-row
+// GEMM multiplies (1085 rows: 5 tiles of 224 rows, the last 189); the other
+// tile maps are tile_rows apart. The tile count is ceil(n / tile_rows) either
+// way.
+__host__ __device__ __forceinline__ int tile_height(int n, int tile_rows) {
+  if (tile_rows != 256 || n <= 0) return tile_rows;
+  const int nt = (n + 255) / 256;
+  return (((n + nt - 1) / nt) + 31) & ~31;
+}
+
 // Map a flat workgroup id so that ids dispatched to the same XCD (the hardware
 // deals workgroups round-robin over the 8 XCDs) get consecutive logical ids.
 // Tiles that share a weight slab then run on one XCD and share its L2.

@@ -137,30 +137,20 @@ __device__ __forceinline__ Tile decode_tile(const FfnArgs& a, int L, int per_spl
     // One group per expert: its token tiles x all weight tiles, the token tile
     // varying fastest. The group of item rem starts at the first tile b of the
     // expert owning tile rem / n_wtiles (tiles of an expert are consecutive
-    // and tile_rows apart, so b follows from that tile's first row).
+    // and its tile height apart, so b follows from that tile's first row).
     const int t0 = rem / a.n_wtiles;
     const int e = tile_map[2 + 2 * t0];
     const int eb = offsets[e], ee = offsets[e + 1];
-    const int b = t0 - (tile_map[3 + 2 * t0] - eb) / tile_rows;
+    const int h = tile_height(ee - eb, tile_rows);
+    const int b = t0 - (tile_map[3 + 2 * t0] - eb) / h;
     const int ne = (ee - eb + tile_rows - 1) / tile_rows;
     const int r2 = rem - b * a.n_wtiles;
     t.wtile = r2 / ne;
     const int tt = b + (r2 - t.wtile * ne);
     t.e = e;
-    if (tile_rows == 256) {
-      // Full tiles: the expert's ne tiles share its rows evenly, in heights
-      // rounded up to the 32-row token-block pair (the MFMAs then skip the
-      // padding rows past the height; 1085 rows: 5 tiles of 224 and 189 rows
-      // instead of 4 x 256 + 61).
-      const int h = (((ee - eb + ne - 1) / ne) + 31) & ~31;
-      t.height = h;
-      t.row0 = eb + (tt - b) * h;
-      t.row_end = min(t.row0 + h, ee);
-    } else {
-      t.height = tile_rows;
-      t.row0 = tile_map[3 + 2 * tt];
-      t.row_end = min(t.row0 + tile_rows, ee);
-    }
+    t.height = h;
+    t.row0 = tile_map[3 + 2 * tt];
+    t.row_end = min(t.row0 + h, ee);
     return t;
   }
   // Items come in groups of gt token tiles x all weight tiles, the token tile
@@ -173,8 +163,8 @@ __device__ __forceinline__ Tile decode_tile(const FfnArgs& a, int L, int per_spl
   const int tt = g * gfull + (r2 - t.wtile * gt);
   t.e = tile_map[2 + 2 * tt];
   t.row0 = tile_map[3 + 2 * tt];
-  t.row_end = min(t.row0 + tile_rows, offsets[t.e + 1]);
-  t.height = tile_rows;
+  t.height = tile_height(offsets[t.e + 1] - offsets[t.e], tile_rows);
+  t.row_end = min(t.row0 + t.height, offsets[t.e + 1]);
   return t;
 }
 

@@ -160,7 +160,8 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
         if (tile_start[mid] <= j) lo = mid; else hi = mid - 1;
       }
       a.tile_map[2 + 2 * j] = lo;
-      a.tile_map[3 + 2 * j] = start[lo] + (j - tile_start[lo]) * a.tile_rows;
+      a.tile_map[3 + 2 * j] =
+          start[lo] + (j - tile_start[lo]) * tile_height(start[lo + 1] - start[lo], a.tile_rows);
     }
   }
 

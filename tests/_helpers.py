@@ -57,6 +57,16 @@ def gpu_fused(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch.Te
     return out
 
 
+def tile_height(n: int, tile_rows: int) -> int:
+    """Rows per token tile of an expert of n rows in the tile map (the
+    kernels' tile_height): 256-row maps share the rows evenly over ceil(n/256)
+    tiles, the height rounded up to 32 rows; other maps are tile_rows apart."""
+    if tile_rows != 256 or n <= 0:
+        return tile_rows
+    nt = -(-n // 256)
+    return -(-(-(-n // nt)) // 32) * 32
+
+
 def read_ws(plan: _capi.Plan, ws: torch.Tensor, off: int, n: int) -> np.ndarray:
     """int32 array of n entries at byte offset `off` of the workspace."""
     return ws[off:off + 4 * n].cpu().view(torch.int32).numpy().copy()

@@ -25,7 +25,7 @@ import pytest
 import torch
 
 from _helpers import (DT, ROUND, assert_matches_rounded, assert_y_rounding, banner, gpu_fused,
-                      make_bank, read_ws, skewed_ids, y_round_of)
+                      make_bank, read_ws, skewed_ids, tile_height, y_round_of)
 from oracle import oracle
 from reframework_amd import _capi
 from reframework_amd.moe import fused_experts
@@ -86,10 +86,11 @@ def test_permute_bit_exact(T, K, E, ids64, drop, dev):
     assert np.array_equal(read_ws(plan, ws, plan.off_slot_to_row, R), s2r)
     n = offsets[-1]
     assert np.array_equal(read_ws(plan, ws, plan.off_row_src, R)[:n], src[:n])
-    # tile map: ceil(m_e / tile_rows) tiles per expert, in expert order
+    # tile map: ceil(m_e / tile_rows) tiles per expert, in expert order, the
+    # expert's tile height apart
     tm = read_ws(plan, ws, plan.off_tile_map, 2 + 2 * plan.max_tiles)
     counts = np.diff(offsets)
-    want = [(e, offsets[e] + j * plan.tile_rows) for e in range(E)
+    want = [(e, offsets[e] + j * tile_height(counts[e], plan.tile_rows)) for e in range(E)
             for j in range(-(-counts[e] // plan.tile_rows))]
     assert tm[0] == len(want) <= plan.max_tiles and tm[1] == plan.tile_rows
     assert [tuple(p) for p in tm[2:2 + 2 * len(want)].reshape(-1, 2)] == want
@@ -143,7 +144,7 @@ def test_decode_grouping_inside_gate_up_bit_exact(T, K, E, ids64, drop, dev):
     n = offsets[-1]
     assert np.array_equal(read_ws(plan, ws, plan.off_row_src, R)[:n], src[:n])
     counts = np.diff(offsets)
-    want = [(e, offsets[e] + j * plan.tile_rows) for e in range(E)
+    want = [(e, offsets[e] + j * tile_height(counts[e], plan.tile_rows)) for e in range(E)
             for j in range(-(-counts[e] // plan.tile_rows))]
     tm = read_ws(plan, ws, plan.off_tile_map, 2 + 2 * plan.max_tiles)
     assert tm[0] == len(want) <= plan.max_tiles and tm[1] == plan.tile_rows
@@ -252,10 +253,8 @@ def test_tile_boundary_group_sizes(m, path, dev):
 
 def _tile_blocks(n):
     """Token-block pairs J the 256-row kernel multiplies for every tile of an
-    expert of n rows: its rows shared evenly over ceil(n / 256) tiles, the
-    height rounded up to 32 rows (J = height / 32)."""
-    nt = -(-n // 256)
-    return -(-(-(-n // nt)) // 32)
+    expert of n rows outside ragged launches: its tile height / 32."""
+    return tile_height(n, 256) // 32
 
 
 @pytest.mark.parametrize("counts,I", [

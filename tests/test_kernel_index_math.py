@@ -38,7 +38,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from _helpers import skewed_ids
+from _helpers import skewed_ids, tile_height
 from oracle import oracle
 from reframework_amd import _capi
 
@@ -126,7 +126,8 @@ def emulate_permute(ids, E, tile_rows, max_tiles, emap=None, zero_first_row_only
             tile_map = [nt, tile_rows]
             for j in range(nt):
                 lo = int(np.searchsorted(tile_start[:E], j, side="right") - 1)
-                tile_map += [lo, int(start[lo] + (j - tile_start[lo]) * tile_rows)]
+                h = tile_height(int(start[lo + 1] - start[lo]), tile_rows)
+                tile_map += [lo, int(start[lo] + (j - tile_start[lo]) * h)]
         wave_cnt = np.full((WAVES, 256), POISON, np.int64)  # LDS at kernel start
         r = 0
         while r < ROUNDS and b * CHUNK + r * THREADS < R:
@@ -264,7 +265,15 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
     tile_rows = plan.tile_rows
     offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
     R = int(offs[-1])
-    tiles = [(e, int(offs[e] + r)) for e in range(E) for r in range(0, int(counts[e]), tile_rows)]
+
+    def height(e):
+        # full tiles share the expert's rows evenly, in heights rounded up to
+        # 32 rows (1085 rows: 5 tiles of 224 and 189 rows)
+        return tile_height(int(counts[e]), tile_rows)
+
+    # the permute's tile map: an expert's tiles its tile height apart
+    tiles = [(e, int(offs[e] + j * height(e))) for e in range(E)
+             for j in range(-(-int(counts[e]) // tile_rows))]
     n_t = len(tiles)
     assert n_t <= plan.max_tiles
     S_d = 1 if gate_up else plan.down_splits
@@ -286,26 +295,15 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
         t0 = rem // n_wt
         e = tiles[t0][0]
         eb, ee = int(offs[e]), int(offs[e + 1])
-        b = t0 - (tiles[t0][1] - eb) // tile_rows
+        b = t0 - (tiles[t0][1] - eb) // height(e)
         ne = (ee - eb + tile_rows - 1) // tile_rows
         r2 = rem - b * n_wt
         wt = r2 // ne
         tt = b + (r2 - wt * ne)
         assert tiles[tt][0] == e
-        if tile_rows == 256:
-            row0 = eb + (tt - b) * height(e)
-            return split, wt, e, row0, min(row0 + height(e), ee)
         row0 = tiles[tt][1]
-        return split, wt, e, row0, min(row0 + tile_rows, ee)
-
-    def height(e):
-        # full tiles share the expert's rows evenly, in heights rounded up to
-        # 32 rows (1085 rows: 5 tiles of 224 and 189 rows)
-        n = int(counts[e])
-        if tile_rows < 256 or n == 0:
-            return tile_rows
-        ne = -(-n // tile_rows)
-        return -(-(-(-n // ne)) // 32) * 32
+        assert row0 == eb + (tt - b) * height(e)
+        return split, wt, e, row0, min(row0 + height(e), ee)
 
     whole = np.zeros((S_d, R, n_wt), np.int64)
     parts = {}
