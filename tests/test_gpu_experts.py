@@ -177,6 +177,8 @@ CASES = [
     ("prefill_ragged", 700, 2, 8, 512, 384, "bf16", _capi.PATH_MFMA_TILED),
     ("prefill_tiled", 1200, 2, 4, 512, 384, "bf16", _capi.PATH_MFMA_TILED),
     ("prefill_f16", 1000, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_TILED),
+    # over 512 rows per expert: the 256-row kernel's non-ragged f16 instance
+    ("prefill_f16_tall", 1400, 2, 4, 256, 256, "f16", _capi.PATH_MFMA_TILED),
     ("fp32_tiny", 96, 2, 8, 256, 352, "f32", _capi.PATH_SIMT),
     ("fp32_decode", 3, 2, 8, 128, 96, "f32", _capi.PATH_SIMT),
     ("bf16_unaligned", 40, 2, 4, 136, 200, "bf16", _capi.PATH_SIMT),
