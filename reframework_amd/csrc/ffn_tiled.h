@@ -8,7 +8,8 @@
 //
 // Tile: 256 weight rows x 256 token rows, 4 waves in a 2x2 arrangement, each
 // wave owning 8x8 blocks of v_mfma_f32_16x16x32 (a 128x128 sub-tile, 256 fp32
-// accumulators). Weight rows are the MFMA M side and tokens the N side, so each
+// accumulators). An expert's token tiles share its rows evenly (tile_height),
+// and the MFMAs multiply only the 32-row token-block pairs a tile needs. Weight rows are the MFMA M side and tokens the N side, so each
 // lane ends up holding 4 consecutive output features of one token and stores
 // them as one vector.
 //   gate_up: the 256 weight rows are 128 gate rows and the 128 matching up
