@@ -75,8 +75,10 @@ typedef struct moe355_plan {
   size_t off_slot_to_row;  /* int32 [T*K]    permuted row of slot (t,k), -1 when dropped */
   size_t off_row_src;      /* int32 [T*K]    source token of each permuted row */
   size_t off_tile_map;     /* int32 [2 + 2*max_tiles]: count, tile_rows, then (expert, first_row)
-                              pairs; an expert's tiles lie its tile height apart (tile_rows, or on
-                              256-row maps its rows over its tiles rounded up to 32) */
+                              pairs; an expert's tiles are consecutive and lie its tile height
+                              apart (tile_rows, or on 256-row maps its rows over its tiles rounded
+                              up to 32); experts in any order (the permute: largest, smallest,
+                              second largest, ..) */
   size_t off_inter;        /* dtype [T*K, I] silu(gate)*up per permuted row */
   size_t off_y;            /* fp32  [down_splits, T*K, H] down-projection partials; for the
                               tiled paths with down_splits == 1, dtype [T*K, H] (rounded to

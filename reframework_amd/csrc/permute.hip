@@ -148,20 +148,63 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
 
   if (b == 0) {
     for (int e = tid; e <= a.E; e += kThreads) a.offsets[e] = start[e];
+    // The tile map lists the experts' tiles in an interleaved order of their
+    // sizes (largest, smallest, second largest, second smallest, ..; ties by
+    // expert id), so the GEMMs' rounds mix weight-stream-bound items of small
+    // experts with MFMA-bound items of large ones: fine-grained 4096 tokens
+    // gate_up -2 %, Phi-3.5 2048 tokens -2 %, Mixtral 4096 tokens down -2 %
+    // against expert-id order. Rank r of the size order goes to place 2 r in
+    // the first half, 2 (E - 1 - r) + 1 in the second.
+    __shared__ int order[kMaxExperts];         // expert at place p
+    __shared__ int place_start[kMaxExperts + 1];  // first tile of place p
+    for (int e = tid; e < a.E; e += kThreads) {
+      const int n = total[e];
+      int r = 0;
+      for (int f = 0; f < a.E; ++f) r += (total[f] > n || (total[f] == n && f < e)) ? 1 : 0;
+      order[2 * r < a.E ? 2 * r : 2 * (a.E - 1 - r) + 1] = e;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      constexpr int kPer = kMaxExperts / kWave;
+      const int per = (a.E + kWave - 1) / kWave;
+      int tl[kPer], st = 0;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int q = lane * per + i;
+        tl[i] = i < per && q < a.E ? (total[order[q]] + a.tile_rows - 1) / a.tile_rows : 0;
+        st += tl[i];
+      }
+      int it = st;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(it, o, kWave);
+        if (lane >= o) it += v;
+      }
+      int et = it - st;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int q = lane * per + i;
+        if (i < per && q < a.E) place_start[q] = et;
+        et += tl[i];
+      }
+      if (lane == kWave - 1) place_start[a.E] = it;
+    }
+    __syncthreads();
     const int ntiles = tile_start[a.E];
     if (tid == 0) {
       a.tile_map[0] = ntiles;
       a.tile_map[1] = a.tile_rows;
     }
     for (int j = tid; j < ntiles; j += kThreads) {
-      int lo = 0, hi = a.E - 1;  // last expert with tile_start[e] <= j
+      int lo = 0, hi = a.E - 1;  // last place with place_start[p] <= j
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (tile_start[mid] <= j) lo = mid; else hi = mid - 1;
+        if (place_start[mid] <= j) lo = mid; else hi = mid - 1;
       }
-      a.tile_map[2 + 2 * j] = lo;
+      const int e = order[lo];
+      a.tile_map[2 + 2 * j] = e;
       a.tile_map[3 + 2 * j] =
-          start[lo] + (j - tile_start[lo]) * tile_height(start[lo + 1] - start[lo], a.tile_rows);
+          start[e] + (j - place_start[lo]) * tile_height(start[e + 1] - start[e], a.tile_rows);
     }
   }
 

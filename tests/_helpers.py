@@ -67,6 +67,17 @@ def tile_height(n: int, tile_rows: int) -> int:
     return -(-(-(-n // nt)) // 32) * 32
 
 
+def tile_order(counts) -> List[int]:
+    """Experts in the order the permute lists their tiles: by row count,
+    largest, smallest, second largest, second smallest, ... (ties by id)."""
+    E = len(counts)
+    by = sorted(range(E), key=lambda e: (-int(counts[e]), e))
+    order = [0] * E
+    for r, e in enumerate(by):
+        order[2 * r if 2 * r < E else 2 * (E - 1 - r) + 1] = e
+    return order
+
+
 def read_ws(plan: _capi.Plan, ws: torch.Tensor, off: int, n: int) -> np.ndarray:
     """int32 array of n entries at byte offset `off` of the workspace."""
     return ws[off:off + 4 * n].cpu().view(torch.int32).numpy().copy()

@@ -38,7 +38,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from _helpers import skewed_ids, tile_height
+from _helpers import skewed_ids, tile_height, tile_order
 from oracle import oracle
 from reframework_amd import _capi
 
@@ -124,10 +124,20 @@ def emulate_permute(ids, E, tile_rows, max_tiles, emap=None, zero_first_row_only
             offsets = start.copy()
             nt = int(tile_start[E])
             tile_map = [nt, tile_rows]
+            # the kernel's place of each expert: its rank r by (rows desc, id)
+            # at 2 r in the first half, 2 (E - 1 - r) + 1 in the second
+            order = np.full(E, POISON, np.int64)
+            for e in range(E):
+                r = sum(1 for f in range(E) if total[f] > total[e] or (total[f] == total[e] and f < e))
+                p = 2 * r if 2 * r < E else 2 * (E - 1 - r) + 1
+                assert 0 <= p < E and order[p] == POISON
+                order[p] = e
+            place_start = np.concatenate([[0], np.cumsum(tiles[order])])
             for j in range(nt):
-                lo = int(np.searchsorted(tile_start[:E], j, side="right") - 1)
-                h = tile_height(int(start[lo + 1] - start[lo]), tile_rows)
-                tile_map += [lo, int(start[lo] + (j - tile_start[lo]) * h)]
+                lo = int(np.searchsorted(place_start[:E], j, side="right") - 1)
+                e = int(order[lo])
+                h = tile_height(int(start[e + 1] - start[e]), tile_rows)
+                tile_map += [e, int(start[e] + (j - place_start[lo]) * h)]
         wave_cnt = np.full((WAVES, 256), POISON, np.int64)  # LDS at kernel start
         r = 0
         while r < ROUNDS and b * CHUNK + r * THREADS < R:
@@ -212,6 +222,12 @@ def test_permute_emulation_in_bounds_and_equal_to_oracle(name, make, E, emap):
     assert np.array_equal(src[:n], o_src[:n])
     assert (src[n:] == POISON).all()  # rows past the routed ones are never written
     assert tile_map[0] <= plan.max_tiles
+    # every expert's tiles, its tile height apart, in the interleaved size order
+    counts = np.diff(o_off)
+    want = [(e, int(o_off[e]) + j * tile_height(int(counts[e]), plan.tile_rows))
+            for e in tile_order(counts) for j in range(-(-int(counts[e]) // plan.tile_rows))]
+    assert tile_map[0] == len(want)
+    assert [tuple(tile_map[2 + 2 * j:4 + 2 * j]) for j in range(len(want))] == want
 
 
 def test_permute_emulation_catches_partial_wave_table_zeroing():
@@ -271,8 +287,9 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
         # 32 rows (1085 rows: 5 tiles of 224 and 189 rows)
         return tile_height(int(counts[e]), tile_rows)
 
-    # the permute's tile map: an expert's tiles its tile height apart
-    tiles = [(e, int(offs[e] + j * height(e))) for e in range(E)
+    # the permute's tile map: an expert's tiles its tile height apart, the
+    # experts in the interleaved size order
+    tiles = [(e, int(offs[e] + j * height(e))) for e in tile_order(counts)
              for j in range(-(-int(counts[e]) // tile_rows))]
     n_t = len(tiles)
     assert n_t <= plan.max_tiles
