@@ -326,18 +326,16 @@ int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renorm
 
 namespace {
 
-// Whether a full-tile launch multiplies only the token blocks each item's
-// rows reach and rotates its XCD slots (the kRagged instance of
-// ffn_tiled16_kernel) instead of the blocks of each expert's tile height.
-// gate_up always (with the interleaved item order: Mixtral 4096 tokens
-// 1458 -> 1433 us, 2048 tokens 831 -> 822 us, fine-grained 8192 tokens -1 %
-// though the down launch after it then measured +3 %); down where experts hold
-// on average two 256-row tiles or fewer (fine-grained 4096 tokens, Phi-3.5
-// 2048 tokens), since at more rows per expert it loses (fine-grained 8192
-// tokens +3 %).
-bool ragged_tiles(const moe355_plan* p, bool gate_up) {
+// Whether the full-tile kernels multiply only the token blocks each item's
+// rows reach and rotate their XCD slots (the kRagged instance of
+// ffn_tiled16_kernel) instead of the blocks of each expert's tile height:
+// where experts hold on average two 256-row tiles or fewer (Mixtral 2048
+// tokens gate_up 831 -> 822 us, fine-grained 4096 tokens 319 -> 314 us,
+// Phi-3.5 2048 tokens 507 -> 504 us); at more rows per expert the uneven items
+// cost about what they save (Mixtral 4096 tokens 1464 -> 1470 us).
+bool ragged_tiles(const moe355_plan* p) {
   const long long act = std::min<long long>(p->E, p->rows);
-  return act > 0 && (gate_up || p->rows / act <= 2 * 256);
+  return act > 0 && p->rows / act <= 2 * 256;
 }
 
 // Checks the permute's arguments and fills its kernel arguments (the caller
@@ -415,7 +413,7 @@ int gate_up_impl(const moe355_plan* p, const void* x, const void* const* w1, int
   if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_TILED128) {
     a.n_wtiles = p->I / 128;
     a.tile_rows = p->tile_rows;
-    a.ragged = ragged_tiles(p, true);
+    a.ragged = ragged_tiles(p);
     // The y and part regions are free until the down projection: they hold
     // the partial tiles of the K-split tail items (256x256 fp32 each).
     a.part = at<float>(workspace, p->off_y);
@@ -526,7 +524,7 @@ int moe355_down(const moe355_plan* p, const void* const* w2, void* workspace, vo
   if (p->path == MOE355_PATH_MFMA_TILED || p->path == MOE355_PATH_MFMA_TILED128) {
     a.n_wtiles = p->H / 256;
     a.tile_rows = p->tile_rows;
-    a.ragged = ragged_tiles(p, false);
+    a.ragged = ragged_tiles(p);
     a.y16 = y_narrow(p);
     // Partial tiles of the K-split last-round items (256x256 fp32 each).
     a.part = at<float>(workspace, p->off_part);

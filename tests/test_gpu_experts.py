@@ -263,12 +263,11 @@ def _tile_blocks(n):
 
 
 @pytest.mark.parametrize("counts,I", [
-    # 8 experts, 385 rows on average (ragged instance, rotated slots, in
-    # both projections):
+    # 8 experts, 385 rows on average (ragged instance, rotated slots):
     # heights of J = 5, 5, 6, 8, 7, 1, 1, 8; a K-split tail
     ([257, 300, 513, 700, 1025, 1, 32, 255], 2048),
-    # the same with 3 x 1200 rows more (over 512 on average: down runs the
-    # instance that multiplies the blocks of each expert's height)
+    # the same with 3 x 1200 rows more (over 512 on average: the instance
+    # that multiplies the blocks of each expert's height)
     ([257, 300, 513, 700, 1025, 1, 32, 255, 1200, 1200, 1200], 2048),
     # 16 experts of 192 rows on average (ragged instance)
     ([29, 94, 140, 187, 257, 281, 369, 514, 1, 33, 64, 97, 128, 160, 224, 500], 1536),

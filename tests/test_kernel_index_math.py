@@ -326,10 +326,10 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
     parts = {}
     n_seq = n_full + n_units
     lds_rows = np.arange(256)
-    # ragged launches (full tiles; gate_up always, down at <= 512 routed rows
-    # per active expert): per-item token-block count and rotated XCD slots
+    # ragged launches (full tiles, <= 512 routed rows per active expert):
+    # per-item token-block count and rotated XCD slots
     act = min(E, plan.rows)
-    ragged = tile_rows == 256 and act > 0 and (gate_up or plan.rows // act <= 512)
+    ragged = tile_rows == 256 and act > 0 and plan.rows // act <= 512
 
     def next_item(pid, L):
         # the full-tile kernel's item sequence: in ragged launches rotated
