@@ -45,11 +45,14 @@ def parse():
     ap.add_argument("--offload-steps", type=int, default=256)
     ap.add_argument("--offload-tokens", type=int, default=8)
     ap.add_argument("--offload-host-pools", type=int, default=4,
-                    help="distinct layers' experts staged in pinned memory; deeper layers reuse them")
+                    help="distinct layers' experts staged in pinned memory (at most 4); deeper "
+                         "layers reuse them")
     ap.add_argument("--offload-modes", type=str,
-                    default="max_pack_2_per_layer_lru,max_pack_2_shared_pool,exact_per_layer_lru,"
-                            "exact_shared_pool",
-                    help="offload residency/forward modes; also max_pack_2_per_layer_lru_lookahead")
+                    default="max_pack_2_per_layer_lru,max_pack_2_shared_pool,"
+                            "max_pack_2_per_layer_lru_cpu_split,exact_chunk2_per_layer_lru,"
+                            "exact_chunk1_shared_pool",
+                    help="offload forward/residency modes; also "
+                         "max_pack_2_shared_pool_lookahead_t1")
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--profile", type=int, default=0,
@@ -431,37 +434,59 @@ def _progress(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, thrash_steps=16,
+# Staging more than this many pinned pools ended in a host-side segmentation
+# fault (exit 139) right after staging, with 32 pools (~129 GiB pinned once
+# torch's pinned allocator rounds each 2.8 GB pool up to 4 GiB); the cause is
+# not known, so deeper stacks share these pools.
+MAX_STAGED_HOST_POOLS = 4
+
+
+def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps=32,
                           modes=("max_pack_2_per_layer_lru", "max_pack_2_shared_pool",
-                                 "exact_per_layer_lru", "exact_shared_pool"), host_pools=4):
+                                 "max_pack_2_per_layer_lru_cpu_split",
+                                 "exact_chunk2_per_layer_lru", "exact_chunk1_shared_pool"),
+                          host_pools=4):
     """Decode through expert offload: a stack of Mixtral-shape layers (8
     experts each, 352 MB per expert in bf16) whose experts live in pinned host
-    memory, with HBM room for 2 experts per layer (64 of 256 experts for 32
-    layers). Synthetic routing (bypasses the router): per layer and token,
+    memory, with HBM room for 2 experts per layer (64 of 256 expert slots for
+    32 layers). Synthetic routing (bypasses the router): per layer and token,
     p=0.7 the previous step's pair again, else two experts from Zipf(1.2).
     Misses stream host->HBM on the caches' copy streams. ``host_pools``
     distinct layers' experts are staged in pinned memory (2.8 GB each); a layer
-    l >= host_pools uses layer l mod host_pools's pool (share_host), so a
-    32-layer stack pins 4 pools instead of 32 while every layer keeps its own
-    routing, HBM slots and LRU, and each miss still copies 352 MB over PCIe.
+    l >= host_pools uses layer l mod host_pools's pool (share_host): every
+    layer keeps its own routing, HBM slots and LRU, and each miss still copies
+    352 MB over PCIe, but only 8 * host_pools distinct experts exist on the
+    host.
 
-    Forwards: the reference's default truncation to RE_MAX_PACK=2 experts per
-    layer, and the exact streaming forward (every routed expert). Residency,
-    same HBM budget: (i) the reference's per-layer LRU of 2 (a layer may
-    overflow it while one request needs more), (ii) one LRU over (layer,
-    expert) shared by all layers (ExpertPool of 2 x layers slots). The exact
-    forward over the shared pool cycles ~5 experts per layer and step through
-    it (no reuse survives a step), so it runs ``thrash_steps`` steps; the
-    others run ``steps``. Mode "max_pack_2_per_layer_lru_lookahead" (not in
-    the default list) attaches the lookahead predictor, which loads the
-    predicted next-step experts while the current step computes; as in the
-    reference, a forward over more than one token counts as prefill and
-    resets it, so it engages at T = 1 only."""
+    Modes (forward, residency), all within 2 HBM slots per layer (the caches
+    evict before they copy, so the slots used are the peak resident set,
+    reported per mode):
+      * max_pack_2_*: the reference's default truncation to RE_MAX_PACK=2
+        experts per layer, with (i) a per-layer LRU of 2 or (ii) one LRU over
+        (layer, expert) of 2 x layers slots shared by all layers;
+      * max_pack_2_per_layer_lru_cpu_split: the same, with the CPU/GPU split
+        forward: experts not resident run on the host cores from the pinned
+        pool while the GPU runs the others; at most 2 copies in flight bring
+        host-computed experts into HBM for later steps;
+      * exact_chunk{2,1}_*: every routed expert, streamed in chunks of 2
+        (per-layer LRU of 2) or 1 (shared pool); these move several times
+        more bytes per step and run ``short_steps`` steps, named in the key.
+    Mode "max_pack_2_shared_pool_lookahead_t1" (not in the default list)
+    attaches the lookahead predictor at batch 1 (a forward over more tokens is
+    a prefill to it, as in the reference) over a pool with 2 spare slots per
+    layer."""
+    import numpy as np
     import torch
 
     from reframework_amd import _capi, synth
     from reframework_amd.moe import ExpertPool, FusedMoE
 
+    if host_pools > MAX_STAGED_HOST_POOLS:
+        raise SystemExit(
+            f"--offload-host-pools {host_pools}: at most {MAX_STAGED_HOST_POOLS} staged pinned "
+            "pools. 32 staged pools (about 129 GiB pinned after torch rounds each 2.8 GB pool up "
+            "to 4 GiB) ended in a host-side segmentation fault right after staging whose cause "
+            "is not known; deeper layers share the staged pools instead.")
     h, e, k, i = 4096, 8, 2, 14336
     t_setup = time.perf_counter()
     g = torch.Generator(device=dev).manual_seed(0)
@@ -495,45 +520,84 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, thrash_step
     b.synchronize()
     peak_h2d = n / (a.elapsed_time(b) / 1000.0) / 1e9
     del src, dst
+    expert_bytes = 3 * h * i * 2
+
+    # the host-compute lever: one expert on the host cores from the pinned pool
+    host = layers[0]._cache._host
+    xh = synth.make_tokens(T, h, torch.bfloat16, seed=9)
+    host_ms = {}
+    for m in (1, 4, T):
+        offs = np.array([0, m], np.int32)
+        toks = np.arange(m, dtype=np.int32)
+        wts = np.ones(m, np.float32)
+        out = torch.zeros(T, h)
+        times = []
+        for rep in range(7):
+            ex = rep % e
+            t0 = time.perf_counter()
+            _capi.host_experts(xh, [host[ex][0]], [host[ex][1]], offs, toks, wts, 0, out)
+            times.append(time.perf_counter() - t0)
+        host_ms[str(m)] = round(sorted(times[1:])[3] * 1000.0, 3)
+    host_expert = {"tokens_ms": host_ms, "threads": len(os.sched_getaffinity(0)),
+                   "gb_s_at_8_tokens": round(expert_bytes / (host_ms[str(T)] / 1000.0) / 1e9, 1),
+                   "copy_ms_at_peak_h2d": round(expert_bytes / peak_h2d / 1e6, 3)}
+    _progress(f"offload decode: host expert {host_ms} ms, copy "
+              f"{host_expert['copy_ms_at_peak_h2d']} ms")
 
     ids_all, w_all = synth.offload_trace(n_layers, warmup_steps + steps, T, e)
     ids_d = torch.from_numpy(ids_all).to(dev)
     w_d = torch.from_numpy(w_all).to(dev)
     x = (torch.randn(T, h, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    x1 = x[:1].contiguous()
 
-    def run_mode(tag, pool, exact, n_steps, lookahead=False):
+    def run_mode(tag, pool, chunk, n_steps, split=False, lookahead=False, tokens=T):
         t_mode = time.perf_counter()
+        xin = x if tokens == T else x1
 
         def fwd(moe, y, st, li):
-            if exact:  # every routed expert (the streaming forward with one chunk)
-                return moe._forward_streaming(y, w_d[st, li], ids_d[st, li], 0)
-            return moe._forward_offload(T, y, w_d[st, li], ids_d[st, li], 0)
+            wi, ii = w_d[st, li, :tokens], ids_d[st, li, :tokens]
+            if split:
+                return moe._forward_split(tokens, y, wi, ii, 0)
+            if chunk:  # every routed expert, chunk experts at a time
+                return moe._forward_streaming(y, wi, ii, 0)
+            return moe._forward_offload(tokens, y, wi, ii, 0)
 
+        if chunk:
+            os.environ["RE_CHUNK_SIZE"] = str(chunk)
         for moe in layers:
             moe._cache.use_pool(pool)
             moe._cache.log_copies(False)
             moe._predictor = None
             moe._cache._predictor = None
+            if split:
+                moe._cache.enable_host_experts()
             if lookahead:
                 moe.attach_predictor(window=8)
-        for st in range(warmup_steps):
-            y = x
-            for li, moe in enumerate(layers):
-                y = fwd(moe, y, st, li)
-        torch.cuda.synchronize()
-        for moe in layers:
-            moe._cache.stats.reset()
-            moe._cache.log_copies(True)
-        t0 = time.perf_counter()
-        for st in range(warmup_steps, warmup_steps + n_steps):
-            y = x
-            for li, moe in enumerate(layers):
-                y = fwd(moe, y, st, li)
-        torch.cuda.synchronize()
-        sec = time.perf_counter() - t0
-        hits = sum(m._cache.stats.hits for m in layers)
-        misses = sum(m._cache.stats.misses for m in layers)
-        predicts = sum(m._cache.stats.predicts for m in layers)
+        try:
+            for st in range(warmup_steps):
+                y = xin
+                for li, moe in enumerate(layers):
+                    y = fwd(moe, y, st, li)
+            torch.cuda.synchronize()
+            for moe in layers:
+                moe._cache.stats.reset()
+                moe._cache.log_copies(True)
+            t0 = time.perf_counter()
+            for st in range(warmup_steps, warmup_steps + n_steps):
+                y = xin
+                for li, moe in enumerate(layers):
+                    y = fwd(moe, y, st, li)
+            torch.cuda.synchronize()
+            sec = time.perf_counter() - t0
+        finally:
+            os.environ.pop("RE_CHUNK_SIZE", None)
+            for moe in layers:
+                moe._cache._cpu_split = False
+        stats = [m._cache.stats for m in layers]
+        hits = sum(s_.hits for s_ in stats)
+        misses = sum(s_.misses for s_ in stats)
+        on_host = sum(s_.host_experts for s_ in stats)
+        predicts = sum(s_.predicts for s_ in stats)
         nbytes, copy_ms = 0, 0.0
         for m in layers:
             b_, ms_ = m._cache.copy_summary()
@@ -541,22 +605,35 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, thrash_step
             copy_ms += ms_
         slots = pool.n_slots if pool is not None else sum(m._cache._n_slots for m in layers)
         _progress(f"offload decode: {tag} done ({time.perf_counter() - t_mode:.0f} s)")
-        return {"steps": n_steps, "tokens_per_s": round(T * n_steps / sec, 2),
-                "ms_per_step": round(sec * 1000.0 / n_steps, 3), "hbm_expert_slots": slots,
-                "hit_rate": round(hits / max(1, hits + misses), 4), "hits": hits, "misses": misses,
-                "lookahead_loads": predicts,
-                "h2d_gb_s": round(nbytes / (copy_ms / 1000.0) / 1e9, 2) if copy_ms > 0 else None,
-                "h2d_bytes": nbytes, "copy_time_frac": round(copy_ms / 1000.0 / sec, 4)}
+        r = {"steps": n_steps, "tokens": tokens, "tokens_per_s": round(tokens * n_steps / sec, 2),
+             "ms_per_step": round(sec * 1000.0 / n_steps, 3), "hbm_expert_slots": slots,
+             # split: share of the experts run that were resident (the rest ran on
+             # the host); otherwise hits / (hits + misses) per OffloadStats
+             "hit_rate": round(hits / max(1, hits + (on_host if split else misses)), 4),
+             "hits": hits,
+             "misses": misses, "lookahead_loads": predicts,
+             "h2d_gb_s": round(nbytes / (copy_ms / 1000.0) / 1e9, 2) if copy_ms > 0 else None,
+             "h2d_bytes": nbytes, "copy_time_frac": round(copy_ms / 1000.0 / sec, 4)}
+        if split:
+            r["host_experts"] = on_host
+            r["copies"] = misses
+        return r
 
-    res = {"workload": f"offload decode, {n_layers} mixtral-shape layers, {2 * n_layers} of "
-                       f"{e * n_layers} experts in HBM", "layers": n_layers, "tokens": T,
-           "host_pools": host_pools, "peak_pinned_h2d_gb_s": round(peak_h2d, 2)}
+    res = {"workload": f"offload decode, {n_layers} mixtral-shape layers, HBM slots for 2 experts "
+                       f"per layer ({2 * n_layers} of {e * n_layers}), host pools of "
+                       f"{e * host_pools} distinct experts",
+           "layers": n_layers, "tokens": T, "host_pools": host_pools,
+           "distinct_host_experts": e * host_pools,
+           "peak_pinned_h2d_gb_s": round(peak_h2d, 2), "host_expert": host_expert}
     for mode in modes:
-        exact = mode.startswith("exact")
-        shared = mode.endswith("shared_pool")
-        res[mode] = run_mode(mode, ExpertPool(capacity=2 * n_layers) if shared else None, exact,
-                             min(steps, thrash_steps) if exact and shared else steps,
-                             lookahead=mode.endswith("lookahead"))
+        shared = "shared_pool" in mode
+        chunk = int(mode.split("chunk")[1].split("_")[0]) if mode.startswith("exact_chunk") else 0
+        lookahead = mode.endswith("lookahead_t1")
+        pool = ExpertPool(capacity=(4 if lookahead else 2) * n_layers) if shared else None
+        n_steps = min(steps, short_steps) if chunk else steps
+        key = f"{mode}_{n_steps}_steps" if chunk else mode
+        res[key] = run_mode(mode, pool, chunk, n_steps, split=mode.endswith("cpu_split"),
+                            lookahead=lookahead, tokens=1 if lookahead else T)
     for moe in layers:
         moe._cache.use_pool(None)
     del layers

@@ -97,6 +97,18 @@ _SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
 _lib: Optional[ctypes.CDLL] = None
 _lock = threading.Lock()
 
+# libmoe355_host.so (include/moe355_host.h): the host half of the CPU/GPU
+# split forward, plain C++ on the host cores.
+HOST_LIB_NAME = "libmoe355_host.so"
+HOST_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), HOST_LIB_NAME)
+HOST_HEADER_PATH = os.path.join(os.path.dirname(HEADER_PATH), "moe355_host.h")
+_HOST_SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
+    "moe355_host_version": (_I, []),
+    "moe355_host_last_error": (ctypes.c_char_p, []),
+    "moe355_host_experts": (_I, [_P, _I, _I, _I, _I, _I, _PP, _PP, _P, _P, _P, _I, _I, _P]),
+}
+_host_lib: Optional[ctypes.CDLL] = None
+
 
 def lib() -> ctypes.CDLL:
     """Load libmoe355.so once; raise if it has not been built."""
@@ -116,6 +128,26 @@ def lib() -> ctypes.CDLL:
                     fn.argtypes = args
                 _lib = handle
     return _lib
+
+
+def host_lib() -> ctypes.CDLL:
+    """Load libmoe355_host.so once; raise if it has not been built."""
+    global _host_lib
+    if _host_lib is None:
+        with _lock:
+            if _host_lib is None:
+                if not os.path.exists(HOST_LIB_PATH):
+                    raise MoeLibError(
+                        f"{HOST_LIB_NAME} is not built at {HOST_LIB_PATH}; run "
+                        "`make -C reframework_amd/csrc` (or __graft_entry__.build())"
+                    )
+                handle = ctypes.CDLL(HOST_LIB_PATH)
+                for name, (res, args) in _HOST_SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _host_lib = handle
+    return _host_lib
 
 
 def header_symbols(path: str = HEADER_PATH) -> List[str]:
@@ -358,6 +390,33 @@ def cast_f32(src: torch.Tensor, dst: torch.Tensor, stream: Optional[int] = None)
 
 def h2d_async(dst_ptr: int, src_ptr: int, nbytes: int, stream: int) -> None:
     _check("moe355_h2d_async", lib().moe355_h2d_async(dst_ptr, src_ptr, nbytes, stream))
+
+
+def host_experts(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch.Tensor],
+                 slot_offsets, slot_tokens, slot_weights, act: int, out: torch.Tensor,
+                 n_threads: int = 0) -> None:
+    """moe355_host_experts: ``out`` (host fp32 [T,H]) += the experts given
+    (host tensors [2I,H] / [H,I] in x's dtype) over their slots. The slot
+    arrays are contiguous int32 / int32 / float32 numpy arrays."""
+    if x.device.type != "cpu" or out.device.type != "cpu" or out.dtype != torch.float32:
+        raise ValueError("host_experts takes host tensors and an fp32 host output")
+    T, H = x.shape
+    I = w2[0].shape[1] if len(w2) else 1
+    for a, b in zip(w1, w2):
+        if a.device.type != "cpu" or b.device.type != "cpu" or a.dtype != x.dtype or \
+                b.dtype != x.dtype or tuple(a.shape) != (2 * I, H) or tuple(b.shape) != (H, I) or \
+                not a.is_contiguous() or not b.is_contiguous():
+            raise ValueError("host expert weights must be contiguous host [2I,H] / [H,I] "
+                             "tensors of x's dtype")
+    t1, _k1 = _ptr_table([int(a.data_ptr()) for a in w1])
+    t2, _k2 = _ptr_table([int(b.data_ptr()) for b in w2])
+    rc = host_lib().moe355_host_experts(
+        _ptr(x), T, H, I, dtype_code(x.dtype), len(w1), t1, t2, slot_offsets.ctypes.data,
+        slot_tokens.ctypes.data, slot_weights.ctypes.data, int(act), int(n_threads), _ptr(out))
+    if rc != 0:
+        msg = host_lib().moe355_host_last_error()
+        raise MoeLibError(f"moe355_host_experts failed (status {rc}): "
+                          f"{msg.decode() if msg else ''}")
 
 
 # ------------------------------------------------------------------ workspace

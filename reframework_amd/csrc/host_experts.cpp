@@ -1,0 +1,365 @@
+// Host-side expert FFN for the CPU/GPU split forward (libmoe355_host.so).
+//
+// The reference computes the experts that are not resident in device memory
+// on the CPU while the GPU runs the resident ones, and sums both halves
+// (reframework/moe/moe_layer.py:523-627, fused.py:140-197, there with int8
+// GEMMs). Here the host half reads the staged 16-bit weights directly and
+// computes with the GPU kernels' numerics: fp32 products and sums for
+// gate|up, the activated intermediate rounded once to the weight type, fp32
+// down projection, and the routing weight applied in fp32 to each slot's y
+// before it is added to an fp32 output row.
+//
+// Decode-sized inputs (a few tokens per expert) make this a weight stream:
+// every weight row is read once from host memory and multiplied against all
+// of an expert's token rows, which stay in L1/L2. Rows are split over the
+// OpenMP threads in fixed blocks, so results do not depend on the thread
+// count. AVX-512F is used where the CPU has it (checked at run time), AVX2 +
+// FMA otherwise; both convert bf16/f16 to fp32 exactly before the FMAs.
+
+#include <immintrin.h>
+#include <omp.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/moe355_host.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+inline float bf16_to_f32(uint16_t b) {
+  uint32_t u = static_cast<uint32_t>(b) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// Round to nearest even, NaN kept quiet.
+inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+inline float round_to_type(float v, int dtype) {
+  if (dtype == MOE355_HOST_BF16) return bf16_to_f32(f32_to_bf16(v));
+  if (dtype == MOE355_HOST_F16) return _cvtsh_ss(_cvtss_sh(v, _MM_FROUND_TO_NEAREST_INT));
+  return v;
+}
+
+inline float load_w(const void* base, size_t i, int dtype) {
+  if (dtype == MOE355_HOST_BF16) return bf16_to_f32(static_cast<const uint16_t*>(base)[i]);
+  if (dtype == MOE355_HOST_F16) return _cvtsh_ss(static_cast<const uint16_t*>(base)[i]);
+  return static_cast<const float*>(base)[i];
+}
+
+inline float act_mul(int act, float g, float u) {
+  float a;
+  if (act == 0) {
+    a = g / (1.0f + std::exp(-g));
+  } else if (act == 1) {
+    a = 0.5f * g * (1.0f + std::erf(g * 0.70710678118654752f));
+  } else {
+    const float c = 0.79788456080286536f;  // sqrt(2/pi)
+    a = 0.5f * g * (1.0f + std::tanh(c * (g + 0.044715f * g * g * g)));
+  }
+  return a * u;
+}
+
+// ---------------------------------------------------------------- dot rows
+// out[t * ldo + r] = sum_k a[t * n + k] * W[r * n + k] for r in [r0, r1),
+// t in [0, m). a is fp32 (m rows of n), W rows are 16-bit or fp32.
+
+constexpr int kMaxTok = 8;  // token rows per pass over a weight row
+
+template <int DT>
+__attribute__((target("avx512f,avx512bw")))
+inline __m512 load16_avx512(const void* w, size_t i) {
+  if constexpr (DT == MOE355_HOST_BF16) {
+    __m256i h = _mm256_loadu_si256(reinterpret_cast<const __m256i*>(
+        static_cast<const uint16_t*>(w) + i));
+    return _mm512_castsi512_ps(_mm512_slli_epi32(_mm512_cvtepu16_epi32(h), 16));
+  } else if constexpr (DT == MOE355_HOST_F16) {
+    __m256i h = _mm256_loadu_si256(reinterpret_cast<const __m256i*>(
+        static_cast<const uint16_t*>(w) + i));
+    return _mm512_cvtph_ps(h);
+  } else {
+    return _mm512_loadu_ps(static_cast<const float*>(w) + i);
+  }
+}
+
+// Ask for the row's next K block (its cache lines) while this one is
+// multiplied: with the K blocking each weight row is read in short runs, which
+// the hardware prefetchers follow poorly.
+template <int DT>
+inline void prefetch_next_block(const void* w, size_t row, int k0, int n) {
+  constexpr int esz = DT == MOE355_HOST_F32 ? 4 : 2;
+  const char* p = static_cast<const char*>(w) + (row + k0) * esz;
+  const int bytes = ((n - k0) < 512 ? (n - k0) : 512) * esz;
+  for (int off = 0; off < bytes; off += 64) _mm_prefetch(p + off, _MM_HINT_T0);
+}
+
+// K is walked in blocks of kKBlock so that the MT token rows' block (MT x
+// kKBlock fp32, 16 KB at 8 tokens) stays in L1 while the 16 weight rows of a
+// row block stream past it; each (row, token) partial is reduced per block.
+constexpr int kKBlock = 512;
+
+template <int MT, int DT>
+__attribute__((target("avx512f,avx512bw")))
+void dot_block_avx512(const float* a, int lda, int n, const void* w, int r0, int r1,
+                      float* out, int ldo) {
+  float part[16][MT];
+  for (int r = 0; r < r1 - r0; ++r)
+    for (int t = 0; t < MT; ++t) part[r][t] = 0.0f;
+  for (int kb = 0; kb < n; kb += kKBlock) {
+    const int ke = (kb + kKBlock) < n ? (kb + kKBlock) : n;
+    const int kv = kb + ((ke - kb) & ~15);
+    for (int r = r0; r < r1; ++r) {
+      const size_t row = static_cast<size_t>(r) * n;
+      prefetch_next_block<DT>(w, row, ke, n);
+      __m512 acc[MT];
+      for (int t = 0; t < MT; ++t) acc[t] = _mm512_setzero_ps();
+      for (int k = kb; k < kv; k += 16) {
+        const __m512 wv = load16_avx512<DT>(w, row + k);
+        for (int t = 0; t < MT; ++t)
+          acc[t] = _mm512_fmadd_ps(wv, _mm512_loadu_ps(a + (size_t)t * lda + k), acc[t]);
+      }
+      for (int t = 0; t < MT; ++t) {
+        float s = _mm512_reduce_add_ps(acc[t]);
+        for (int k = kv; k < ke; ++k) s += load_w(w, row + k, DT) * a[(size_t)t * lda + k];
+        part[r - r0][t] += s;
+      }
+    }
+  }
+  for (int r = r0; r < r1; ++r)
+    for (int t = 0; t < MT; ++t) out[(size_t)t * ldo + r] = part[r - r0][t];
+}
+
+template <int MT>
+__attribute__((target("avx512f,avx512bw")))
+void dot_block_dt_avx512(const float* a, int lda, int n, const void* w, int dtype, int r0,
+                      int r1, float* out, int ldo) {
+  if (dtype == MOE355_HOST_BF16)
+    dot_block_avx512<MT, MOE355_HOST_BF16>(a, lda, n, w, r0, r1, out, ldo);
+  else if (dtype == MOE355_HOST_F16)
+    dot_block_avx512<MT, MOE355_HOST_F16>(a, lda, n, w, r0, r1, out, ldo);
+  else
+    dot_block_avx512<MT, MOE355_HOST_F32>(a, lda, n, w, r0, r1, out, ldo);
+}
+
+__attribute__((target("avx512f,avx512bw")))
+void dot_rows_avx512(const float* a, int lda, int m, int n, const void* w, int dtype, int r0, int r1,
+                     float* out, int ldo) {
+  for (int t0 = 0; t0 < m; t0 += kMaxTok) {
+    const float* at = a + (size_t)t0 * lda;
+    float* ot = out + (size_t)t0 * ldo;
+    switch ((m - t0) < kMaxTok ? (m - t0) : kMaxTok) {
+      case 1: dot_block_dt_avx512<1>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      case 2: dot_block_dt_avx512<2>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      case 3: dot_block_dt_avx512<3>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      case 4: dot_block_dt_avx512<4>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      case 5: dot_block_dt_avx512<5>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      case 6: dot_block_dt_avx512<6>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      case 7: dot_block_dt_avx512<7>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      default: dot_block_dt_avx512<8>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+    }
+  }
+}
+
+template <int DT>
+__attribute__((target("avx2,fma,f16c")))
+inline __m256 load8_avx2(const void* w, size_t i) {
+  if constexpr (DT == MOE355_HOST_BF16) {
+    __m128i h = _mm_loadu_si128(reinterpret_cast<const __m128i*>(
+        static_cast<const uint16_t*>(w) + i));
+    return _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(h), 16));
+  } else if constexpr (DT == MOE355_HOST_F16) {
+    __m128i h = _mm_loadu_si128(reinterpret_cast<const __m128i*>(
+        static_cast<const uint16_t*>(w) + i));
+    return _mm256_cvtph_ps(h);
+  } else {
+    return _mm256_loadu_ps(static_cast<const float*>(w) + i);
+  }
+}
+
+__attribute__((target("avx2,fma,f16c")))
+inline float hsum_avx2(__m256 v) {
+  __m128 s = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
+  s = _mm_add_ps(s, _mm_movehl_ps(s, s));
+  s = _mm_add_ss(s, _mm_movehdup_ps(s));
+  return _mm_cvtss_f32(s);
+}
+
+template <int MT, int DT>
+__attribute__((target("avx2,fma,f16c")))
+void dot_block_avx2(const float* a, int lda, int n, const void* w, int r0, int r1,
+                    float* out, int ldo) {
+  float part[16][MT];
+  for (int r = 0; r < r1 - r0; ++r)
+    for (int t = 0; t < MT; ++t) part[r][t] = 0.0f;
+  for (int kb = 0; kb < n; kb += kKBlock) {
+    const int ke = (kb + kKBlock) < n ? (kb + kKBlock) : n;
+    const int kv = kb + ((ke - kb) & ~7);
+    for (int r = r0; r < r1; ++r) {
+      const size_t row = static_cast<size_t>(r) * n;
+      prefetch_next_block<DT>(w, row, ke, n);
+      __m256 acc[MT];
+      for (int t = 0; t < MT; ++t) acc[t] = _mm256_setzero_ps();
+      for (int k = kb; k < kv; k += 8) {
+        const __m256 wv = load8_avx2<DT>(w, row + k);
+        for (int t = 0; t < MT; ++t)
+          acc[t] = _mm256_fmadd_ps(wv, _mm256_loadu_ps(a + (size_t)t * lda + k), acc[t]);
+      }
+      for (int t = 0; t < MT; ++t) {
+        float s = hsum_avx2(acc[t]);
+        for (int k = kv; k < ke; ++k) s += load_w(w, row + k, DT) * a[(size_t)t * lda + k];
+        part[r - r0][t] += s;
+      }
+    }
+  }
+  for (int r = r0; r < r1; ++r)
+    for (int t = 0; t < MT; ++t) out[(size_t)t * ldo + r] = part[r - r0][t];
+}
+
+template <int MT>
+__attribute__((target("avx2,fma,f16c")))
+void dot_block_dt_avx2(const float* a, int lda, int n, const void* w, int dtype, int r0,
+                      int r1, float* out, int ldo) {
+  if (dtype == MOE355_HOST_BF16)
+    dot_block_avx2<MT, MOE355_HOST_BF16>(a, lda, n, w, r0, r1, out, ldo);
+  else if (dtype == MOE355_HOST_F16)
+    dot_block_avx2<MT, MOE355_HOST_F16>(a, lda, n, w, r0, r1, out, ldo);
+  else
+    dot_block_avx2<MT, MOE355_HOST_F32>(a, lda, n, w, r0, r1, out, ldo);
+}
+
+__attribute__((target("avx2,fma,f16c")))
+void dot_rows_avx2(const float* a, int lda, int m, int n, const void* w, int dtype, int r0, int r1,
+                   float* out, int ldo) {
+  constexpr int kTok = 4;
+  for (int t0 = 0; t0 < m; t0 += kTok) {
+    const float* at = a + (size_t)t0 * lda;
+    float* ot = out + (size_t)t0 * ldo;
+    switch ((m - t0) < kTok ? (m - t0) : kTok) {
+      case 1: dot_block_dt_avx2<1>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      case 2: dot_block_dt_avx2<2>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      case 3: dot_block_dt_avx2<3>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+      default: dot_block_dt_avx2<4>(at, lda, n, w, dtype, r0, r1, ot, ldo); break;
+    }
+  }
+}
+
+bool have_avx512() {
+  static const bool ok = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw");
+  return ok;
+}
+
+// MOE355_HOST_NO_AVX512=1 keeps the AVX2 path on an AVX-512 host (read per
+// call, so one process can compare both paths).
+bool use_avx512() {
+  const char* e = std::getenv("MOE355_HOST_NO_AVX512");
+  return have_avx512() && !(e && e[0] == '1');
+}
+
+bool have_avx2() {
+  static const bool ok = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") &&
+                         __builtin_cpu_supports("f16c");
+  return ok;
+}
+
+// Rows of W split in blocks of kRowBlock over the threads (static schedule).
+constexpr int kRowBlock = 16;
+
+void dot_rows(const float* a, int lda, int m, int n, const void* w, int dtype, int rows,
+              float* out, int ldo, int n_threads) {
+  const int blocks = (rows + kRowBlock - 1) / kRowBlock;
+  const bool v512 = use_avx512();
+#pragma omp parallel for schedule(static) num_threads(n_threads)
+  for (int b = 0; b < blocks; ++b) {
+    const int r0 = b * kRowBlock;
+    const int r1 = (r0 + kRowBlock) < rows ? (r0 + kRowBlock) : rows;
+    if (v512)
+      dot_rows_avx512(a, lda, m, n, w, dtype, r0, r1, out, ldo);
+    else
+      dot_rows_avx2(a, lda, m, n, w, dtype, r0, r1, out, ldo);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* moe355_host_last_error(void) { return g_err.c_str(); }
+
+int moe355_host_version(void) { return 100; }
+
+int moe355_host_experts(const void* x, int T, int H, int I, int dtype, int n_experts,
+                        const void* const* w1, const void* const* w2,
+                        const int32_t* slot_offsets, const int32_t* slot_tokens,
+                        const float* slot_weights, int act, int n_threads, float* out) {
+  if (!x || !out || !slot_offsets || (n_experts > 0 && (!w1 || !w2 || !slot_tokens ||
+                                                         !slot_weights)))
+    return fail(MOE355_HOST_EINVAL, "null pointer argument");
+  if (T < 0 || H <= 0 || I <= 0 || n_experts < 0)
+    return fail(MOE355_HOST_EINVAL, "bad sizes");
+  if (dtype != MOE355_HOST_F32 && dtype != MOE355_HOST_BF16 && dtype != MOE355_HOST_F16)
+    return fail(MOE355_HOST_EINVAL, "dtype must be f32, bf16 or f16");
+  if (act < 0 || act > 2) return fail(MOE355_HOST_EINVAL, "unknown activation code");
+  if (!have_avx2()) return fail(MOE355_HOST_ECPU, "the host CPU lacks AVX2/FMA/F16C");
+  if (slot_offsets[0] != 0) return fail(MOE355_HOST_EINVAL, "slot_offsets[0] must be 0");
+  for (int e = 0; e < n_experts; ++e) {
+    if (slot_offsets[e + 1] < slot_offsets[e])
+      return fail(MOE355_HOST_EINVAL, "slot_offsets must be non-decreasing");
+    if (!w1[e] || !w2[e]) return fail(MOE355_HOST_EINVAL, "null expert weight pointer");
+  }
+  const int n_slots = n_experts > 0 ? slot_offsets[n_experts] : 0;
+  for (int s = 0; s < n_slots; ++s)
+    if (slot_tokens[s] < 0 || slot_tokens[s] >= T)
+      return fail(MOE355_HOST_EINVAL, "slot token index out of range");
+  if (n_threads <= 0) n_threads = omp_get_max_threads();
+
+  std::vector<float> xa, gu, inter, y;
+  for (int e = 0; e < n_experts; ++e) {
+    const int s0 = slot_offsets[e], m = slot_offsets[e + 1] - s0;
+    if (m == 0) continue;
+    // token rows padded by 64 bytes: rows n*4 bytes apart (n a multiple of
+    // 1024, as H and I usually are) would all fall in the same L1 sets
+    const int ldx = H + 16, ldi = I + 16;
+    xa.assign(static_cast<size_t>(m) * ldx, 0.0f);
+    for (int j = 0; j < m; ++j) {
+      const size_t src = static_cast<size_t>(slot_tokens[s0 + j]) * H;
+      for (int h = 0; h < H; ++h) xa[(size_t)j * ldx + h] = load_w(x, src + h, dtype);
+    }
+    // gate|up: [m, 2I], gate rows first
+    gu.assign(static_cast<size_t>(m) * 2 * I, 0.0f);
+    dot_rows(xa.data(), ldx, m, H, w1[e], dtype, 2 * I, gu.data(), 2 * I, n_threads);
+    inter.assign(static_cast<size_t>(m) * ldi, 0.0f);
+    for (int j = 0; j < m; ++j)
+      for (int i = 0; i < I; ++i)
+        inter[(size_t)j * ldi + i] = round_to_type(
+            act_mul(act, gu[(size_t)j * 2 * I + i], gu[(size_t)j * 2 * I + I + i]), dtype);
+    // down: [m, H]
+    y.assign(static_cast<size_t>(m) * H, 0.0f);
+    dot_rows(inter.data(), ldi, m, I, w2[e], dtype, H, y.data(), H, n_threads);
+    for (int j = 0; j < m; ++j) {
+      float* o = out + static_cast<size_t>(slot_tokens[s0 + j]) * H;
+      const float wt = slot_weights[s0 + j];
+      for (int h = 0; h < H; ++h) o[h] += wt * y[(size_t)j * H + h];
+    }
+  }
+  return 0;
+}
+
+}  // extern "C"

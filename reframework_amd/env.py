@@ -93,6 +93,14 @@ def get_moe_cpu_split() -> bool:
     return _get_bool("RE_MOE_CPU_SPLIT", False)
 
 
+def get_moe_split_copy_depth() -> int:
+    """RE_MOE_SPLIT_COPY_DEPTH (not in the reference): host->device expert
+    copies the CPU/GPU split forward keeps in flight per device when it makes
+    the experts it computed on the host resident for later steps (the
+    reference loads every one, moe_layer.py:601). 0 loads none."""
+    return max(0, _get_int("RE_MOE_SPLIT_COPY_DEPTH", 2))
+
+
 def get_moe_shuttle_steps() -> int:
     return _get_int("RE_MOE_SHUTTLE_STEPS", 0)
 
@@ -131,6 +139,7 @@ __all__ = [
     "get_moe_prefill_overlap",
     "get_moe_cache_policy",
     "get_moe_cpu_split",
+    "get_moe_split_copy_depth",
     "get_moe_shuttle_steps",
     "get_chunk_size",
     "get_max_pack",

@@ -109,6 +109,16 @@ def run_experts(
                           device=x.device)
     if T == 0:
         return out
+    K = topk_ids.shape[1]
+    if len(w1_ptrs) < K:
+        # Fewer bank rows than slots per token (a streaming chunk or a
+        # truncated offload step holding fewer experts than top_k, the other
+        # slots renamed to -1): the library plans for at least K experts, so
+        # the tables are padded with a row no slot maps to.
+        if not len(w1_ptrs):
+            raise ValueError("run_experts needs at least one expert")
+        w1_ptrs = list(w1_ptrs) + [w1_ptrs[-1]] * (K - len(w1_ptrs))
+        w2_ptrs = list(w2_ptrs) + [w2_ptrs[-1]] * (K - len(w2_ptrs))
     stream = _capi.stream_handle(x.device)
     plan = _capi.make_plan(T, H, intermediate_size, len(w1_ptrs), topk_ids.shape[1],
                            _capi.dtype_code(x.dtype), path)

@@ -18,6 +18,14 @@ state dict, offload wiring (``build_offload_cache``, ``attach_predictor``,
     of that many experts, accumulated in fp32 (moe_layer.py:354-420). Chunk
     i+1's host->HBM copies are queued on the cache's side stream while chunk
     i's kernels run.
+  * CPU/GPU split (``enable_cpu_split``, moe_layer.py:523-627): the experts
+    the offload forward would run (``RE_MAX_PACK`` truncation, or every routed
+    expert with ``RE_CHUNK_SIZE`` > 0) are split by residency. Resident ones
+    run on the GPU into an fp32 accumulator while the host cores compute the
+    others from the staged pool (libmoe355_host, 16-bit weights, the device
+    kernels' numerics); the host half is added in fp32 and the sum cast once.
+    Then, while fewer than ``RE_MOE_SPLIT_COPY_DEPTH`` copies are in flight,
+    the host-computed experts are copied to device memory for later steps.
 
 Optional shared experts (``n_shared_experts``; not in the reference, which
 has none): the dense SwiGLU that fine-grained MoEs add to every token after
@@ -30,9 +38,10 @@ expert-sized pieces and folded into the routed call as extra experts that
 every token reaches with weight 1; otherwise it runs as a second call into the
 same fp32 accumulator.
 
-All compute is in libmoe355: the router kernel (GEMV + softmax + top-k) and
-one fused_experts call per forward (or per chunk). A CPU tensor is an error,
-not a slower path.
+All device compute is in libmoe355: the router kernel (GEMV + softmax +
+top-k) and one fused_experts call per forward (or per chunk). A CPU tensor is
+an error, not a slower path; host compute happens only in the split forward,
+which a caller turns on explicitly.
 """
 
 from __future__ import annotations
@@ -42,6 +51,7 @@ import time
 from collections import deque
 from typing import Deque, Dict, List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from reframework_amd import _capi, env
@@ -210,17 +220,16 @@ class FusedMoE(BaseOP):
         self._predictor = self._cache._predictor
 
     def enable_cpu_split(self) -> None:
-        """Accepted for interface compatibility; the split stays off.
-
-        The reference computes non-resident experts on the host with int8
-        GEMMs (moe_layer.py:263-282, 523-627). On MI355X a miss streams from
-        the pinned pool over PCIe on a side stream instead, so every expert is
-        computed by the GPU kernels; ``cpu_split`` remains False.
-        """
+        """Turn on the CPU/GPU split forward for this offloaded layer
+        (reference: moe_layer.py:263-282, 523-627): experts not resident in
+        device memory are computed on the host cores while the GPU runs the
+        resident ones. The host half multiplies the staged 16-bit weights
+        (libmoe355_host) instead of an int8 copy, with the device kernels'
+        numerics. No-op for a layer without an offload cache."""
         if self._cache is None:
             return
-        logger.warning("RE_MOE_CPU_SPLIT: host-side expert compute is not used on MI355X; "
-                       "misses stream to HBM on a side stream instead")
+        self._cache.enable_host_experts()
+        self._cpu_split_enabled = True
 
     def set_shuttle(self, shuttle: Optional[CpuShuttle]) -> None:
         self._shuttle = shuttle
@@ -383,7 +392,9 @@ class FusedMoE(BaseOP):
         w, ids = self._route32(xd, with_shared_cols=not self.uses_offload and self._shared_folded)
         act = activation_code(self.activation)
 
-        if self.uses_offload and env.get_chunk_size(0) > 0:
+        if self.cpu_split:
+            out = self._forward_split(M, xd, w, ids, act)
+        elif self.uses_offload and env.get_chunk_size(0) > 0:
             out = self._forward_streaming(xd, w, ids, act)
         elif self.uses_offload:
             out = self._forward_offload(M, xd, w, ids, act)
@@ -423,7 +434,9 @@ class FusedMoE(BaseOP):
                                           gate.to(self.dtype).contiguous(), None, self.top_k,
                                           self.renormalize, True, normed, w, ids)
         act = activation_code(self.activation)
-        if self.uses_offload and env.get_chunk_size(0) > 0:
+        if self.cpu_split:
+            out = self._forward_split(T, normed, w, ids, act)
+        elif self.uses_offload and env.get_chunk_size(0) > 0:
             out = self._forward_streaming(normed, w, ids, act)
         elif self.uses_offload:
             out = self._forward_offload(T, normed, w, ids, act)
@@ -439,14 +452,7 @@ class FusedMoE(BaseOP):
         cache = self._cache
         ids_host = ids.reshape(-1).tolist()
         w_host = w.reshape(-1).tolist()
-        # Rank experts by summed routing weight (ties: first appearance) and keep
-        # the first RE_MAX_PACK (moe_layer.py:426-442).
-        weight_sum: Dict[int, float] = {}
-        for eid, wt in zip(ids_host, w_host):
-            if eid >= 0:
-                weight_sum[eid] = weight_sum.get(eid, 0.0) + wt
-        kept = [eid for eid, _ in sorted(weight_sum.items(), key=lambda kv: -kv[1])]
-        kept = kept[:env.get_max_pack(2)]
+        kept = self._kept_experts(ids_host, w_host)
         w1s, w2s, local_index = cache.prefetch_slots(kept)
         # Dropped slots contribute nothing; in the routed set recorded for the
         # lookahead they read as the smallest kept id (moe_layer.py:479-486).
@@ -463,6 +469,74 @@ class FusedMoE(BaseOP):
         if not w1p and not len(self.shared_w1):
             return torch.zeros_like(xd)
         return self._experts(xd, w, ids, act, w1p, w2p, expert_map=expert_map)
+
+    @staticmethod
+    def _kept_experts(ids_host: List[int], w_host: List[float]) -> List[int]:
+        """Experts ranked by summed routing weight (ties: first appearance),
+        the first RE_MAX_PACK kept (moe_layer.py:426-442)."""
+        weight_sum: Dict[int, float] = {}
+        for eid, wt in zip(ids_host, w_host):
+            if eid >= 0:
+                weight_sum[eid] = weight_sum.get(eid, 0.0) + wt
+        kept = [eid for eid, _ in sorted(weight_sum.items(), key=lambda kv: -kv[1])]
+        return kept[:env.get_max_pack(2)]
+
+    def _forward_split(self, M: int, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
+                       act: int) -> torch.Tensor:
+        """CPU/GPU split forward (moe_layer.py:523-627). The experts to run
+        are the offload forward's (RE_MAX_PACK truncation, or all routed with
+        RE_CHUNK_SIZE > 0); resident ones with their copy landed run on the
+        GPU into an fp32 accumulator, the rest on the host cores from the
+        staged pool while the GPU works; the host sum is added in fp32 and the
+        total cast once. Each slot's output lands on its own token (the
+        reference indexes tokens as if top_k were 1, F6). Afterwards the
+        host-computed experts are copied to device memory while fewer than
+        RE_MOE_SPLIT_COPY_DEPTH copies are in flight (the reference copies
+        every one: reactive_load, moe_layer.py:601)."""
+        cache = self._cache
+        T, K = ids.shape
+        ids_host = ids.reshape(-1).tolist()  # waits for the router: x is ready too
+        w_host = w.reshape(-1).tolist()
+        if env.get_chunk_size(0) > 0:
+            run = sorted({i for i in ids_host if i >= 0})
+        else:
+            run = self._kept_experts(ids_host, w_host)
+        w1s, w2s, local_index, host_ids = cache.split_slots(run)
+        x_host = xd.cpu() if host_ids else None
+        acc = torch.zeros((T, self.hidden_size), dtype=torch.float32, device=xd.device)
+        expert_map = [-1] * self.num_experts
+        for g, loc in local_index.items():
+            expert_map[g] = loc
+        if w1s or len(self.shared_w1):
+            self._experts(xd, w, ids, act, [t.data_ptr() for t in w1s],
+                          [t.data_ptr() for t in w2s], expert_map=expert_map, out=acc,
+                          accumulate_f32=True)
+        if host_ids:
+            offs, toks, wts = [0], [], []
+            for e in host_ids:
+                for j, eid in enumerate(ids_host):
+                    if eid == e:
+                        toks.append(j // K)
+                        wts.append(w_host[j])
+                offs.append(len(toks))
+            host_out = torch.zeros((T, self.hidden_size), dtype=torch.float32,
+                                   pin_memory=cache._pinned)
+            _capi.host_experts(x_host, [cache._host[e][0] for e in host_ids],
+                               [cache._host[e][1] for e in host_ids],
+                               np.asarray(offs, np.int32), np.asarray(toks or [0], np.int32),
+                               np.asarray(wts or [0.0], np.float32), act, host_out)
+            acc.add_(host_out.to(xd.device, non_blocking=cache._pinned))
+            cache.stats.host_experts += len(host_ids)
+            cache.load_while_idle(host_ids, env.get_moe_split_copy_depth())
+        if self._predictor is not None:
+            ran = set(run)
+            fallback = min(run) if run else -1  # the first kept id, as in _forward_offload
+            routed = [i if i in ran else fallback for i in ids_host]
+            self._predictor.record_step(routed, is_prefill=(M > 1),
+                                        forward_ms=self._since_last_step_ms())
+        out = torch.empty((T, self.hidden_size), dtype=xd.dtype, device=xd.device)
+        _capi.cast_f32(acc, out)
+        return out
 
     def _forward_streaming(self, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
                            act: int) -> torch.Tensor:

@@ -72,10 +72,13 @@ class OffloadStats:
     subs: int = 0
     predicts: int = 0
     inflight_bytes: int = 0
+    # CPU/GPU split forward: experts computed on the host cores (not in the
+    # reference's counters, so not in as_dict)
+    host_experts: int = 0
 
     def reset(self) -> None:
         for name in ("hits", "misses", "evictions", "transfers_bytes", "subs", "predicts",
-                     "inflight_bytes"):
+                     "inflight_bytes", "host_experts"):
             setattr(self, name, 0)
 
     def as_dict(self) -> dict:
@@ -150,6 +153,60 @@ class Prediction:
         return out
 
 
+# Host->device expert copies still running, per device (events of every
+# cache's copies, pruned as they complete): the CPU/GPU split forward bounds
+# its loads by this count so they never queue up behind each other.
+_INFLIGHT: Dict[int, List[object]] = {}
+
+
+def inflight_copies(device: torch.device) -> int:
+    evs = _INFLIGHT.get(device.index if device.index is not None else 0)
+    if not evs:
+        return 0
+    evs[:] = [e for e in evs if not e.query()]
+    return len(evs)
+
+
+def _note_inflight(device: torch.device, event) -> None:
+    evs = _INFLIGHT.setdefault(device.index if device.index is not None else 0, [])
+    evs[:] = [e for e in evs if not e.query()]
+    evs.append(event)
+
+
+class _HostPool:
+    """Owner of one staged host buffer, shared by every cache that reads it
+    (``share_host``).
+
+    Copies out of the buffer are raw ``hipMemcpyAsync`` calls, which torch's
+    pinned allocator does not track: once the last reference to a pinned
+    block is gone it may hand the pages out again at once. Each cache
+    therefore notes the last copy it queued on its copy stream here, and the
+    buffer is released only after every noted copy has finished (when the
+    holder itself is dropped, i.e. when the last cache reading it lets go or
+    replaces it)."""
+
+    __slots__ = ("buf", "_last")
+
+    def __init__(self, buf: torch.Tensor) -> None:
+        self.buf = buf
+        self._last: Dict[int, object] = {}  # copy stream handle -> last copy event
+
+    def note_copy(self, stream_key: int, event) -> None:
+        self._last[stream_key] = event  # stream order: it covers the earlier copies
+
+    def drain(self) -> None:
+        """Wait for every copy noted so far."""
+        last, self._last = self._last, {}
+        for ev in last.values():
+            ev.synchronize()
+
+    def __del__(self) -> None:
+        try:
+            self.drain()
+        except Exception:  # interpreter shutdown: the runtime may already be gone
+            pass
+
+
 class _Slot:
     """One HBM buffer holding an expert's w1 then w2, plus its stream events."""
 
@@ -199,10 +256,12 @@ class ExpertPool:
     def forget(self, cache: "ExpertOffloadCache", idx: int) -> None:
         self._order.pop((id(cache), int(idx)), None)
 
-    def evict(self, cache: "ExpertOffloadCache", hard: Sequence[int]) -> None:
-        """Evict oldest-first down to capacity, sparing ``cache``'s ``hard``."""
+    def evict(self, cache: "ExpertOffloadCache", hard: Sequence[int], incoming: int = 0) -> None:
+        """Evict oldest-first down to capacity, sparing ``cache``'s ``hard``;
+        with ``incoming`` > 0, make room for that many entries about to be
+        admitted (the victims the same admission would evict afterwards)."""
         spare = {(id(cache), int(i)) for i in hard}
-        while len(self._order) > self.capacity:
+        while len(self._order) + incoming > self.capacity:
             victim = next((k for k in self._order if k not in spare), None)
             if victim is None:
                 return
@@ -239,6 +298,7 @@ class ExpertOffloadCache:
         self.dtype = dtype
         self._host: List[Tuple[torch.Tensor, torch.Tensor]] = []
         self._host_buf: Optional[torch.Tensor] = None
+        self._host_pool: Optional[_HostPool] = None
         self._host_off: List[int] = []
         self._pinned = False
         self._lru: "OrderedDict[int, Tuple[torch.Tensor, torch.Tensor]]" = OrderedDict()
@@ -311,6 +371,7 @@ class ExpertOffloadCache:
             raise ValueError("the other cache has no staged experts")
         if other.dtype != self.dtype:
             raise ValueError(f"host pool dtype {other.dtype} != cache dtype {self.dtype}")
+        self._host_pool = other._host_pool
         self._host_buf = other._host_buf
         self._host = list(other._host)
         self._host_off = list(other._host_off)
@@ -325,16 +386,15 @@ class ExpertOffloadCache:
         total = 0
         for s1, s2 in shapes:
             total += s1[0] * s1[1] + s2[0] * s2[1]
-        if self._copy_stream is not None:
-            # copies out of the pool being replaced must finish before the
-            # pinned allocator can reuse its pages
-            self._copy_stream.synchronize()
+        # The pool being replaced (if any) is released when its holder is
+        # dropped, after the copies every sharing cache queued out of it.
         try:
             buf = torch.empty(total, dtype=self.dtype, pin_memory=True)
             self._pinned = True
         except (RuntimeError, AssertionError):
             buf = torch.empty(total, dtype=self.dtype)
             self._pinned = False
+        self._host_pool = _HostPool(buf)
         self._host_buf = buf
         self._host, self._host_off = [], []
         off = 0
@@ -480,6 +540,12 @@ class ExpertOffloadCache:
         hits = sum(1 for i in uniq if i in self._lru)
         logger.debug("[offload] prefetch: requested=%d unique=%d hit=%d miss=%d lru_size=%d",
                      len(indices), len(uniq), hits, len(uniq) - hits, len(self._lru))
+        if self.sim_table is None:
+            # Evict first what admitting the misses will evict anyway, so
+            # their copies reuse the freed slots and residency never exceeds
+            # max(capacity, request). (With a similarity table a victim may
+            # still serve a miss as its substitute: keep the reference order.)
+            self._make_room(uniq, len(uniq) - hits)
         for idx in uniq:
             if idx in self._lru:
                 self.stats.hits += 1
@@ -493,6 +559,18 @@ class ExpertOffloadCache:
         else:
             self._evict(uniq, self._next_reserve - set(uniq))
         return uniq
+
+    def _make_room(self, hard: Sequence[int], incoming: int) -> None:
+        """Evict, ahead of admitting ``incoming`` new entries, the entries
+        the eviction after the admission would pick: the admitted entries are
+        hard-protected, so they are never the victims, and the victims' order
+        does not depend on them."""
+        if incoming <= 0:
+            return
+        if self._pool is not None:
+            self._pool.evict(self, hard, incoming=incoming)
+        else:
+            self._evict(hard, self._next_reserve - set(int(i) for i in hard), incoming=incoming)
 
     def prefetch(self, indices: Sequence[int]) -> Tuple[torch.Tensor, torch.Tensor, Dict[int, int]]:
         """Bring ``indices`` resident; return stacked banks ``[N,2I,H]``,
@@ -528,8 +606,66 @@ class ExpertOffloadCache:
                      torch.empty((0, H, I), dtype=self.dtype, device=self.device), {})
         return banks, misses
 
+    def enable_host_experts(self) -> None:
+        """Arm the CPU/GPU split for this cache: experts that are not
+        resident are computed on the host cores straight from the staged
+        pool (libmoe355_host), so no int8 bank is built (the reference's
+        quantize_int8_host, offload_cache.py:386-407, stays available)."""
+        if not self._host:
+            return
+        _capi.host_lib()  # a missing host library fails here, not mid-forward
+        self._cpu_split = True
+
+    def split_slots(self, indices: Sequence[int]):
+        """Split ``indices`` for the CPU/GPU split forward (reference:
+        split_prefetch, offload_cache.py:509-552): experts resident in device
+        memory whose copy has landed go to the device half (hits: moved to the
+        recent end), every other one to the host half. Nothing is copied here.
+        Returns (w1 views, w2 views, {id: row}) of the device half, in
+        ascending id, and the host half's ids."""
+        uniq = sorted(set(int(i) for i in indices if int(i) >= 0))
+        dev_ids, host_ids = [], []
+        for i in uniq:
+            slot = self._slot_of.get(i)
+            landed = i in self._lru and (slot is None or slot.ready is None or slot.ready.query())
+            if landed:
+                self.stats.hits += 1
+                self._lru.move_to_end(i)
+                if self._pool is not None:
+                    self._pool.touch(self, i)
+                dev_ids.append(i)
+            else:
+                host_ids.append(i)
+        self._wait_ready(dev_ids)
+        w1 = [self._lru[i][0] for i in dev_ids]
+        w2 = [self._lru[i][1] for i in dev_ids]
+        return w1, w2, {idx: k for k, idx in enumerate(dev_ids)}, host_ids
+
+    def load_while_idle(self, indices: Sequence[int], max_inflight: int) -> List[int]:
+        """The split forward's reactive load (reference: reactive_load after
+        the merge, moe_layer.py:601): make the non-resident experts of
+        ``indices`` resident, in ascending id, while fewer than
+        ``max_inflight`` host->device copies run on this device. Evicts as
+        reactive_load does (only the experts being loaded are protected).
+        Returns the ids loaded."""
+        loaded: List[int] = []
+        if self.device.type != "cuda":
+            return loaded
+        for i in sorted(set(int(x) for x in indices)):
+            if i in self._lru:
+                continue
+            if inflight_copies(self.device) >= max_inflight:
+                break
+            self._make_room(loaded + [i], 1)
+            self._fill(i)
+            loaded.append(i)
+            if self._pool is not None:
+                self._pool.touch(self, i)
+        return loaded
+
     def reactive_load(self, indices: Sequence[int]) -> None:
         uniq = sorted(set(int(i) for i in indices))
+        self._make_room(uniq, sum(1 for i in uniq if i not in self._lru))
         for i in uniq:
             if i not in self._lru:
                 self._fill(i)
@@ -578,6 +714,11 @@ class ExpertOffloadCache:
                 if nbytes > budget and loaded:
                     break
                 budget -= nbytes
+            # only stale entries (outside protect) make room, before the copy
+            if self._pool is not None:
+                self._pool.evict(self, protect, incoming=1)
+            else:
+                self._evict(protect, incoming=1)
             self._fill(idx)
             self.stats.predicts += 1
             loaded.append(idx)
@@ -673,11 +814,13 @@ class ExpertOffloadCache:
             _capi.h2d_async(slot.buf.data_ptr(), src, nbytes, cs.cuda_stream)
             # The copy is raw hipMemcpyAsync: tell torch's device allocator
             # that the copy stream uses the slot, so a dropped slot's memory
-            # is not handed out again before the copy is done. (The host pool
-            # is only replaced after the copy stream drains: _alloc_pool.)
+            # is not handed out again before the copy is done, and note the
+            # copy on the host pool, which is not released before it is done.
             slot.buf.record_stream(cs)
             ev = torch.cuda.Event(enable_timing=t0 is not None)
             ev.record(cs)
+            self._host_pool.note_copy(cs.cuda_stream, ev)
+            _note_inflight(self.device, ev)
             if t0 is not None:
                 self._copy_log.append((t0, ev, nbytes))
             slot.ready = ev
@@ -699,10 +842,12 @@ class ExpertOffloadCache:
             self._release(slot)
         self.stats.evictions += 1
 
-    def _evict(self, hard_protect: Sequence[int], soft_protect: Sequence[int] = ()) -> None:
-        """Evict down to ``lru_capacity``: stale entries first, then soft ones,
-        never hard ones. ``lru`` picks the oldest; ``least_stale`` picks the
-        largest routing age (never seen = window), oldest on ties."""
+    def _evict(self, hard_protect: Sequence[int], soft_protect: Sequence[int] = (),
+               incoming: int = 0) -> None:
+        """Evict down to ``lru_capacity`` (less ``incoming`` entries about to
+        be admitted): stale entries first, then soft ones, never hard ones.
+        ``lru`` picks the oldest; ``least_stale`` picks the largest routing age
+        (never seen = window), oldest on ties."""
         hard = {int(i) for i in hard_protect}
         soft = {int(i) for i in soft_protect} - hard
         predictor = self._predictor
@@ -720,7 +865,7 @@ class ExpertOffloadCache:
             def victim_of(cands: List[int]) -> Optional[int]:
                 return cands[0] if cands else None
 
-        while len(self._lru) > self.lru_capacity:
+        while len(self._lru) + incoming > self.lru_capacity:
             victim = victim_of([i for i in self._lru if i not in hard and i not in soft])
             if victim is None:
                 victim = victim_of([i for i in self._lru if i in soft])

@@ -94,4 +94,10 @@ def _check_asm(asm):
                 assert "scratch_" not in code, f"{name}: scratch access: {l.strip()}"
         meta = "\n".join(l for l in lines if l.strip().startswith(f".set {name}."))
         assert re.search(rf"{re.escape(name)}\.num_agpr, 256\b", meta), name
+        # The fixed operand fragments v128-v255 are named only by the inline
+        # assembly: the kernel's arch VGPR count must still cover them, or
+        # the accumulators (AGPRs after accum_offset) would overlap them.
+        assert re.search(rf"{re.escape(name)}\.num_vgpr, 256\b", meta), name
         assert re.search(rf"{re.escape(name)}\.private_seg_size, 0\b", meta), name
+    offsets = [int(m) for m in re.findall(r"\.amdhsa_accum_offset (\d+)", asm.read_text())]
+    assert len(offsets) == 2 and all(o >= 256 for o in offsets), offsets

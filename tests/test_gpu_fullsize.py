@@ -6,9 +6,11 @@ and down run their items on one workgroup per CU; the items of a last,
 partly filled round are cut along K over the idle CUs, their fp32 partial
 tiles summed (and activated, for gate_up) by a fix-up kernel. These tests
 build routings whose tile counts put that split on (checked with the host
-replica of its rule), and compare
-sampled tokens (the first and last token of every expert group, whose rows
-sit in the first and last tiles, plus random ones) with the fp64 oracle:
+replica of its rule), and compare sampled tokens with the fp64 oracle: the
+tokens at the first, middle and last row of every token tile of the tile map
+(the tiles' rows and heights by the permute's rules, which
+test_gpu_experts.py checks against the map the kernel writes), so every tile
+of every launch is checked, plus a few random tokens:
   * <= 2e-2 max-relative against the fp64 oracle;
   * against the oracle that rounds the intermediate (and, for the tiled
     paths with one down K-split, y) like the kernels: every element within
@@ -32,7 +34,7 @@ import pytest
 import torch
 
 from _helpers import (ROUND, assert_matches_rounded, assert_y_rounding, banner, gpu_fused,
-                      read_ws, tiled_down_split, tiled_gate_up_split, y_round_of)
+                      read_ws, tile_height, tiled_down_split, tiled_gate_up_split, y_round_of)
 from oracle import oracle
 from reframework_amd import _capi, synth
 
@@ -105,14 +107,29 @@ def _ids_from_counts(counts, experts, seed):
     return ids[:, None]
 
 
-def _sample_tokens(ids, n_random, seed):
-    """First and last token of every expert's group plus random tokens."""
+def _sample_tokens(ids, n_random, seed, tile_rows=256):
+    """The tokens whose rows sit at the first, middle and last position of
+    every token tile of the tile map (``tile_rows``-row map: an expert of n
+    rows has ceil(n / tile_rows) tiles ``tile_height`` rows apart, the last
+    one ending at its n-th row), plus ``n_random`` random tokens. Rows map to
+    tokens through the stable grouping (expert ascending, token ascending)."""
     T = ids.shape[0]
-    pick = set()
-    for e in np.unique(ids):
-        t = np.nonzero((ids == e).any(axis=1))[0]
-        pick.update((int(t[0]), int(t[-1])))
+    E = int(ids.max()) + 1
+    offsets, _, src = oracle.permute(ids, E)
+    pick, n_tiles = set(), 0
+    for e in range(E):
+        n = int(offsets[e + 1] - offsets[e])
+        if n == 0:
+            continue
+        h = tile_height(n, tile_rows)
+        for j in range(-(-n // tile_rows)):
+            lo, hi = j * h, min((j + 1) * h, n) - 1
+            assert lo <= hi, (e, n, j, h)
+            n_tiles += 1
+            for r in (lo, (lo + hi) // 2, hi):
+                pick.add(int(src[offsets[e] + r]))
     pick.update(int(t) for t in np.random.default_rng(seed).choice(T, n_random, replace=False))
+    print(f"  {n_tiles} token tiles of {tile_rows} rows: {len(pick)} tokens checked", flush=True)
     return sorted(pick)
 
 
@@ -289,7 +306,8 @@ def test_mixtral_t256_sampled_tokens(mixtral, dev):
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
     w = rng.random((T, K)).astype(np.float32)
     out = gpu_fused(x, m["w1"], m["w2"], w, ids)
-    _check_sampled(out, x, m["w1"], m["w2"], w, ids, _sample_tokens(ids, 8, seed=6))
+    _check_sampled(out, x, m["w1"], m["w2"], w, ids,
+                   _sample_tokens(ids, 8, seed=6, tile_rows=plan.tile_rows))
 
 
 def test_phi35_t2048_sampled_tokens(dev):
