@@ -47,12 +47,9 @@ def parse():
     ap.add_argument("--offload-host-pools", type=int, default=4,
                     help="distinct layers' experts staged in pinned memory (at most 4); deeper "
                          "layers reuse them")
-    ap.add_argument("--offload-modes", type=str,
-                    default="max_pack_2_per_layer_lru,max_pack_2_shared_pool,"
-                            "max_pack_2_per_layer_lru_cpu_split,exact_chunk2_per_layer_lru,"
-                            "exact_chunk1_shared_pool",
-                    help="offload forward/residency modes; also "
-                         "max_pack_2_shared_pool_lookahead_t1")
+    ap.add_argument("--offload-modes", type=str, default="",
+                    help="comma-separated offload forward/residency modes (default: all of "
+                         "bench.OFFLOAD_MODES)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--profile", type=int, default=0,
@@ -441,11 +438,14 @@ def _progress(msg):
 MAX_STAGED_HOST_POOLS = 4
 
 
-def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps=32,
-                          modes=("max_pack_2_per_layer_lru", "max_pack_2_shared_pool",
-                                 "max_pack_2_per_layer_lru_cpu_split",
-                                 "exact_chunk2_per_layer_lru", "exact_chunk1_shared_pool"),
-                          host_pools=4):
+OFFLOAD_MODES = ("max_pack_2_per_layer_lru", "max_pack_2_shared_pool",
+                 "max_pack_2_per_layer_lru_cpu_split", "exact_per_layer_lru_cpu_split",
+                 "exact_chunk1_shared_pool", "max_pack_2_shared_pool_t1",
+                 "max_pack_2_shared_pool_lookahead_t1")
+
+
+def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps=16,
+                          modes=OFFLOAD_MODES, host_pools=4):
     """Decode through expert offload: a stack of Mixtral-shape layers (8
     experts each, 352 MB per expert in bf16) whose experts live in pinned host
     memory, with HBM room for 2 experts per layer (64 of 256 expert slots for
@@ -468,13 +468,16 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps
         forward: experts not resident run on the host cores from the pinned
         pool while the GPU runs the others; at most 2 copies in flight bring
         host-computed experts into HBM for later steps;
-      * exact_chunk{2,1}_*: every routed expert, streamed in chunks of 2
-        (per-layer LRU of 2) or 1 (shared pool); these move several times
-        more bytes per step and run ``short_steps`` steps, named in the key.
-    Mode "max_pack_2_shared_pool_lookahead_t1" (not in the default list)
-    attaches the lookahead predictor at batch 1 (a forward over more tokens is
-    a prefill to it, as in the reference) over a pool with 2 spare slots per
-    layer."""
+      * exact_per_layer_lru_cpu_split: every routed expert (no truncation),
+        with the CPU/GPU split, ``4 * short_steps`` steps;
+      * exact_chunk1_shared_pool: every routed expert, streamed one expert per
+        chunk over the shared pool (chunk i+1's copy runs under chunk i's
+        kernels); it moves several times more bytes per step than truncation
+        and runs ``short_steps`` steps, named in the key;
+      * max_pack_2_shared_pool_t1 and ..._lookahead_t1: batch 1 (a forward
+        over more tokens is a prefill to the predictor, as in the reference)
+        over a pool with 2 spare slots per layer (4 per layer), without and
+        with the lookahead predictor, ``steps // 2`` steps each."""
     import numpy as np
     import torch
 
@@ -523,7 +526,9 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps
     expert_bytes = 3 * h * i * 2
 
     # the host-compute lever: one expert on the host cores from the pinned pool
+    # (its pages read once first, as enabling the split does)
     host = layers[0]._cache._host
+    layers[0]._cache._host_pool.touch_pages()
     xh = synth.make_tokens(T, h, torch.bfloat16, seed=9)
     host_ms = {}
     for m in (1, 4, T):
@@ -627,13 +632,20 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps
            "peak_pinned_h2d_gb_s": round(peak_h2d, 2), "host_expert": host_expert}
     for mode in modes:
         shared = "shared_pool" in mode
-        chunk = int(mode.split("chunk")[1].split("_")[0]) if mode.startswith("exact_chunk") else 0
-        lookahead = mode.endswith("lookahead_t1")
-        pool = ExpertPool(capacity=(4 if lookahead else 2) * n_layers) if shared else None
-        n_steps = min(steps, short_steps) if chunk else steps
-        key = f"{mode}_{n_steps}_steps" if chunk else mode
-        res[key] = run_mode(mode, pool, chunk, n_steps, split=mode.endswith("cpu_split"),
-                            lookahead=lookahead, tokens=1 if lookahead else T)
+        split = mode.endswith("cpu_split")
+        t1 = mode.endswith("_t1")
+        if mode.startswith("exact_chunk"):
+            chunk = int(mode.split("chunk")[1].split("_")[0])
+        else:  # the split runs every routed expert when RE_CHUNK_SIZE > 0
+            chunk = 8 if mode.startswith("exact") else 0
+        pool = ExpertPool(capacity=(4 if t1 else 2) * n_layers) if shared else None
+        if chunk:  # every routed expert: several times the bytes of truncation per step
+            n_steps = min(steps, 4 * short_steps if split else short_steps)
+        else:
+            n_steps = max(1, steps // 2) if t1 else steps
+        key = f"{mode}_{n_steps}_steps" if n_steps != steps else mode
+        res[key] = run_mode(mode, pool, chunk, n_steps, split=split,
+                            lookahead=mode.endswith("lookahead_t1"), tokens=1 if t1 else T)
     for moe in layers:
         moe._cache.use_pool(None)
     del layers
@@ -754,7 +766,7 @@ def main():
         configs["offload_decode"] = config_offload_decode(
             dev, args.offload_layers, args.offload_steps, T=args.offload_tokens,
             host_pools=args.offload_host_pools,
-            modes=tuple(m for m in args.offload_modes.split(",") if m))
+            modes=tuple(m for m in args.offload_modes.split(",") if m) or OFFLOAD_MODES)
 
     cpu = None
     if not args.skip_cpu:

@@ -260,6 +260,41 @@ int moe355_fused_experts_static(const void* x, const void* const* w1, const void
 int moe355_cast_f32(const float* src, void* dst, size_t n, int dtype, void* stream);
 
 /*
+ * Zero-copy staging for the CPU/GPU split forward. The reference's split moves
+ * the step's routing and hidden states to the host with synchronous copies
+ * (`topk_ids.reshape(-1).tolist()`, reframework/moe/moe_layer.py:550-551;
+ * `hidden_states.detach().cpu()`, reframework/moe/fused.py:175) and the host
+ * half back with `cpu_out.to(dev)` (moe_layer.py:597). On MI355X those small
+ * transfers would queue on the DMA engines behind the 352 MB expert copies
+ * the split keeps in flight, so a kernel on the compute stream moves them
+ * through mapped pinned host memory instead.
+ *
+ * moe355_host_staging_alloc: `bytes` of mapped, coherent pinned host memory
+ * (hipHostMalloc), readable and writable by kernels. Free with
+ * moe355_host_staging_free once no queued kernel uses it.
+ */
+int moe355_host_staging_alloc(size_t bytes, void** host_ptr);
+int moe355_host_staging_free(void* host_ptr);
+
+/*
+ * Copy `bytes` of device memory at `src` into staging memory at `host_dst`
+ * (any address inside a moe355_host_staging_alloc buffer, or other mapped
+ * pinned memory) with a kernel on `stream`; both 16-byte aligned. The host
+ * reads the bytes after waiting for an event recorded behind the call.
+ */
+int moe355_copy_to_host(void* host_dst, const void* src, size_t bytes, void* stream);
+
+/*
+ * out[i] = (dtype) (acc[i] + host_src[i]) for i < n, reading host_src
+ * (fp32 in mapped pinned memory, written by the host before the call) from
+ * the kernel: the merge `out.float() + cpu_out.to(dev)` then `.to(x2.dtype)`
+ * of reframework/moe/moe_layer.py:597-598. n a multiple of 4; acc, host_src
+ * 16-byte aligned; acc is fp32 device memory, out [n] of `dtype`.
+ */
+int moe355_merge_host_f32(const float* acc, const float* host_src, size_t n, int dtype, void* out,
+                          void* stream);
+
+/*
  * Host -> HBM expert copy on `stream` (a side stream), asynchronous when `src`
  * is pinned. Replaces ExpertOffloadCache._fill's `.to(device, non_blocking)`
  * (reframework/moe/offload_cache.py:645-652). Completion is observed with an

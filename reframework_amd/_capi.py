@@ -92,6 +92,10 @@ _SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
                                          _I, _I, _I, _P, _I, _P]),
     "moe355_cast_f32": (_I, [_P, _P, _Z, _I, _P]),
     "moe355_h2d_async": (_I, [_P, _P, _Z, _P]),
+    "moe355_host_staging_alloc": (_I, [_Z, ctypes.POINTER(ctypes.c_void_p)]),
+    "moe355_host_staging_free": (_I, [_P]),
+    "moe355_copy_to_host": (_I, [_P, _P, _Z, _P]),
+    "moe355_merge_host_f32": (_I, [_P, _P, _Z, _I, _P, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -390,6 +394,63 @@ def cast_f32(src: torch.Tensor, dst: torch.Tensor, stream: Optional[int] = None)
 
 def h2d_async(dst_ptr: int, src_ptr: int, nbytes: int, stream: int) -> None:
     _check("moe355_h2d_async", lib().moe355_h2d_async(dst_ptr, src_ptr, nbytes, stream))
+
+
+def copy_to_host(host_dst: int, src: torch.Tensor, nbytes: int,
+                 stream: Optional[int] = None) -> None:
+    """moe355_copy_to_host: ``nbytes`` of ``src`` into mapped pinned host
+    memory at address ``host_dst`` by a kernel on the stream."""
+    s = stream if stream is not None else stream_handle(src.device)
+    _check("moe355_copy_to_host", lib().moe355_copy_to_host(host_dst, _ptr(src), nbytes, s))
+
+
+def merge_host_f32(acc: torch.Tensor, host_src: int, out: torch.Tensor,
+                   stream: Optional[int] = None) -> None:
+    """moe355_merge_host_f32: out = (out dtype) (acc + the fp32 host array at
+    address ``host_src``), the host array read by the kernel."""
+    s = stream if stream is not None else stream_handle(acc.device)
+    _check("moe355_merge_host_f32", lib().moe355_merge_host_f32(
+        _ptr(acc), host_src, acc.numel(), dtype_code(out.dtype), _ptr(out), s))
+
+
+class HostStaging:
+    """One mapped, coherent pinned host buffer (moe355_host_staging_alloc)
+    that kernels on one stream read and write directly: the CPU/GPU split
+    forward's routing, hidden states and host-half result travel through it.
+    Calls on one stream are ordered, so a step may reuse it once the previous
+    step's kernels that touch it are queued before its own. Kept for the life
+    of the process (a queued kernel may still read it when a caller drops
+    it)."""
+
+    CAPACITY = 8 << 20
+
+    def __init__(self, nbytes: int = CAPACITY) -> None:
+        p = ctypes.c_void_p()
+        _check("moe355_host_staging_alloc", lib().moe355_host_staging_alloc(nbytes,
+                                                                            ctypes.byref(p)))
+        self.ptr = int(p.value)
+        self.nbytes = nbytes
+        self._bytes = (ctypes.c_uint8 * nbytes).from_address(self.ptr)
+
+    def array(self, offset: int, dtype, count: int):
+        """numpy view of ``count`` elements of ``dtype`` at byte ``offset``."""
+        import numpy as np
+
+        return np.frombuffer(self._bytes, dtype=dtype, count=count, offset=offset)
+
+
+_STAGING: Dict[Tuple[int, int], HostStaging] = {}
+
+
+def staging(device: torch.device, stream: int) -> HostStaging:
+    """The staging buffer of (device, stream), created on first use."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    buf = _STAGING.get(key)
+    if buf is None:
+        with torch.cuda.device(key[0]):
+            buf = HostStaging()
+        _STAGING[key] = buf
+    return buf
 
 
 def host_experts(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch.Tensor],

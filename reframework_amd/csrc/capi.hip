@@ -612,6 +612,59 @@ int moe355_cast_f32(const float* src, void* dst, size_t n, int dtype, void* stre
   return check_hip(launch_cast_f32(src, dst, n, dtype, as_stream(stream)), "cast launch");
 }
 
+int moe355_host_staging_alloc(size_t bytes, void** host_ptr) {
+  if (!host_ptr) return fail(MOE355_EINVAL, "NULL host_ptr");
+  *host_ptr = nullptr;
+  if (bytes == 0) return fail(MOE355_EINVAL, "zero-byte staging buffer");
+  return check_hip(hipHostMalloc(host_ptr, bytes,
+                                 hipHostMallocMapped | hipHostMallocCoherent |
+                                     hipHostMallocPortable),
+                   "hipHostMalloc (mapped, coherent)");
+}
+
+int moe355_host_staging_free(void* host_ptr) {
+  if (!host_ptr) return MOE355_OK;
+  return check_hip(hipHostFree(host_ptr), "hipHostFree");
+}
+
+namespace {
+// The device address of a mapped pinned host pointer (interior pointers
+// included); fails, and nothing is launched, for memory the runtime did not
+// map for the device.
+int device_view(const void* host_ptr, void** dev_ptr, const char* what) {
+  *dev_ptr = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(dev_ptr, const_cast<void*>(host_ptr), 0);
+  if (e != hipSuccess || !*dev_ptr)
+    return fail(MOE355_EINVAL, "%s is not mapped pinned host memory (%s)", what,
+                hipGetErrorString(e));
+  return MOE355_OK;
+}
+}  // namespace
+
+int moe355_copy_to_host(void* host_dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return MOE355_OK;
+  if (!host_dst || !src) return fail(MOE355_EINVAL, "NULL host_dst or src");
+  if ((reinterpret_cast<uintptr_t>(host_dst) | reinterpret_cast<uintptr_t>(src)) & 15)
+    return fail(MOE355_EINVAL, "host_dst and src must be 16-byte aligned");
+  void* dst = nullptr;
+  if (int rc = device_view(host_dst, &dst, "host_dst")) return rc;
+  return check_hip(launch_copy_bytes(src, dst, bytes, as_stream(stream)), "copy_to_host launch");
+}
+
+int moe355_merge_host_f32(const float* acc, const float* host_src, size_t n, int dtype, void* out,
+                          void* stream) {
+  if (!valid_dtype(dtype)) return fail(MOE355_EINVAL, "unknown dtype %d", dtype);
+  if (n == 0) return MOE355_OK;
+  if (!acc || !host_src || !out) return fail(MOE355_EINVAL, "NULL acc, host_src or out");
+  if (n % 4 || ((reinterpret_cast<uintptr_t>(acc) | reinterpret_cast<uintptr_t>(host_src)) & 15))
+    return fail(MOE355_EINVAL, "n must be a multiple of 4 and acc, host_src 16-byte aligned");
+  void* src = nullptr;
+  if (int rc = device_view(host_src, &src, "host_src")) return rc;
+  return check_hip(launch_merge_host(acc, static_cast<const float*>(src), out, n, dtype,
+                                     as_stream(stream)),
+                   "merge_host launch");
+}
+
 int moe355_h2d_async(void* dst, const void* src, size_t bytes, void* stream) {
   if (bytes == 0) return MOE355_OK;
   if (!dst || !src) return fail(MOE355_EINVAL, "NULL dst or src");

@@ -231,7 +231,67 @@ hipError_t launch_combine_t(const CombineArgs& a, int dtype, hipStream_t s) {
   return launch_combine_v<OutT, 4, kWave>(a, dtype, s);
 }
 
+// Zero-copy staging for the CPU/GPU split forward (the host buffers are
+// mapped, coherent pinned memory): a kernel moves a decode step's few bytes
+// between HBM and host memory itself, so nothing waits on the DMA engines,
+// which the background expert copies keep busy.
+__global__ __launch_bounds__(kThreads) void copy_bytes_kernel(const uint8_t* src, uint8_t* dst,
+                                                             size_t n) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  const size_t n16 = n / 16;
+  const size_t t = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+  for (size_t i = t; i < n16; i += stride)
+    reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+  for (size_t i = n16 * 16 + t; i < n; i += stride) dst[i] = src[i];
+}
+
+// out = acc + host, rounded once to OutT: the host half of the split forward
+// read straight from host memory (16-byte vectors; n a multiple of 4).
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void merge_host_kernel(const float4* acc,
+                                                             const float4* host, OutT* out,
+                                                             size_t n4) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; i < n4;
+       i += static_cast<size_t>(gridDim.x) * kThreads) {
+    const float4 a = acc[i], h = host[i];
+    out[4 * i + 0] = from_f32<OutT>(a.x + h.x);
+    out[4 * i + 1] = from_f32<OutT>(a.y + h.y);
+    out[4 * i + 2] = from_f32<OutT>(a.z + h.z);
+    out[4 * i + 3] = from_f32<OutT>(a.w + h.w);
+  }
+}
+
 }  // namespace
+
+hipError_t launch_copy_bytes(const void* src, void* dst, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  size_t blocks = (n / 16 + kThreads - 1) / kThreads;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 1024) blocks = 1024;
+  copy_bytes_kernel<<<dim3(blocks), dim3(kThreads), 0, s>>>(static_cast<const uint8_t*>(src),
+                                                           static_cast<uint8_t*>(dst), n);
+  return hipGetLastError();
+}
+
+hipError_t launch_merge_host(const float* acc, const float* host, void* out, size_t n, int dtype,
+                             hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const size_t n4 = n / 4;
+  size_t blocks = (n4 + kThreads - 1) / kThreads;
+  if (blocks > 4096) blocks = 4096;
+  const float4* a = reinterpret_cast<const float4*>(acc);
+  const float4* h = reinterpret_cast<const float4*>(host);
+  if (dtype == MOE355_BF16)
+    merge_host_kernel<bf16><<<dim3(blocks), dim3(kThreads), 0, s>>>(a, h, static_cast<bf16*>(out),
+                                                                    n4);
+  else if (dtype == MOE355_F16)
+    merge_host_kernel<f16><<<dim3(blocks), dim3(kThreads), 0, s>>>(a, h, static_cast<f16*>(out),
+                                                                   n4);
+  else
+    merge_host_kernel<float><<<dim3(blocks), dim3(kThreads), 0, s>>>(a, h,
+                                                                     static_cast<float*>(out), n4);
+  return hipGetLastError();
+}
 
 // out_dtype is the layer dtype (the type of y when a.y16).
 hipError_t launch_combine(const CombineArgs& a, int out_dtype, hipStream_t s) {

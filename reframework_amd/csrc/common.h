@@ -282,5 +282,8 @@ hipError_t launch_gate_up_simt(const FfnArgs& a, int dtype, hipStream_t s);
 hipError_t launch_down_simt(const FfnArgs& a, int dtype, hipStream_t s);
 hipError_t launch_combine(const CombineArgs& a, int out_dtype, hipStream_t s);
 hipError_t launch_cast_f32(const float* src, void* dst, size_t n, int dtype, hipStream_t s);
+hipError_t launch_copy_bytes(const void* src, void* dst, size_t n, hipStream_t s);
+hipError_t launch_merge_host(const float* acc, const float* host, void* out, size_t n, int dtype,
+                             hipStream_t s);
 
 }  // namespace moe355

@@ -468,7 +468,9 @@ class FusedMoE(BaseOP):
         w2p = [t.data_ptr() for t in w2s]
         if not w1p and not len(self.shared_w1):
             return torch.zeros_like(xd)
-        return self._experts(xd, w, ids, act, w1p, w2p, expert_map=expert_map)
+        out = self._experts(xd, w, ids, act, w1p, w2p, expert_map=expert_map)
+        cache.mark_read(local_index)
+        return out
 
     @staticmethod
     def _kept_experts(ids_host: List[int], w_host: List[float]) -> List[int]:
@@ -492,18 +494,47 @@ class FusedMoE(BaseOP):
         reference indexes tokens as if top_k were 1, F6). Afterwards the
         host-computed experts are copied to device memory while fewer than
         RE_MOE_SPLIT_COPY_DEPTH copies are in flight (the reference copies
-        every one: reactive_load, moe_layer.py:601)."""
+        every one: reactive_load, moe_layer.py:601).
+
+        The routing, the hidden states and the host half travel through a
+        mapped pinned buffer that kernels on the compute stream read and
+        write (moe355_copy_to_host / moe355_merge_host_f32): copies through
+        the DMA engines would wait behind the expert copies in flight."""
         cache = self._cache
         T, K = ids.shape
-        ids_host = ids.reshape(-1).tolist()  # waits for the router: x is ready too
-        w_host = w.reshape(-1).tolist()
+        H = self.hidden_size
+        dev = xd.device
+        stream = _capi.stream_handle(dev)
+        ids32 = (ids if ids.dtype == torch.int32 else ids.int()).contiguous()
+        w32 = w.contiguous()
+        esz = xd.element_size()
+
+        def up(n: int) -> int:
+            return (n + 255) & ~255
+
+        o_w = up(T * K * 4)
+        o_x = o_w + up(T * K * 4)
+        o_out = o_x + up(T * H * esz)
+        stg = _capi.staging(dev, stream) if o_out + T * H * 4 <= _capi.HostStaging.CAPACITY \
+            else None
+        if stg is not None:
+            _capi.copy_to_host(stg.ptr, ids32, T * K * 4, stream)
+            _capi.copy_to_host(stg.ptr + o_w, w32, T * K * 4, stream)
+            _capi.copy_to_host(stg.ptr + o_x, xd, T * H * esz, stream)
+            done = torch.cuda.Event()
+            done.record(torch.cuda.current_stream(dev))
+            done.synchronize()
+            ids_host = stg.array(0, np.int32, T * K).tolist()
+            w_host = stg.array(o_w, np.float32, T * K).tolist()
+        else:
+            ids_host = ids32.reshape(-1).tolist()  # waits for the router: x is ready too
+            w_host = w32.reshape(-1).tolist()
         if env.get_chunk_size(0) > 0:
             run = sorted({i for i in ids_host if i >= 0})
         else:
             run = self._kept_experts(ids_host, w_host)
         w1s, w2s, local_index, host_ids = cache.split_slots(run)
-        x_host = xd.cpu() if host_ids else None
-        acc = torch.zeros((T, self.hidden_size), dtype=torch.float32, device=xd.device)
+        acc = torch.zeros((T, H), dtype=torch.float32, device=dev)
         expert_map = [-1] * self.num_experts
         for g, loc in local_index.items():
             expert_map[g] = loc
@@ -511,6 +542,8 @@ class FusedMoE(BaseOP):
             self._experts(xd, w, ids, act, [t.data_ptr() for t in w1s],
                           [t.data_ptr() for t in w2s], expert_map=expert_map, out=acc,
                           accumulate_f32=True)
+            cache.mark_read(local_index)
+        out = torch.empty((T, H), dtype=xd.dtype, device=dev)
         if host_ids:
             offs, toks, wts = [0], [], []
             for e in host_ids:
@@ -519,23 +552,34 @@ class FusedMoE(BaseOP):
                         toks.append(j // K)
                         wts.append(w_host[j])
                 offs.append(len(toks))
-            host_out = torch.zeros((T, self.hidden_size), dtype=torch.float32,
-                                   pin_memory=cache._pinned)
+            if stg is not None:
+                x_host = torch.from_numpy(stg.array(o_x, np.uint16, T * H)).view(
+                    xd.dtype).reshape(T, H) if esz == 2 else \
+                    torch.from_numpy(stg.array(o_x, np.float32, T * H)).reshape(T, H)
+                host_out = torch.from_numpy(stg.array(o_out, np.float32, T * H)).reshape(T, H)
+                host_out.zero_()
+            else:
+                x_host = xd.cpu()
+                host_out = torch.zeros((T, H), dtype=torch.float32, pin_memory=cache._pinned)
             _capi.host_experts(x_host, [cache._host[e][0] for e in host_ids],
                                [cache._host[e][1] for e in host_ids],
                                np.asarray(offs, np.int32), np.asarray(toks or [0], np.int32),
                                np.asarray(wts or [0.0], np.float32), act, host_out)
-            acc.add_(host_out.to(xd.device, non_blocking=cache._pinned))
+            if stg is not None:
+                _capi.merge_host_f32(acc, stg.ptr + o_out, out, stream)
+            else:
+                acc.add_(host_out.to(dev, non_blocking=cache._pinned))
+                _capi.cast_f32(acc, out)
             cache.stats.host_experts += len(host_ids)
             cache.load_while_idle(host_ids, env.get_moe_split_copy_depth())
+        else:
+            _capi.cast_f32(acc, out)
         if self._predictor is not None:
             ran = set(run)
             fallback = min(run) if run else -1  # the first kept id, as in _forward_offload
             routed = [i if i in ran else fallback for i in ids_host]
             self._predictor.record_step(routed, is_prefill=(M > 1),
                                         forward_ms=self._since_last_step_ms())
-        out = torch.empty((T, self.hidden_size), dtype=xd.dtype, device=xd.device)
-        _capi.cast_f32(acc, out)
         return out
 
     def _forward_streaming(self, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
@@ -559,6 +603,7 @@ class FusedMoE(BaseOP):
             self._experts(xd, w, ids, act, [t.data_ptr() for t in w1s],
                           [t.data_ptr() for t in w2s], expert_map=expert_map, out=acc,
                           accumulate_f32=True, with_shared=(n == 0))
+            cache.mark_read(local_index)
         out = torch.empty((xd.shape[0], self.hidden_size), dtype=xd.dtype, device=xd.device)
         _capi.cast_f32(acc, out)
         return out

@@ -185,11 +185,23 @@ class _HostPool:
     holder itself is dropped, i.e. when the last cache reading it lets go or
     replaces it)."""
 
-    __slots__ = ("buf", "_last")
+    __slots__ = ("buf", "_last", "touched")
 
     def __init__(self, buf: torch.Tensor) -> None:
         self.buf = buf
         self._last: Dict[int, object] = {}  # copy stream handle -> last copy event
+        self.touched = False  # every page read once by the host (see touch_pages)
+
+    def touch_pages(self) -> None:
+        """Read one element of every 4 KiB page from the host. The driver
+        maps pinned pages into the process on first access, so without this
+        the first host computation of each expert pays a page fault per page
+        (~20 ms for a Mixtral expert)."""
+        if self.touched:
+            return
+        step = max(1, 4096 // self.buf.element_size())
+        self.buf[::step].float().sum()
+        self.touched = True
 
     def note_copy(self, stream_key: int, event) -> None:
         self._last[stream_key] = event  # stream order: it covers the earlier copies
@@ -210,7 +222,8 @@ class _HostPool:
 class _Slot:
     """One HBM buffer holding an expert's w1 then w2, plus its stream events."""
 
-    __slots__ = ("buf", "w1", "w2", "ready", "last_copy", "free_after", "refs")
+    __slots__ = ("buf", "w1", "w2", "ready", "last_copy", "free_after", "refs", "reads",
+                 "handed")
 
     def __init__(self, buf: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor) -> None:
         self.buf = buf
@@ -221,7 +234,13 @@ class _Slot:
         # before anything read it may still be filling on one layer's copy
         # stream when another layer's copy stream takes it.
         self.last_copy: Optional[torch.cuda.Event] = None
-        self.free_after: Optional[torch.cuda.Event] = None  # last reader finished
+        # Events the next copy into the slot waits for: its readers finished.
+        self.free_after: List[torch.cuda.Event] = []
+        # Readers marked by mark_read (one event per compute stream), and
+        # whether the slot was handed out since the last mark: an unmarked
+        # hand-out makes the release wait for everything queued.
+        self.reads: Dict[int, torch.cuda.Event] = {}
+        self.handed = False
         self.refs = 0
 
 
@@ -584,9 +603,36 @@ class ExpertOffloadCache:
         still filling them."""
         uniq = self._admit(indices)
         self._wait_ready(uniq)
+        self._hand_out(uniq)
         w1 = [self._lru[i][0] for i in uniq]
         w2 = [self._lru[i][1] for i in uniq]
         return w1, w2, {idx: k for k, idx in enumerate(uniq)}
+
+    def _hand_out(self, ids: Sequence[int]) -> None:
+        for i in ids:
+            slot = self._slot_of.get(i)
+            if slot is not None:
+                slot.handed = True
+
+    def mark_read(self, ids: Sequence[int]) -> None:
+        """Record that every kernel reading the slots of ``ids`` (views
+        handed out by prefetch_slots / split_slots) is queued on the current
+        stream: a later copy into one of these slots then waits only for an
+        event recorded here, not for everything queued at its eviction. A
+        caller that never marks keeps that conservative wait."""
+        if self.device.type != "cuda":
+            return
+        stream = torch.cuda.current_stream(self.device)
+        ev = None
+        for i in ids:
+            slot = self._slot_of.get(int(i))
+            if slot is None:
+                continue
+            if ev is None:
+                ev = torch.cuda.Event()
+                ev.record(stream)
+            slot.reads[int(stream.cuda_stream)] = ev
+            slot.handed = False
 
     def split_prefetch(self, indices: Sequence[int]):
         """Split the routed set by residency: stacked banks of the hits and the
@@ -614,6 +660,8 @@ class ExpertOffloadCache:
         if not self._host:
             return
         _capi.host_lib()  # a missing host library fails here, not mid-forward
+        if self._host_pool is not None:
+            self._host_pool.touch_pages()
         self._cpu_split = True
 
     def split_slots(self, indices: Sequence[int]):
@@ -637,6 +685,7 @@ class ExpertOffloadCache:
             else:
                 host_ids.append(i)
         self._wait_ready(dev_ids)
+        self._hand_out(dev_ids)
         w1 = [self._lru[i][0] for i in dev_ids]
         w2 = [self._lru[i][1] for i in dev_ids]
         return w1, w2, {idx: k for k, idx in enumerate(dev_ids)}, host_ids
@@ -764,16 +813,20 @@ class ExpertOffloadCache:
     def _release(self, slot: _Slot) -> None:
         """Return a slot to the free list once its last holder lets go. Its
         next copy (``_fill``, possibly on another layer's copy stream) waits
-        for ``free_after`` (every kernel queued so far on the compute stream,
-        the slot's readers among them) and for ``last_copy`` (the copy that
-        filled it, which nothing may have waited for if the slot was evicted
-        unread)."""
+        for ``free_after`` (the events of its marked readers; if the slot was
+        handed out since the last ``mark_read``, every kernel queued so far on
+        the compute stream) and for ``last_copy`` (the copy that filled it,
+        which nothing may have waited for if the slot was evicted unread)."""
         slot.refs -= 1
         if slot.refs > 0:
             return
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.device))
-        slot.free_after = ev
+        if slot.handed:
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))
+            slot.reads[int(torch.cuda.current_stream(self.device).cuda_stream)] = ev
+        slot.free_after = list(slot.reads.values())
+        slot.reads = {}
+        slot.handed = False
         slot.ready = None
         if self._pool is not None:
             self._pool.release(slot)
@@ -802,8 +855,8 @@ class ExpertOffloadCache:
         if self.device.type == "cuda":
             slot = self._acquire_slot()
             cs = self._side_stream()
-            if slot.free_after is not None:
-                cs.wait_event(slot.free_after)
+            for ev_ in slot.free_after:
+                cs.wait_event(ev_)
             if slot.last_copy is not None:
                 cs.wait_event(slot.last_copy)
             src = self._host_buf.data_ptr() + self._host_off[idx] * self._host_buf.element_size()
@@ -902,6 +955,7 @@ class ExpertOffloadCache:
         self._wait_ready(uniq)
         w1 = torch.stack([self._lru[i][0] for i in uniq], dim=0)
         w2 = torch.stack([self._lru[i][1] for i in uniq], dim=0)
+        self.mark_read(uniq)  # the stacking copies are the slots' readers
         return w1, w2, local_index
 
     # ------------------------------------------------------------------- stats

@@ -128,6 +128,19 @@ def test_entry_points_reject_null_arguments_without_launching():
                                     _capi.BF16, 0, None, 0, None, 0, None) == -3
 
 
+def test_staging_entry_points_reject_bad_arguments_before_any_hip_call():
+    lib = _capi.lib()
+    assert lib.moe355_copy_to_host(None, None, 0, None) == 0
+    assert lib.moe355_copy_to_host(None, None, 64, None) == -1
+    assert lib.moe355_copy_to_host(0x1008, 0x2000, 64, None) == -1  # host_dst not 16-byte aligned
+    assert "aligned" in lib.moe355_last_error().decode()
+    assert lib.moe355_merge_host_f32(0x1000, 0x2000, 6, _capi.BF16, 0x3000, None) == -1
+    assert "multiple of 4" in lib.moe355_last_error().decode()
+    assert lib.moe355_merge_host_f32(0x1000, 0x2000, 8, 7, 0x3000, None) == -1
+    assert lib.moe355_host_staging_alloc(16, None) == -1
+    assert lib.moe355_host_staging_free(None) == 0
+
+
 def test_zero_tokens_is_a_no_op():
     lib = _capi.lib()
     assert lib.moe355_router_topk(None, None, None, 0, 64, 8, 2, _capi.BF16, 1, 0, 0, None, None,
