@@ -13,8 +13,9 @@
 // every weight row is read once from host memory and multiplied against all
 // of an expert's token rows, which stay in L1/L2. Rows are split over the
 // OpenMP threads in fixed blocks, so results do not depend on the thread
-// count. AVX-512F is used where the CPU has it (checked at run time), AVX2 +
-// FMA otherwise; both convert bf16/f16 to fp32 exactly before the FMAs.
+// count. For bf16 weights on a CPU with AVX512-BF16, vdpbf16ps multiplies bf16
+// pairs (exact products) into fp32 sums; otherwise AVX-512F or AVX2 + FMA
+// convert bf16/f16 to fp32 exactly before the FMAs (checked at run time).
 
 #include <immintrin.h>
 #include <omp.h>
@@ -178,6 +179,62 @@ void dot_rows_avx512(const float* a, int lda, int m, int n, const void* w, int d
   }
 }
 
+// bf16 weights against bf16 token rows with vdpbf16ps: each instruction
+// multiplies 32 bf16 pairs (products exact in fp32) and adds them to 16 fp32
+// sums, half the instructions of convert + FMA per weight. The intermediate
+// is already rounded to bf16, so the token rows lose nothing.
+template <int MT>
+__attribute__((target("avx512f,avx512bw,avx512bf16")))
+void dot_block_bf16dp(const uint16_t* a, int lda, int n, const uint16_t* w, int r0, int r1,
+                      float* out, int ldo) {
+  float part[16][MT];
+  for (int r = 0; r < r1 - r0; ++r)
+    for (int t = 0; t < MT; ++t) part[r][t] = 0.0f;
+  for (int kb = 0; kb < n; kb += kKBlock) {
+    const int ke = (kb + kKBlock) < n ? (kb + kKBlock) : n;
+    const int kv = kb + ((ke - kb) & ~31);
+    for (int r = r0; r < r1; ++r) {
+      const size_t row = static_cast<size_t>(r) * n;
+      prefetch_next_block<MOE355_HOST_BF16>(w, row, ke, n);
+      __m512 acc[MT];
+      for (int t = 0; t < MT; ++t) acc[t] = _mm512_setzero_ps();
+      for (int k = kb; k < kv; k += 32) {
+        const __m512bh wv = (__m512bh)_mm512_loadu_si512(w + row + k);
+        for (int t = 0; t < MT; ++t)
+          acc[t] = _mm512_dpbf16_ps(acc[t], wv,
+                                    (__m512bh)_mm512_loadu_si512(a + (size_t)t * lda + k));
+      }
+      for (int t = 0; t < MT; ++t) {
+        float s = _mm512_reduce_add_ps(acc[t]);
+        for (int k = kv; k < ke; ++k)
+          s += bf16_to_f32(w[row + k]) * bf16_to_f32(a[(size_t)t * lda + k]);
+        part[r - r0][t] += s;
+      }
+    }
+  }
+  for (int r = r0; r < r1; ++r)
+    for (int t = 0; t < MT; ++t) out[(size_t)t * ldo + r] = part[r - r0][t];
+}
+
+__attribute__((target("avx512f,avx512bw,avx512bf16")))
+void dot_rows_bf16dp(const uint16_t* a, int lda, int m, int n, const uint16_t* w, int r0, int r1,
+                     float* out, int ldo) {
+  for (int t0 = 0; t0 < m; t0 += kMaxTok) {
+    const uint16_t* at = a + (size_t)t0 * lda;
+    float* ot = out + (size_t)t0 * ldo;
+    switch ((m - t0) < kMaxTok ? (m - t0) : kMaxTok) {
+      case 1: dot_block_bf16dp<1>(at, lda, n, w, r0, r1, ot, ldo); break;
+      case 2: dot_block_bf16dp<2>(at, lda, n, w, r0, r1, ot, ldo); break;
+      case 3: dot_block_bf16dp<3>(at, lda, n, w, r0, r1, ot, ldo); break;
+      case 4: dot_block_bf16dp<4>(at, lda, n, w, r0, r1, ot, ldo); break;
+      case 5: dot_block_bf16dp<5>(at, lda, n, w, r0, r1, ot, ldo); break;
+      case 6: dot_block_bf16dp<6>(at, lda, n, w, r0, r1, ot, ldo); break;
+      case 7: dot_block_bf16dp<7>(at, lda, n, w, r0, r1, ot, ldo); break;
+      default: dot_block_bf16dp<8>(at, lda, n, w, r0, r1, ot, ldo); break;
+    }
+  }
+}
+
 template <int DT>
 __attribute__((target("avx2,fma,f16c")))
 inline __m256 load8_avx2(const void* w, size_t i) {
@@ -266,11 +323,9 @@ bool have_avx512() {
   return ok;
 }
 
-// MOE355_HOST_NO_AVX512=1 keeps the AVX2 path on an AVX-512 host (read per
-// call, so one process can compare both paths).
-bool use_avx512() {
-  const char* e = std::getenv("MOE355_HOST_NO_AVX512");
-  return have_avx512() && !(e && e[0] == '1');
+bool have_avx512bf16() {
+  static const bool ok = have_avx512() && __builtin_cpu_supports("avx512bf16");
+  return ok;
 }
 
 bool have_avx2() {
@@ -279,18 +334,35 @@ bool have_avx2() {
   return ok;
 }
 
+// Instruction set used: the best the CPU has, capped by MOE355_HOST_ISA
+// (avx2 | avx512 | avx512bf16; read per call, so one process can compare the
+// paths).
+enum Isa { kAvx2 = 0, kAvx512 = 1, kAvx512Bf16 = 2 };
+
+Isa isa() {
+  Isa best = have_avx512bf16() ? kAvx512Bf16 : (have_avx512() ? kAvx512 : kAvx2);
+  const char* e = std::getenv("MOE355_HOST_ISA");
+  if (e && std::strcmp(e, "avx2") == 0) return kAvx2;
+  if (e && std::strcmp(e, "avx512") == 0 && best > kAvx512) return kAvx512;
+  return best;
+}
+
 // Rows of W split in blocks of kRowBlock over the threads (static schedule).
 constexpr int kRowBlock = 16;
 
-void dot_rows(const float* a, int lda, int m, int n, const void* w, int dtype, int rows,
-              float* out, int ldo, int n_threads) {
+// a: the token rows in fp32 (lda floats apart); a16: the same rows as bf16
+// bits (lda16 elements apart), used by the vdpbf16ps path for bf16 weights.
+void dot_rows(const float* a, int lda, const uint16_t* a16, int lda16, int m, int n,
+              const void* w, int dtype, int rows, float* out, int ldo, int n_threads, Isa use) {
   const int blocks = (rows + kRowBlock - 1) / kRowBlock;
-  const bool v512 = use_avx512();
+  const bool dp = use == kAvx512Bf16 && dtype == MOE355_HOST_BF16;
 #pragma omp parallel for schedule(static) num_threads(n_threads)
   for (int b = 0; b < blocks; ++b) {
     const int r0 = b * kRowBlock;
     const int r1 = (r0 + kRowBlock) < rows ? (r0 + kRowBlock) : rows;
-    if (v512)
+    if (dp)
+      dot_rows_bf16dp(a16, lda16, m, n, static_cast<const uint16_t*>(w), r0, r1, out, ldo);
+    else if (use >= kAvx512)
       dot_rows_avx512(a, lda, m, n, w, dtype, r0, r1, out, ldo);
     else
       dot_rows_avx2(a, lda, m, n, w, dtype, r0, r1, out, ldo);
@@ -329,30 +401,50 @@ int moe355_host_experts(const void* x, int T, int H, int I, int dtype, int n_exp
     if (slot_tokens[s] < 0 || slot_tokens[s] >= T)
       return fail(MOE355_HOST_EINVAL, "slot token index out of range");
   if (n_threads <= 0) n_threads = omp_get_max_threads();
+  const Isa use = isa();
+  const bool dp = use == kAvx512Bf16 && dtype == MOE355_HOST_BF16;
 
   std::vector<float> xa, gu, inter, y;
+  std::vector<uint16_t> xa16, inter16;
   for (int e = 0; e < n_experts; ++e) {
     const int s0 = slot_offsets[e], m = slot_offsets[e + 1] - s0;
     if (m == 0) continue;
     // token rows padded by 64 bytes: rows n*4 bytes apart (n a multiple of
     // 1024, as H and I usually are) would all fall in the same L1 sets
-    const int ldx = H + 16, ldi = I + 16;
-    xa.assign(static_cast<size_t>(m) * ldx, 0.0f);
-    for (int j = 0; j < m; ++j) {
-      const size_t src = static_cast<size_t>(slot_tokens[s0 + j]) * H;
-      for (int h = 0; h < H; ++h) xa[(size_t)j * ldx + h] = load_w(x, src + h, dtype);
+    const int ldx = H + 16, ldi = I + 16, ldx16 = H + 32, ldi16 = I + 32;
+    if (dp) {
+      xa16.assign(static_cast<size_t>(m) * ldx16, 0);
+      for (int j = 0; j < m; ++j)
+        std::memcpy(&xa16[(size_t)j * ldx16],
+                    static_cast<const uint16_t*>(x) + static_cast<size_t>(slot_tokens[s0 + j]) * H,
+                    sizeof(uint16_t) * H);
+    } else {
+      xa.assign(static_cast<size_t>(m) * ldx, 0.0f);
+      for (int j = 0; j < m; ++j) {
+        const size_t src = static_cast<size_t>(slot_tokens[s0 + j]) * H;
+        for (int h = 0; h < H; ++h) xa[(size_t)j * ldx + h] = load_w(x, src + h, dtype);
+      }
     }
     // gate|up: [m, 2I], gate rows first
     gu.assign(static_cast<size_t>(m) * 2 * I, 0.0f);
-    dot_rows(xa.data(), ldx, m, H, w1[e], dtype, 2 * I, gu.data(), 2 * I, n_threads);
-    inter.assign(static_cast<size_t>(m) * ldi, 0.0f);
+    dot_rows(xa.data(), ldx, xa16.data(), ldx16, m, H, w1[e], dtype, 2 * I, gu.data(), 2 * I,
+             n_threads, use);
+    if (dp)
+      inter16.assign(static_cast<size_t>(m) * ldi16, 0);
+    else
+      inter.assign(static_cast<size_t>(m) * ldi, 0.0f);
     for (int j = 0; j < m; ++j)
-      for (int i = 0; i < I; ++i)
-        inter[(size_t)j * ldi + i] = round_to_type(
-            act_mul(act, gu[(size_t)j * 2 * I + i], gu[(size_t)j * 2 * I + I + i]), dtype);
+      for (int i = 0; i < I; ++i) {
+        const float v = act_mul(act, gu[(size_t)j * 2 * I + i], gu[(size_t)j * 2 * I + I + i]);
+        if (dp)
+          inter16[(size_t)j * ldi16 + i] = f32_to_bf16(v);
+        else
+          inter[(size_t)j * ldi + i] = round_to_type(v, dtype);
+      }
     // down: [m, H]
     y.assign(static_cast<size_t>(m) * H, 0.0f);
-    dot_rows(inter.data(), ldi, m, I, w2[e], dtype, H, y.data(), H, n_threads);
+    dot_rows(inter.data(), ldi, inter16.data(), ldi16, m, I, w2[e], dtype, H, y.data(), H,
+             n_threads, use);
     for (int j = 0; j < m; ++j) {
       float* o = out + static_cast<size_t>(slot_tokens[s0 + j]) * H;
       const float wt = slot_weights[s0 + j];

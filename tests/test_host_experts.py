@@ -50,14 +50,14 @@ def _case(T, H, I, E, K, dt, seed):
     return x, w1, w2, ids, w
 
 
-@pytest.mark.parametrize("no_avx512", ["0", "1"])
+@pytest.mark.parametrize("isa", ["avx2", "avx512", "avx512bf16"])
 @pytest.mark.parametrize("dt,H,I,act", [
     (torch.bfloat16, 256, 384, 0), (torch.bfloat16, 200, 136, 1), (torch.float16, 512, 256, 2),
     (torch.float32, 192, 160, 0), (torch.bfloat16, 64, 40, 0)])
-def test_host_experts_match_oracle(dt, H, I, act, no_avx512, monkeypatch):
+def test_host_experts_match_oracle(dt, H, I, act, isa, monkeypatch):
     """Random routing over 5 experts, 3 of them run on the host (the others
     marked -1 for the oracle), tails of 8/16-wide vectors included."""
-    monkeypatch.setenv("MOE355_HOST_NO_AVX512", no_avx512)
+    monkeypatch.setenv("MOE355_HOST_ISA", isa)
     T, E, K = 11, 5, 2
     x, w1, w2, ids, w = _case(T, H, I, E, K, dt, seed=H + I)
     host = [3, 0, 4]
