@@ -1,0 +1,103 @@
+"""GPU parity of the CPU/GPU split forward beyond the Mixtral-shape decode of
+test_gpu_offload_mixtral.py: other dtypes, shared experts, every routed
+expert (RE_CHUNK_SIZE), and token counts past the zero-copy staging buffer
+(the layer then moves routing, hidden states and the host half with ordinary
+copies).
+
+Reference: FusedMoE._forward_split (reframework/moe/moe_layer.py:523-627),
+with the experts the offload forward would run (RE_MAX_PACK truncation or
+every routed expert), each slot's output on its own token. Every step's
+output is checked against the fp64 oracle with the dropped slots removed:
+<= 2e-2 max-relative for bf16/f16, <= 1e-5 for fp32. The layer's 2-slot
+window guarantees that some experts of every step run on the host and some,
+resident from earlier steps, on the GPU.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import banner
+from _offload_replay import truncated_request
+from oracle import oracle
+from reframework_amd import _capi, synth
+from reframework_amd.moe import FusedMoE
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def _layer(E, K, H, I, dtype, seed, n_shared=0):
+    moe = FusedMoE(num_experts=E, top_k=K, hidden_size=H, intermediate_size=I, dtype=dtype,
+                   n_shared_experts=n_shared)
+    layer = synth.make_layer(synth.MoEShape("t", H, E, K, I), dtype, seed=seed, sigma_w=0.02)
+    sd = {"gate.weight": (layer["gate"].double() * 10.0).to(dtype)}
+    for e in range(E):
+        sd[f"experts.{e}.gate_proj.weight"] = layer["w1"][e][:I]
+        sd[f"experts.{e}.up_proj.weight"] = layer["w1"][e][I:]
+        sd[f"experts.{e}.down_proj.weight"] = layer["w2"][e]
+    sh = None
+    if n_shared:
+        sh = synth.make_shared(1, H, n_shared * I, dtype, seed=seed)
+        sd["shared_experts.gate_proj.weight"] = sh["gate_proj"]
+        sd["shared_experts.up_proj.weight"] = sh["up_proj"]
+        sd["shared_experts.down_proj.weight"] = sh["down_proj"]
+    moe.load_state_dict(sd)
+    return moe, layer, sh
+
+
+@pytest.mark.parametrize("dtype,T,H,I,exact,n_shared", [
+    (torch.bfloat16, 8, 512, 512, False, 0),
+    (torch.float16, 5, 512, 768, False, 0),
+    (torch.float32, 6, 256, 512, False, 0),
+    (torch.bfloat16, 8, 512, 512, True, 0),
+    (torch.bfloat16, 4, 512, 256, False, 2),
+    # past the 8 MB staging buffer at this width: ordinary copies
+    (torch.bfloat16, 3000, 512, 256, False, 0),
+])
+def test_split_forward_matches_oracle(dtype, T, H, I, exact, n_shared, dev, monkeypatch):
+    E, K = 8, 2
+    monkeypatch.setenv("RE_MAX_PACK", "2")
+    if exact:
+        monkeypatch.setenv("RE_CHUNK_SIZE", "8")
+    else:
+        monkeypatch.delenv("RE_CHUNK_SIZE", raising=False)
+    staged = T * (H * (4 + torch.tensor([], dtype=dtype).element_size()) + 2 * K * 4) + 4096 \
+        <= _capi.HostStaging.CAPACITY
+    banner(f"split forward {dtype} T={T} H={H} I={I} exact={exact} shared={n_shared} "
+           f"staged={staged}")
+    moe, layer, sh = _layer(E, K, H, I, dtype, seed=T + H, n_shared=n_shared)
+    moe.gate.data = moe.gate.data.to(dev)
+    for p in list(moe.shared_w1) + list(moe.shared_w2):
+        p.data = p.data.to(dev)
+    cache = moe.build_offload_cache(dev, lru_capacity=2)
+    moe.enable_cpu_split()
+    assert moe.cpu_split
+    outs, xs, routes = [], [], []
+    for step in range(5):
+        x = synth.make_tokens(T, H, dtype, seed=100 + step).to(dev)
+        xs.append(x)
+        routes.append(moe.route(x))
+        outs.append(moe(x))
+    torch.cuda.synchronize()
+    st = cache.stats
+    print(f"  {st.hits} experts on the GPU, {st.host_experts} on the host, {st.misses} copied",
+          flush=True)
+    assert st.host_experts > 0 and st.hits > 0
+    assert cache._n_slots <= 2 or exact
+    for step in range(5):
+        wn, idn = (t.cpu().numpy() for t in routes[step])
+        if not exact:
+            kept = truncated_request(idn, wn, 2)
+            idn = np.where(np.isin(idn, kept), idn, -1)
+        x = xs[step].cpu()
+        ref = oracle.fused_experts(x, layer["w1"], layer["w2"], wn, idn)
+        if n_shared:
+            ref = ref + oracle.fused_experts(x, sh["w1"], sh["w2"], np.ones((T, 1), np.float32),
+                                             np.zeros((T, 1), np.int64))
+        err = oracle.max_rel(outs[step].float().cpu().numpy(), ref)
+        print(f"  step {step}: max_rel {err:.2e}", flush=True)
+        assert err <= TOL[dtype]
