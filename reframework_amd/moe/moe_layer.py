@@ -450,8 +450,7 @@ class FusedMoE(BaseOP):
     def _forward_offload(self, M: int, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
                          act: int) -> torch.Tensor:
         cache = self._cache
-        ids_host = ids.reshape(-1).tolist()
-        w_host = w.reshape(-1).tolist()
+        ids_host, w_host, _ = self._routing_to_host(ids, w)
         kept = self._kept_experts(ids_host, w_host)
         w1s, w2s, local_index = cache.prefetch_slots(kept)
         # Dropped slots contribute nothing; in the routed set recorded for the
@@ -471,6 +470,45 @@ class FusedMoE(BaseOP):
         out = self._experts(xd, w, ids, act, w1p, w2p, expert_map=expert_map)
         cache.mark_read(local_index)
         return out
+
+    @staticmethod
+    def _staged_layout(T: int, K: int, H: int, esz: int):
+        """Byte offsets of ids, weights, hidden states and the host-half
+        output in the staging buffer, and whether a step of this size fits."""
+        def up(n: int) -> int:
+            return (n + 255) & ~255
+        o_w = up(T * K * 4)
+        o_x = o_w + up(T * K * 4)
+        o_out = o_x + up(T * H * esz)
+        return o_w, o_x, o_out, o_out + T * H * 4 <= _capi.HostStaging.CAPACITY
+
+    def _routing_to_host(self, ids: torch.Tensor, w: torch.Tensor,
+                         xd: Optional[torch.Tensor] = None):
+        """(ids list, weights list, staging buffer or None) of a step, read
+        through the mapped staging buffer by a kernel on the compute stream
+        (with xd too, when given) when the step fits it, else with
+        synchronous copies. A copy through the DMA engines would wait behind
+        expert copies in flight (lookahead loads, the split's background
+        loads); the kernel does not."""
+        T, K = ids.shape
+        dev = ids.device
+        o_w, o_x, _, fits = self._staged_layout(T, K, self.hidden_size,
+                                                xd.element_size() if xd is not None else 2)
+        ids32 = (ids if ids.dtype == torch.int32 else ids.int()).contiguous()
+        w32 = w.contiguous()
+        if not fits:
+            return ids32.reshape(-1).tolist(), w32.reshape(-1).tolist(), None
+        stream = _capi.stream_handle(dev)
+        stg = _capi.staging(dev, stream)
+        _capi.copy_to_host(stg.ptr, ids32, T * K * 4, stream)
+        _capi.copy_to_host(stg.ptr + o_w, w32, T * K * 4, stream)
+        if xd is not None:
+            _capi.copy_to_host(stg.ptr + o_x, xd, xd.numel() * xd.element_size(), stream)
+        done = torch.cuda.Event()
+        done.record(torch.cuda.current_stream(dev))
+        done.synchronize()
+        return (stg.array(0, np.int32, T * K).tolist(), stg.array(o_w, np.float32, T * K).tolist(),
+                stg)
 
     @staticmethod
     def _kept_experts(ids_host: List[int], w_host: List[float]) -> List[int]:
@@ -505,30 +543,9 @@ class FusedMoE(BaseOP):
         H = self.hidden_size
         dev = xd.device
         stream = _capi.stream_handle(dev)
-        ids32 = (ids if ids.dtype == torch.int32 else ids.int()).contiguous()
-        w32 = w.contiguous()
         esz = xd.element_size()
-
-        def up(n: int) -> int:
-            return (n + 255) & ~255
-
-        o_w = up(T * K * 4)
-        o_x = o_w + up(T * K * 4)
-        o_out = o_x + up(T * H * esz)
-        stg = _capi.staging(dev, stream) if o_out + T * H * 4 <= _capi.HostStaging.CAPACITY \
-            else None
-        if stg is not None:
-            _capi.copy_to_host(stg.ptr, ids32, T * K * 4, stream)
-            _capi.copy_to_host(stg.ptr + o_w, w32, T * K * 4, stream)
-            _capi.copy_to_host(stg.ptr + o_x, xd, T * H * esz, stream)
-            done = torch.cuda.Event()
-            done.record(torch.cuda.current_stream(dev))
-            done.synchronize()
-            ids_host = stg.array(0, np.int32, T * K).tolist()
-            w_host = stg.array(o_w, np.float32, T * K).tolist()
-        else:
-            ids_host = ids32.reshape(-1).tolist()  # waits for the router: x is ready too
-            w_host = w32.reshape(-1).tolist()
+        _, o_x, o_out, _ = self._staged_layout(T, K, H, esz)
+        ids_host, w_host, stg = self._routing_to_host(ids, w, xd)
         if env.get_chunk_size(0) > 0:
             run = sorted({i for i in ids_host if i >= 0})
         else:
@@ -589,7 +606,8 @@ class FusedMoE(BaseOP):
         experts join the first chunk."""
         cache = self._cache
         chunk_size = env.get_chunk_size(8)
-        uniq = sorted({i for i in ids.reshape(-1).tolist() if i >= 0})
+        ids_host, _, _ = self._routing_to_host(ids, w)
+        uniq = sorted({i for i in ids_host if i >= 0})
         acc = torch.zeros((xd.shape[0], self.hidden_size), dtype=torch.float32, device=xd.device)
         starts = list(range(0, len(uniq), chunk_size)) or [0]
         for n, start in enumerate(starts):
