@@ -143,15 +143,21 @@ int moe355_add_rmsnorm(const void* x, const void* residual, void* residual_out,
 /*
  * moe355_add_rmsnorm followed by moe355_router_topk on the normed rows, in one
  * call on one stream: post_attention_layernorm.forward_add_residual + route
- * (reframework/models/base.py:135-136, moe/moe_layer.py:320-344).
+ * (reframework/models/base.py:135-136, moe/moe_layer.py:320-344). For bf16/f16
+ * with H <= 8192 (a multiple of 8), T * E <= 8192 and E <= 16 (E <= 64 when
+ * logits_out is NULL) one kernel does both: the normed rows (written to
+ * normed_out, bit for bit moe355_add_rmsnorm's) stay in registers for the
+ * router's dot products. The router's fp32 sums then run in another order than
+ * moe355_router_topk's, so a logit may round to the neighbouring bf16/f16 value.
+ * logits_out ([T,E] fp32, the logits top-k ranked) may be NULL.
  */
 int moe355_add_rmsnorm_router_topk(const void* x, const void* residual, void* residual_out,
                                    const void* norm_weight, const void* norm_bias,
                                    int weight_dtype, float eps,
                                    const void* gate, const float* router_bias, int T, int H, int E,
                                    int K, int dtype, int renormalize, int round_logits,
-                                   void* normed_out, float* topk_w, int32_t* topk_ids,
-                                   void* stream);
+                                   void* normed_out, float* logits_out, float* topk_w,
+                                   int32_t* topk_ids, void* stream);
 
 /*
  * softmax -> top-k -> renormalise on given fp32 logits.

@@ -79,7 +79,7 @@ _SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "moe355_topk_from_logits": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "moe355_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _I, ctypes.c_float, _I, _I, _I, _P, _P]),
     "moe355_add_rmsnorm_router_topk": (_I, [_P, _P, _P, _P, _P, _I, ctypes.c_float, _P, _P, _I,
-                                            _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+                                            _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
     "moe355_make_plan": (_I, [_I, _I, _I, _I, _I, _I, _PPLAN]),
     "moe355_make_plan_path": (_I, [_I, _I, _I, _I, _I, _I, _I, _PPLAN]),
     "moe355_permute": (_I, [_PPLAN, _P, _I, _PI32, _I, _P, _P]),
@@ -286,7 +286,8 @@ def add_rmsnorm_router_topk(x: torch.Tensor, residual: Optional[torch.Tensor],
                             norm_bias: Optional[torch.Tensor], eps: float, gate: torch.Tensor,
                             router_bias: Optional[torch.Tensor], K: int, renormalize: bool,
                             round_logits: bool, normed_out: torch.Tensor, topk_w: torch.Tensor,
-                            topk_ids: torch.Tensor, stream: Optional[int] = None) -> None:
+                            topk_ids: torch.Tensor, stream: Optional[int] = None,
+                            logits_out: Optional[torch.Tensor] = None) -> None:
     T, H = x.shape
     E = gate.shape[0]
     s = stream if stream is not None else stream_handle(x.device)
@@ -294,7 +295,7 @@ def add_rmsnorm_router_topk(x: torch.Tensor, residual: Optional[torch.Tensor],
         _ptr(x), _ptr(residual), _ptr(residual_out), _ptr(norm_weight), _ptr(norm_bias),
         dtype_code(norm_weight.dtype), float(eps), _ptr(gate), _ptr(router_bias), T, H, E, K,
         dtype_code(x.dtype), int(renormalize), int(round_logits), _ptr(normed_out),
-        _ptr(topk_w), _ptr(topk_ids), s))
+        _ptr(logits_out), _ptr(topk_w), _ptr(topk_ids), s))
 
 
 def permute(plan: Plan, topk_ids: torch.Tensor, workspace: torch.Tensor,

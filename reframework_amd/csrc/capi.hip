@@ -299,13 +299,41 @@ int moe355_add_rmsnorm_router_topk(const void* x, const void* residual, void* re
                                    int weight_dtype, float eps,
                                    const void* gate, const float* router_bias, int T, int H, int E,
                                    int K, int dtype, int renormalize, int round_logits,
-                                   void* normed_out, float* topk_w, int32_t* topk_ids,
-                                   void* stream) {
-  int rc = moe355_add_rmsnorm(x, residual, residual_out, norm_weight, norm_bias, weight_dtype, eps,
-                              T, H, dtype, normed_out, stream);
-  if (rc) return rc;
-  return moe355_router_topk(normed_out, gate, router_bias, T, H, E, K, dtype, renormalize,
-                            round_logits, 0, nullptr, topk_w, topk_ids, stream);
+                                   void* normed_out, float* logits_out, float* topk_w,
+                                   int32_t* topk_ids, void* stream) {
+  if (!norm_router_fusable(T, H, E, dtype, logits_out != nullptr)) {
+    int rc = moe355_add_rmsnorm(x, residual, residual_out, norm_weight, norm_bias, weight_dtype,
+                                eps, T, H, dtype, normed_out, stream);
+    if (rc) return rc;
+    return moe355_router_topk_ld(normed_out, gate, router_bias, T, H, E, K, dtype, renormalize,
+                                 round_logits, 0, logits_out, topk_w, topk_ids, K, stream);
+  }
+  // The arguments both halves would check, then one launch.
+  if (T < 0 || H <= 0) return fail(MOE355_EINVAL, "bad sizes T=%d H=%d", T, H);
+  if (!valid_dtype(weight_dtype)) return fail(MOE355_EINVAL, "unknown weight dtype %d", weight_dtype);
+  if (K < 1 || K > E) return fail(MOE355_EINVAL, "top-k K=%d outside [1, E=%d]", K, E);
+  if (!(eps >= 0.0f)) return fail(MOE355_EINVAL, "eps must be >= 0");
+  if (T == 0) return MOE355_OK;
+  if (!x || !norm_weight || !normed_out || !gate || !topk_w || !topk_ids)
+    return fail(MOE355_EINVAL, "NULL tensor argument");
+  if (residual && !residual_out) return fail(MOE355_EINVAL, "residual given without residual_out");
+  if (!aligned16(x) || !aligned16(normed_out) || (residual && !aligned16(residual)) ||
+      (residual && !aligned16(residual_out)) || !aligned16(gate))
+    return fail(MOE355_EINVAL, "x/residual/out/gate not 16-byte aligned");
+  if (!aligned16(norm_weight) || (norm_bias && !aligned16(norm_bias)))
+    return fail(MOE355_EINVAL, "norm weight/bias not 16-byte aligned");
+  NormArgs na{};
+  na.x = x; na.residual = residual; na.residual_out = residual_out; na.weight = norm_weight;
+  na.bias = norm_bias; na.out = normed_out;
+  na.T = T; na.H = H; na.weight_dtype = weight_dtype; na.eps = eps;
+  RouterArgs ra{};
+  ra.x = normed_out; ra.gate = gate; ra.bias = router_bias; ra.logits_out = logits_out;
+  ra.topk_w = topk_w; ra.topk_ids = topk_ids;
+  ra.T = T; ra.H = H; ra.E = E; ra.K = K;
+  ra.renormalize = renormalize != 0; ra.round_logits = round_logits != 0;
+  ra.entropy_k_min = 0; ra.out_ld = K;
+  return check_hip(launch_add_rmsnorm_router(na, ra, dtype, as_stream(stream)),
+                   "add_rmsnorm_router launch");
 }
 
 int moe355_topk_from_logits(const float* logits, int T, int E, int K, int renormalize,

@@ -281,6 +281,13 @@ hipError_t launch_down_skinny(const FfnArgs& a, int dtype, hipStream_t s);
 hipError_t launch_gate_up_simt(const FfnArgs& a, int dtype, hipStream_t s);
 hipError_t launch_down_simt(const FfnArgs& a, int dtype, hipStream_t s);
 hipError_t launch_combine(const CombineArgs& a, int out_dtype, hipStream_t s);
+// Fused residual add + RMSNorm + router (norm.hip): 16-bit types, E <= 64,
+// H a multiple of 8 up to 8192, T * E <= 8192, and E <= 16 where a logits
+// buffer lets the split router run instead.
+constexpr int kMaxRouterExperts = 64;
+bool norm_router_fusable(int T, int H, int E, int dtype, bool has_logits);
+hipError_t launch_add_rmsnorm_router(const NormArgs& a, const RouterArgs& ra, int dtype,
+                                     hipStream_t s);
 hipError_t launch_cast_f32(const float* src, void* dst, size_t n, int dtype, hipStream_t s);
 hipError_t launch_copy_bytes(const void* src, void* dst, size_t n, hipStream_t s);
 hipError_t launch_merge_host(const float* acc, const float* host, void* out, size_t n, int dtype,

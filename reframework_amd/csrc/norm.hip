@@ -10,12 +10,15 @@
 // scaling, so the row is read once and each output written once: HBM bound,
 // 2 * H * elem bytes read and 2 * H * elem written per row (1 + 1 without the
 // residual add).
+#include <climits>
+
 #include "common.h"
 
 namespace moe355 {
 namespace {
 
 constexpr int kThreads = 256;
+#include "topk_wave.h"
 constexpr int kMaxChunks = 8;  // 16-byte chunks per thread: H <= 8 * 256 * (16 / elem)
 
 template <typename T>
@@ -156,6 +159,246 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(const NormArgs a)
   }
 }
 
+// Residual add + RMSNorm + router on TB rows per workgroup, 16-bit storage
+// types: the decoder step before the MoE (reframework/models/base.py:135-136)
+// in one launch. The norm is add_rmsnorm_kernel's arithmetic with the same
+// per-thread chunks and reduction order, so residual_out and normed are bit
+// for bit that kernel's. The normed rows then stay in registers, rounded to T
+// as the reference stores them, for the router's dot products with the gate:
+// fp32 sums over this thread's chunks for EG experts at a time, the gate read
+// from L2 once per TB rows; folded across the wave by transpose_reduce and
+// across the 4 waves through LDS; logits rounded to T (round_logits) plus the
+// bias; then softmax / top-k / renormalisation by wave_topk as the router
+// does (FusedMoE.route, reframework/moe/moe_layer.py:320-344). Rows past T
+// load the last row again and are not stored.
+//
+// The kernel is a chain of dependent steps per workgroup, so every load that
+// does not depend on an earlier result is issued first: the rows, the norm
+// weight and bias, and (where it fits in registers, PF) the gate chunks of
+// the first EG experts; each later pass's gate chunks are loaded while the
+// pass before it multiplies. One memory round trip then precedes the
+// arithmetic.
+template <typename T, typename W, int CPT, int TB, int EG>
+__global__ __launch_bounds__(kThreads) void add_rmsnorm_router_kernel(const NormArgs a,
+                                                                      const RouterArgs ra) {
+  constexpr int N = Vec16<T>::N;  // elements per 16-byte chunk
+  constexpr int NV = TB * EG;     // router partial sums per thread
+  static_assert(NV <= 64, "one value per lane after the transposed reduction");
+  constexpr int SH = 6 - log2i(NV);
+  constexpr int kWaves = kThreads / kWave;
+  constexpr bool PF = CPT * EG <= 16;  // gate passes double-buffered (2 x 64 VGPRs at most)
+  const int t0 = blockIdx.x * TB, ntok = min(TB, a.T - t0);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int chunks = a.H / N;
+  const T* gate = static_cast<const T*>(ra.gate);
+  __shared__ float red[TB][kWaves];
+  __shared__ float part[kWaves][64];
+  __shared__ float lg[TB][kMaxRouterExperts];
+  __shared__ float psel[kWaves][kMaxRouterExperts];
+  __shared__ int32_t isel[kWaves][kMaxRouterExperts];
+
+  u32x4 npk[TB][CPT];  // the rows: residual sums, then normed, rounded to T
+  u32x4 gcur[PF ? CPT : 1][PF ? EG : 1];  // this pass's gate chunks
+  ParamChunk<W, N> wc[CPT], bc[CPT];
+  {
+    u32x4 rraw[TB][CPT];
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      const size_t row = static_cast<size_t>(t0 + min(t, ntok - 1)) * a.H;
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const int ch = tid + c * kThreads;
+        if (ch < chunks) {
+          npk[t][c] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.x) + row +
+                                                      static_cast<size_t>(ch) * N);
+          if (a.residual)
+            rraw[t][c] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.residual) +
+                                                         row + static_cast<size_t>(ch) * N);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = tid + c * kThreads;
+      if (ch < chunks) {
+        wc[c].load(static_cast<const W*>(a.weight), ch * N);
+        if (a.bias) bc[c].load(static_cast<const W*>(a.bias), ch * N);
+        if constexpr (PF) {
+#pragma unroll
+          for (int j = 0; j < EG; ++j)
+            gcur[c][j] = *reinterpret_cast<const u32x4*>(
+                gate + static_cast<size_t>(min(j, ra.E - 1)) * a.H + static_cast<size_t>(ch) * N);
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      float ss = 0.f;
+      const size_t row = static_cast<size_t>(t0 + t) * a.H;
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const int ch = tid + c * kThreads;
+        if (ch >= chunks) continue;
+        float r[N];
+        Vec16<T>::unpack(npk[t][c], r);
+        if (a.residual) {
+          float sv[N];
+          Vec16<T>::unpack(rraw[t][c], sv);
+#pragma unroll
+          for (int i = 0; i < N; ++i) r[i] = to_f32(from_f32<T>(r[i] + sv[i]));
+          npk[t][c] = pack16<T>(r);
+          if (t < ntok)
+            *reinterpret_cast<u32x4*>(static_cast<T*>(a.residual_out) + row +
+                                      static_cast<size_t>(ch) * N) = npk[t][c];
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) ss += r[i] * r[i];
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) red[t][wave] = ss;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < TB; ++t) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += red[t][w];
+    const float inv = 1.0f / sqrtf(tot / static_cast<float>(a.H) + a.eps);
+    const size_t row = static_cast<size_t>(t0 + t) * a.H;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = tid + c * kThreads;
+      if (ch >= chunks) continue;
+      float r[N], wv[N], bv[N], o[N];
+      Vec16<T>::unpack(npk[t][c], r);
+      wc[c].unpack(wv);
+      if (a.bias) bc[c].unpack(bv);
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        o[i] = r[i] * inv * wv[i];
+        if (a.bias) o[i] += bv[i];
+      }
+      npk[t][c] = pack16<T>(o);
+      if (t < ntok)
+        *reinterpret_cast<u32x4*>(static_cast<T*>(a.out) + row + static_cast<size_t>(ch) * N) =
+            npk[t][c];
+    }
+  }
+
+  // One pass per EG experts: the logits of experts e0 .. e0+EG-1 for the TB rows.
+  for (int e0 = 0; e0 < ra.E; e0 += EG) {
+    const bool more = e0 + EG < ra.E;
+    u32x4 gnext[PF ? CPT : 1][PF ? EG : 1];
+    if constexpr (PF) {
+      if (more) {
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+          const int ch = tid + c * kThreads;
+          if (ch < chunks) {
+#pragma unroll
+            for (int j = 0; j < EG; ++j)
+              gnext[c][j] = *reinterpret_cast<const u32x4*>(
+                  gate + static_cast<size_t>(min(e0 + EG + j, ra.E - 1)) * a.H +
+                  static_cast<size_t>(ch) * N);
+          }
+        }
+      }
+    }
+    float acc[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = tid + c * kThreads;
+      if (ch >= chunks) continue;
+      u32x4 graw[EG];
+#pragma unroll
+      for (int j = 0; j < EG; ++j) {
+        if constexpr (PF)
+          graw[j] = gcur[c][j];
+        else
+          graw[j] = *reinterpret_cast<const u32x4*>(
+              gate + static_cast<size_t>(min(e0 + j, ra.E - 1)) * a.H + static_cast<size_t>(ch) * N);
+      }
+      float xf[TB][N];
+#pragma unroll
+      for (int t = 0; t < TB; ++t) Vec16<T>::unpack(npk[t][c], xf[t]);
+#pragma unroll
+      for (int j = 0; j < EG; ++j) {
+        float gf[N];
+        Vec16<T>::unpack(graw[j], gf);
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
+#pragma unroll
+          for (int q = 0; q < N; ++q) acc[t * EG + j] = fmaf(xf[t][q], gf[q], acc[t * EG + j]);
+      }
+    }
+    const float r = transpose_reduce<NV>(acc, lane);
+    if ((lane & ((1 << SH) - 1)) == 0) part[wave][lane >> SH] = r;
+    __syncthreads();
+    for (int i = tid; i < NV; i += kThreads) {
+      const int t = i / EG, e = e0 + i % EG;
+      if (t < ntok && e < ra.E) {
+        float l = (part[0][i] + part[1][i]) + (part[2][i] + part[3][i]);
+        if (ra.round_logits) l = to_f32(from_f32<T>(l));
+        if (ra.bias) l += ra.bias[e];
+        lg[t][e] = l;
+        if (ra.logits_out) ra.logits_out[static_cast<size_t>(t0 + t) * ra.E + e] = l;
+      }
+    }
+    __syncthreads();
+    if constexpr (PF) {
+      if (more) {
+#pragma unroll
+        for (int c = 0; c < CPT; ++c)
+#pragma unroll
+          for (int j = 0; j < EG; ++j) gcur[c][j] = gnext[c][j];
+      }
+    }
+  }
+  for (int t = wave; t < ntok; t += kWaves)
+    wave_topk(lg[t], ra.E, ra.K, ra.renormalize, 0, psel[wave], isel[wave],
+              ra.topk_w + static_cast<size_t>(t0 + t) * ra.out_ld,
+              ra.topk_ids + static_cast<size_t>(t0 + t) * ra.out_ld, lane);
+}
+
+template <typename T, typename W, int CPT>
+hipError_t launch_norm_router_cpt(const NormArgs& a, const RouterArgs& ra, hipStream_t s) {
+  const dim3 block(kThreads);
+  // Two rows per workgroup from 512 rows on: the gate is then read from L2
+  // once per two rows, and 256+ workgroups still fill the chip.
+  if (a.T >= 512) {
+    const dim3 grid((a.T + 1) / 2);
+    if (ra.E <= 8)
+      add_rmsnorm_router_kernel<T, W, CPT, 2, 8><<<grid, block, 0, s>>>(a, ra);
+    else
+      add_rmsnorm_router_kernel<T, W, CPT, 2, 16><<<grid, block, 0, s>>>(a, ra);
+  } else {
+    const dim3 grid(a.T);
+    if (ra.E <= 8)
+      add_rmsnorm_router_kernel<T, W, CPT, 1, 8><<<grid, block, 0, s>>>(a, ra);
+    else
+      add_rmsnorm_router_kernel<T, W, CPT, 1, 16><<<grid, block, 0, s>>>(a, ra);
+  }
+  return hipGetLastError();
+}
+
+template <typename T, typename W>
+hipError_t launch_norm_router_tw(const NormArgs& a, const RouterArgs& ra, hipStream_t s) {
+  const int per_thread = (a.H / Vec16<T>::N + kThreads - 1) / kThreads;
+  if (per_thread <= 1) return launch_norm_router_cpt<T, W, 1>(a, ra, s);
+  if (per_thread <= 2) return launch_norm_router_cpt<T, W, 2>(a, ra, s);
+  return launch_norm_router_cpt<T, W, 4>(a, ra, s);
+}
+
+template <typename T>
+hipError_t launch_norm_router_t(const NormArgs& a, const RouterArgs& ra, hipStream_t s) {
+  if (a.weight_dtype == MOE355_BF16) return launch_norm_router_tw<T, bf16>(a, ra, s);
+  if (a.weight_dtype == MOE355_F16) return launch_norm_router_tw<T, f16>(a, ra, s);
+  return launch_norm_router_tw<T, float>(a, ra, s);
+}
+
 template <typename T, typename W>
 hipError_t launch_norm_tw(const NormArgs& a, hipStream_t s) {
   const int per_thread = (a.H / Vec16<T>::N + kThreads - 1) / kThreads;
@@ -182,6 +425,27 @@ hipError_t launch_norm_t(const NormArgs& a, hipStream_t s) {
 
 int norm_max_hidden(int dtype) {
   return kMaxChunks * kThreads * (dtype == MOE355_F32 ? 4 : 8);
+}
+
+// The fused kernel reads the gate from L2 once per one or two rows, the
+// separate MFMA router once per 16 rows: fused wins while T * E stays small
+// (Mixtral H=4096 E=8: 12.7 against 16.4 us at T=1024, even at T=2048 and
+// 4096; 64 experts H=2048: 58 against 26 us at T=4096), and at decode sizes
+// it saves a launch (8 against 14 us per call at T=1..256). Over more than 16
+// experts one workgroup per token pulls the whole gate through one CU (256 KB
+// at 64 experts, H=2048: 13.6 us at T=1), so given a logits buffer the split
+// router, which spreads a token's experts over workgroups, runs instead.
+bool norm_router_fusable(int T, int H, int E, int dtype, bool has_logits) {
+  return (dtype == MOE355_BF16 || dtype == MOE355_F16) && E >= 1 && E <= kMaxRouterExperts &&
+         H % 8 == 0 && H <= 4 * kThreads * 8 && T >= 1 &&
+         static_cast<long long>(T) * E <= 8192 && (E <= 16 || !has_logits);
+}
+
+hipError_t launch_add_rmsnorm_router(const NormArgs& a, const RouterArgs& ra, int dtype,
+                                     hipStream_t s) {
+  if (a.T == 0) return hipSuccess;
+  if (dtype == MOE355_BF16) return launch_norm_router_t<bf16>(a, ra, s);
+  return launch_norm_router_t<f16>(a, ra, s);
 }
 
 hipError_t launch_add_rmsnorm(const NormArgs& a, int dtype, hipStream_t s) {

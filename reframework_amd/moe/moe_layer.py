@@ -146,7 +146,7 @@ class FusedMoE(BaseOP):
         ])
         self._checked_tables: set = set()
         self._shared_cols = None  # cached (key, weights [T,K+n], ids [T,K+n]); see _route32
-        self._logits = None  # cached (key, fp32 [T,E] router logits buffer); see _route32
+        self._logits = None  # cached (key, fp32 [T,E] router logits buffer); see _logits_buffer
         self._cache: Optional[ExpertOffloadCache] = None
         self._cpu_split_enabled: bool = False
         self._predictor: Optional[Prediction] = None
@@ -281,16 +281,20 @@ class FusedMoE(BaseOP):
             if self.entropy_k_min < 1:
                 raise ValueError("entropy-adaptive routing needs entropy_k_min >= 1")
             kmin = min(int(self.entropy_k_min), self.top_k)
-        # A logits buffer lets the router spread few tokens over many experts
-        # across workgroups (it writes the logits there, then selects); one per
-        # token count and stream, reused by the next forward on that stream.
-        lkey = (T, xd.device, _capi.stream_handle(xd.device))
+        _capi.router_topk(xd, gate, None, self.top_k, self.renormalize, True, kmin, w, ids,
+                          logits_out=self._logits_buffer(T, xd.device))
+        return w, ids
+
+    def _logits_buffer(self, T: int, device: torch.device) -> torch.Tensor:
+        """fp32 [T, E] logits buffer. It lets the router spread few tokens
+        over many experts across workgroups (it writes the logits there, then
+        selects); one per token count and stream, reused by the next forward
+        on that stream."""
+        lkey = (T, device, _capi.stream_handle(device))
         if self._logits is None or self._logits[0] != lkey:
             self._logits = (lkey, torch.empty((T, self.num_experts), dtype=torch.float32,
-                                              device=xd.device))
-        _capi.router_topk(xd, gate, None, self.top_k, self.renormalize, True, kmin, w, ids,
-                          logits_out=self._logits[1])
-        return w, ids
+                                              device=device))
+        return self._logits[1]
 
     def route(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
         """Return (topk_weights [M,K] fp32, topk_ids [M,K] int64) for ``x``."""
@@ -432,7 +436,8 @@ class FusedMoE(BaseOP):
         else:
             _capi.add_rmsnorm_router_topk(xd, res, new_res, nw, nb, norm.eps,
                                           gate.to(self.dtype).contiguous(), None, self.top_k,
-                                          self.renormalize, True, normed, w, ids)
+                                          self.renormalize, True, normed, w, ids,
+                                          logits_out=self._logits_buffer(T, xd.device))
         act = activation_code(self.activation)
         if self.cpu_split:
             out = self._forward_split(T, normed, w, ids, act)
