@@ -439,7 +439,8 @@ MAX_STAGED_HOST_POOLS = 4
 
 
 OFFLOAD_MODES = ("max_pack_2_per_layer_lru", "max_pack_2_shared_pool",
-                 "max_pack_2_per_layer_lru_cpu_split", "exact_per_layer_lru_cpu_split",
+                 "max_pack_2_per_layer_lru_cpu_split", "max_pack_2_per_layer_lru_cpu_split_int8",
+                 "exact_per_layer_lru_cpu_split", "exact_per_layer_lru_cpu_split_int8",
                  "exact_chunk1_shared_pool", "max_pack_2_shared_pool_t1",
                  "max_pack_2_shared_pool_lookahead_t1")
 
@@ -470,6 +471,8 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps
         host-computed experts into HBM for later steps;
       * exact_per_layer_lru_cpu_split: every routed expert (no truncation),
         with the CPU/GPU split, ``4 * short_steps`` steps;
+      * ..._cpu_split_int8: the same two, the host half on the per-tensor
+        int8 bank with the reference's int8 numerics (half the host bytes);
       * exact_chunk1_shared_pool: every routed expert, streamed one expert per
         chunk over the shared pool (chunk i+1's copy runs under chunk i's
         kernels); it moves several times more bytes per step than truncation
@@ -543,10 +546,34 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps
             _capi.host_experts(xh, [host[ex][0]], [host[ex][1]], offs, toks, wts, 0, out)
             times.append(time.perf_counter() - t0)
         host_ms[str(m)] = round(sorted(times[1:])[3] * 1000.0, 3)
+    # the same from the int8 bank (half the bytes), built for the split modes anyway
+    int8_ms = {}
+    if any(m.endswith("_int8") for m in modes):
+        layers[0]._cache.quantize_int8_host()
+        bank, sums = layers[0]._cache._int8_host, layers[0]._cache._int8_rowsums
+        for m in (1, 4, T):
+            offs = np.array([0, m], np.int32)
+            toks = np.arange(m, dtype=np.int32)
+            wts = np.ones(m, np.float32)
+            out = torch.zeros(T, h)
+            times = []
+            for rep in range(7):
+                ex = rep % e
+                t0 = time.perf_counter()
+                _capi.host_experts_int8(xh, [bank[ex][0]], [bank[ex][1]], [bank[ex][2]],
+                                        [bank[ex][3]], [sums[ex][0]], [sums[ex][1]], offs, toks,
+                                        wts, 0, out)
+                times.append(time.perf_counter() - t0)
+            int8_ms[str(m)] = round(sorted(times[1:])[3] * 1000.0, 3)
+        layers[0]._cache._cpu_split = False
     host_expert = {"tokens_ms": host_ms, "threads": len(os.sched_getaffinity(0)),
                    "gb_s_at_8_tokens": round(expert_bytes / (host_ms[str(T)] / 1000.0) / 1e9, 1),
                    "copy_ms_at_peak_h2d": round(expert_bytes / peak_h2d / 1e6, 3)}
-    _progress(f"offload decode: host expert {host_ms} ms, copy "
+    if int8_ms:
+        host_expert["int8_tokens_ms"] = int8_ms
+        host_expert["int8_gb_s_at_8_tokens"] = round(
+            expert_bytes / 2 / (int8_ms[str(T)] / 1000.0) / 1e9, 1)
+    _progress(f"offload decode: host expert {host_ms} ms (int8 {int8_ms} ms), copy "
               f"{host_expert['copy_ms_at_peak_h2d']} ms")
 
     ids_all, w_all = synth.offload_trace(n_layers, warmup_steps + steps, T, e)
@@ -555,7 +582,7 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps
     x = (torch.randn(T, h, generator=g, device=dev) * 0.5).to(torch.bfloat16)
     x1 = x[:1].contiguous()
 
-    def run_mode(tag, pool, chunk, n_steps, split=False, lookahead=False, tokens=T):
+    def run_mode(tag, pool, chunk, n_steps, split=False, lookahead=False, tokens=T, int8=False):
         t_mode = time.perf_counter()
         xin = x if tokens == T else x1
 
@@ -575,7 +602,7 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps
             moe._predictor = None
             moe._cache._predictor = None
             if split:
-                moe._cache.enable_host_experts()
+                moe._cache.enable_host_experts(int8=int8)
             if lookahead:
                 moe.attach_predictor(window=8)
         try:
@@ -632,7 +659,8 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps
            "peak_pinned_h2d_gb_s": round(peak_h2d, 2), "host_expert": host_expert}
     for mode in modes:
         shared = "shared_pool" in mode
-        split = mode.endswith("cpu_split")
+        split = "cpu_split" in mode
+        int8 = mode.endswith("_int8")
         t1 = mode.endswith("_t1")
         if mode.startswith("exact_chunk"):
             chunk = int(mode.split("chunk")[1].split("_")[0])
@@ -645,7 +673,8 @@ def config_offload_decode(dev, n_layers, steps, T=8, warmup_steps=4, short_steps
             n_steps = max(1, steps // 2) if t1 else steps
         key = f"{mode}_{n_steps}_steps" if n_steps != steps else mode
         res[key] = run_mode(mode, pool, chunk, n_steps, split=split,
-                            lookahead=mode.endswith("lookahead_t1"), tokens=1 if t1 else T)
+                            lookahead=mode.endswith("lookahead_t1"), tokens=1 if t1 else T,
+                            int8=int8)
     for moe in layers:
         moe._cache.use_pool(None)
     del layers

@@ -7,10 +7,11 @@
  *                                           the GPU half)
  *   reframework/moe/fused.py:140-197      (fused_experts_cpu_int8)
  * The reference quantizes the host bank to int8 and multiplies with
- * torch._int_mm; this library multiplies the staged 16-bit (or fp32)
- * weights directly, with the same numerics as the device kernels: fp32
- * gate|up, the activated intermediate rounded once to the weight type, fp32
- * down projection, routing weight applied in fp32.
+ * torch._int_mm (moe355_host_experts_int8 restates that). moe355_host_experts
+ * multiplies the staged 16-bit (or fp32) weights directly, with the same
+ * numerics as the device kernels: fp32 gate|up, the activated intermediate
+ * rounded once to the weight type, fp32 down projection, routing weight
+ * applied in fp32.
  *
  * Host memory only (pinned or pageable), no GPU calls, no allocation visible
  * to the caller beyond per-call scratch. Thread-safe except for the
@@ -32,7 +33,7 @@ extern "C" {
 #define MOE355_HOST_EINVAL (-1)
 #define MOE355_HOST_ECPU (-2)
 
-/* Version of this ABI (100). */
+/* Version of this ABI (101). */
 int moe355_host_version(void);
 
 /* Message of the last failed call on this thread. */
@@ -55,6 +56,32 @@ int moe355_host_experts(const void* x, int T, int H, int I, int dtype, int n_exp
                         const void* const* w1, const void* const* w2,
                         const int32_t* slot_offsets, const int32_t* slot_tokens,
                         const float* slot_weights, int act, int n_threads, float* out);
+
+/* Symmetric per-tensor int8 codes of a [rows, cols] weight in dtype:
+ * amax = max |w|; amax <= 0 gives zero codes and *scale = 1; otherwise
+ * *scale = amax / 127 (fp32) and q = clamp(round_half_even(w / scale), -127,
+ * 127), the division in fp32. row_sums[r] = sum of row r's codes (the int8
+ * expert call needs them). Replaces _sym_int8_quantize as called by
+ * quantize_int8_host (reframework/moe/offload_cache.py:58-72, 386-407). */
+int moe355_host_quantize_int8(const void* w, int rows, int cols, int dtype, int8_t* q,
+                              float* scale, int32_t* row_sums, int n_threads);
+
+/* moe355_host_experts on int8 weights with the reference's numerics
+ * (fused_experts_cpu_int8, reframework/moe/fused.py:140-197): per expert, the
+ * token rows of its slots (x in dtype, widened to fp32) are quantized as one
+ * block like the weights; gate|up is the exact integer product dequantized as
+ * fp32(acc) * fp32(xs * s1[e]); act(g) * u in fp32; the [m, I] intermediate
+ * block is quantized the same way; y = fp32(acc) * fp32(is * s2[e]), times the
+ * slot's weight, added to out in fp32. w1q[e] [2I, H] and w2q[e] [H, I] are
+ * codes with scales s1[e], s2[e] and row code sums rs1[e] [2I], rs2[e] [H]
+ * from moe355_host_quantize_int8. Slots and out as moe355_host_experts (each
+ * slot's own token, not the reference's i % M). */
+int moe355_host_experts_int8(const void* x, int T, int H, int I, int dtype, int n_experts,
+                             const int8_t* const* w1q, const int8_t* const* w2q, const float* s1,
+                             const float* s2, const int32_t* const* rs1,
+                             const int32_t* const* rs2, const int32_t* slot_offsets,
+                             const int32_t* slot_tokens, const float* slot_weights, int act,
+                             int n_threads, float* out);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,10 @@
  *   oracle_fused_experts_bound  the same, plus the tests' per-element bound for
  *                         fp32 evaluation (a checker bound, no reference counterpart)
  *   oracle_add_rmsnorm    reframework/layers/norm.py:27-53 (RMSNorm._forward, forward_add_residual)
+ *   oracle_quantize_int8  reframework/moe/offload_cache.py:58-72 (_sym_int8_quantize)
+ *   oracle_experts_int8   reframework/moe/fused.py:140-197 (fused_experts_cpu_int8), in the
+ *                         reference's own fp32 / int steps rather than fp64, each slot on
+ *                         its own token
  *
  * Inputs are given in their storage type (fp32, or raw bf16/f16 bits) and are
  * widened exactly. Results are fp64 (outputs) or fp32 rounded once (weights).
@@ -452,4 +456,110 @@ void oracle_add_rmsnorm(const void* x, const void* residual, int type, const dou
  * rounding helpers to the Python side of the oracle. */
 void oracle_round(double* v, size_t n, int mode) {
   for (size_t i = 0; i < n; ++i) v[i] = round_to(v[i], mode);
+}
+
+/* ------------------------------------------------------------------- int8 */
+/* _sym_int8_quantize (reframework/moe/offload_cache.py:58-72) on n fp32
+ * values: amax = max |v| (w.abs().max()); amax <= 0 -> zero codes, scale 1;
+ * else scale = amax / 127.0 (an fp32 tensor divided by a Python float: fp32),
+ * codes = (v / scale).round().clamp(-127, 127): fp32 true division, rounding
+ * half to even. Returns the scale. */
+float oracle_quantize_int8(const float* v, size_t n, int8_t* q) {
+  float amax = 0.0f;
+  for (size_t i = 0; i < n; ++i) {
+    const float a = fabsf(v[i]);
+    if (a > amax) amax = a;
+  }
+  if (!(amax > 0.0f)) {
+    memset(q, 0, n);
+    return 1.0f;
+  }
+  const float scale = amax / 127.0f;
+  for (size_t i = 0; i < n; ++i) {
+    float c = nearbyintf(v[i] / scale);
+    if (c < -127.0f) c = -127.0f;
+    if (c > 127.0f) c = 127.0f;
+    q[i] = (int8_t)c;
+  }
+  return scale;
+}
+
+/* F.silu / F.gelu / F.gelu(approximate="tanh") of the gate times up, in fp32
+ * as torch evaluates them elementwise (reframework/layers/activation.py:15-59):
+ * silu x / (1 + exp(-x)); gelu x * 0.5 * (1 + erf(x * sqrt(1/2)));
+ * tanh form 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))). */
+static float act_mul_f32(int act, float g, float u) {
+  float a;
+  if (act == 0) {
+    a = g / (1.0f + expf(-g));
+  } else if (act == 1) {
+    a = 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
+  } else {
+    const float c = 0.79788456080286536f;
+    a = 0.5f * g * (1.0f + tanhf(c * (g + 0.044715f * g * g * g)));
+  }
+  return a * u;
+}
+
+/* y[t * rows + r] = sum_k a[t * n + k] * w[r * n + k], exact (int64 sums of
+ * int8 products, returned as the int32 torch._int_mm gives). */
+static void int_mm(const int8_t* a, int m, int n, const int8_t* w, int rows, int32_t* y) {
+  for (int t = 0; t < m; ++t)
+    for (int r = 0; r < rows; ++r) {
+      int64_t s = 0;
+      for (int k = 0; k < n; ++k) s += (int64_t)a[(size_t)t * n + k] * w[(size_t)r * n + k];
+      y[(size_t)t * rows + r] = (int32_t)s;
+    }
+}
+
+/* fused_experts_cpu_int8 (reframework/moe/fused.py:140-197) for n_experts
+ * host experts in the order given: expert e's slots slot_offsets[e] ..
+ * slot_offsets[e+1]-1, each on its own token slot_tokens[s] with weight
+ * slot_weights[s]. Per expert: x rows widened to fp32 and quantized as one
+ * block (xq, xs); gu = fp32(int_mm(xq, w1q)) * fp32(xs * s1) (the Python
+ * float product, cast to fp32 by torch's tensor-scalar multiply);
+ * inter = act(gate) * up; (iq, is) = quantize(inter block);
+ * y = fp32(int_mm(iq, w2q)) * fp32(is * s2); y *= w; out[token] += y.
+ * out [T, H] fp32 is accumulated. Returns 0, or -1 on bad sizes. */
+int oracle_experts_int8(const void* x, int x_type, int T, int H, int I, int n_experts,
+                        const int8_t* const* w1q, const int8_t* const* w2q, const float* s1,
+                        const float* s2, const int32_t* slot_offsets, const int32_t* slot_tokens,
+                        const float* slot_weights, int act, float* out) {
+  if (T < 0 || H <= 0 || I <= 0 || n_experts < 0) return -1;
+  for (int e = 0; e < n_experts; ++e) {
+    const int s0 = slot_offsets[e], m = slot_offsets[e + 1] - s0;
+    if (m <= 0) continue;
+    float* xa = malloc(sizeof(float) * (size_t)m * H);
+    int8_t* xq = malloc((size_t)m * H);
+    int32_t* gu = malloc(sizeof(int32_t) * (size_t)m * 2 * I);
+    float* inter = malloc(sizeof(float) * (size_t)m * I);
+    int8_t* iq = malloc((size_t)m * I);
+    int32_t* y = malloc(sizeof(int32_t) * (size_t)m * H);
+    for (int j = 0; j < m; ++j)
+      for (int h = 0; h < H; ++h)
+        xa[(size_t)j * H + h] = (float)load_elem(x, (size_t)slot_tokens[s0 + j] * H + h, x_type);
+    const float xs = oracle_quantize_int8(xa, (size_t)m * H, xq);
+    int_mm(xq, m, H, w1q[e], 2 * I, gu);
+    const float m1 = (float)((double)xs * (double)s1[e]);
+    for (int j = 0; j < m; ++j)
+      for (int i = 0; i < I; ++i) {
+        const float g = (float)gu[(size_t)j * 2 * I + i] * m1;
+        const float u = (float)gu[(size_t)j * 2 * I + I + i] * m1;
+        inter[(size_t)j * I + i] = act_mul_f32(act, g, u);
+      }
+    const float is = oracle_quantize_int8(inter, (size_t)m * I, iq);
+    int_mm(iq, m, I, w2q[e], H, y);
+    const float m2 = (float)((double)is * (double)s2[e]);
+    for (int j = 0; j < m; ++j) {
+      float* o = out + (size_t)slot_tokens[s0 + j] * H;
+      const float wt = slot_weights[s0 + j];
+      for (int h = 0; h < H; ++h) {
+        float v = (float)y[(size_t)j * H + h] * m2;
+        v = v * wt;
+        o[h] = o[h] + v;
+      }
+    }
+    free(xa); free(xq); free(gu); free(inter); free(iq); free(y);
+  }
+  return 0;
 }

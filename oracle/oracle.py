@@ -52,6 +52,11 @@ def lib() -> ctypes.CDLL:
         h.oracle_round.restype = None
         h.oracle_add_rmsnorm.argtypes = [P, P, I, P, P, ctypes.c_double, I, I, P, P]
         h.oracle_add_rmsnorm.restype = None
+        h.oracle_quantize_int8.argtypes = [P, ctypes.c_size_t, P]
+        h.oracle_quantize_int8.restype = ctypes.c_float
+        h.oracle_experts_int8.argtypes = [P, I, I, I, I, I, ctypes.POINTER(P), ctypes.POINTER(P),
+                                          P, P, P, P, P, I, P]
+        h.oracle_experts_int8.restype = I
         _lib = h
     return _lib
 
@@ -207,3 +212,41 @@ def max_rel(out: np.ndarray, ref: np.ndarray) -> float:
     ref = np.asarray(ref, dtype=np.float64)
     denom = float(np.max(np.abs(ref)))
     return float(np.max(np.abs(out - ref))) / (denom if denom > 0 else 1.0)
+
+
+def quantize_int8(w) -> tuple:
+    """(int8 codes, scale) of ``w`` (any shape; widened to fp32) by the
+    reference's symmetric per-tensor rule."""
+    v = np.ascontiguousarray(_cpu(w).float().numpy() if isinstance(w, torch.Tensor) else
+                             np.asarray(w, dtype=np.float32))
+    q = np.empty(v.shape, dtype=np.int8)
+    scale = lib().oracle_quantize_int8(v.ctypes.data, v.size, q.ctypes.data)
+    return q, float(scale)
+
+
+def experts_int8(x: torch.Tensor, w1q: Sequence[np.ndarray], w2q: Sequence[np.ndarray],
+                 s1: Sequence[float], s2: Sequence[float], slot_offsets: np.ndarray,
+                 slot_tokens: np.ndarray, slot_weights: np.ndarray, act: int = 0) -> np.ndarray:
+    """fp32 [T,H]: the reference's int8 host experts (fused_experts_cpu_int8)
+    over the given slots, in the reference's own fp32 / integer steps."""
+    xt, tx = _raw(x)
+    T, H = xt.shape
+    n = len(w1q)
+    I = w2q[0].shape[1] if n else 1
+    q1 = [np.ascontiguousarray(a, dtype=np.int8) for a in w1q]
+    q2 = [np.ascontiguousarray(b, dtype=np.int8) for b in w2q]
+    P = ctypes.c_void_p
+    t1 = (P * max(n, 1))(*[a.ctypes.data for a in q1])
+    t2 = (P * max(n, 1))(*[b.ctypes.data for b in q2])
+    sc1 = np.ascontiguousarray(np.asarray(s1, dtype=np.float32).reshape(-1))
+    sc2 = np.ascontiguousarray(np.asarray(s2, dtype=np.float32).reshape(-1))
+    offs = np.ascontiguousarray(slot_offsets, dtype=np.int32)
+    toks = np.ascontiguousarray(slot_tokens, dtype=np.int32)
+    wts = np.ascontiguousarray(slot_weights, dtype=np.float32)
+    out = np.zeros((T, H), dtype=np.float32)
+    rc = lib().oracle_experts_int8(xt.data_ptr(), tx, T, H, I, n, t1, t2, sc1.ctypes.data,
+                                   sc2.ctypes.data, offs.ctypes.data, toks.ctypes.data,
+                                   wts.ctypes.data, int(act), out.ctypes.data)
+    if rc != 0:
+        raise ValueError("oracle_experts_int8: bad sizes")
+    return out

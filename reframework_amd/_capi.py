@@ -16,6 +16,7 @@ import threading
 from collections import OrderedDict
 from typing import Dict, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 LIB_NAME = "libmoe355.so"
@@ -110,6 +111,9 @@ _HOST_SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "moe355_host_version": (_I, []),
     "moe355_host_last_error": (ctypes.c_char_p, []),
     "moe355_host_experts": (_I, [_P, _I, _I, _I, _I, _I, _PP, _PP, _P, _P, _P, _I, _I, _P]),
+    "moe355_host_quantize_int8": (_I, [_P, _I, _I, _I, _P, _P, _P, _I]),
+    "moe355_host_experts_int8": (_I, [_P, _I, _I, _I, _I, _I, _PP, _PP, _P, _P, _PP, _PP, _P, _P,
+                                      _P, _I, _I, _P]),
 }
 _host_lib: Optional[ctypes.CDLL] = None
 
@@ -479,6 +483,63 @@ def host_experts(x: torch.Tensor, w1: Sequence[torch.Tensor], w2: Sequence[torch
         msg = host_lib().moe355_host_last_error()
         raise MoeLibError(f"moe355_host_experts failed (status {rc}): "
                           f"{msg.decode() if msg else ''}")
+
+
+def _host_check(name: str, rc: int) -> None:
+    if rc != 0:
+        msg = host_lib().moe355_host_last_error()
+        raise MoeLibError(f"{name} failed (status {rc}): {msg.decode() if msg else ''}")
+
+
+def host_quantize_int8(w: torch.Tensor, n_threads: int = 0):
+    """moe355_host_quantize_int8 on a contiguous host [rows, cols] weight:
+    (int8 codes [rows, cols], scale (float), int32 row code sums [rows])."""
+    if w.device.type != "cpu" or w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("host_quantize_int8 takes a contiguous host [rows, cols] tensor")
+    rows, cols = w.shape
+    q = torch.empty((rows, cols), dtype=torch.int8)
+    rs = torch.empty((rows,), dtype=torch.int32)
+    scale = ctypes.c_float(0.0)
+    _host_check("moe355_host_quantize_int8", host_lib().moe355_host_quantize_int8(
+        _ptr(w), rows, cols, dtype_code(w.dtype), _ptr(q), ctypes.addressof(scale), _ptr(rs),
+        int(n_threads)))
+    return q, float(scale.value), rs
+
+
+def host_experts_int8(x: torch.Tensor, w1q: Sequence[torch.Tensor], w2q: Sequence[torch.Tensor],
+                      s1: Sequence[float], s2: Sequence[float], rs1: Sequence[torch.Tensor],
+                      rs2: Sequence[torch.Tensor], slot_offsets, slot_tokens, slot_weights,
+                      act: int, out: torch.Tensor, n_threads: int = 0) -> None:
+    """moe355_host_experts_int8: ``out`` (host fp32 [T,H]) += the int8
+    experts given (codes [2I,H] / [H,I], their scales and row code sums from
+    host_quantize_int8) over their slots, with the reference's int8 numerics."""
+    if x.device.type != "cpu" or out.device.type != "cpu" or out.dtype != torch.float32:
+        raise ValueError("host_experts_int8 takes host tensors and an fp32 host output")
+    T, H = x.shape
+    n = len(w1q)
+    if not (len(w2q) == len(s1) == len(s2) == len(rs1) == len(rs2) == n):
+        raise ValueError("host_experts_int8: per-expert lists differ in length")
+    I = w2q[0].shape[1] if n else 1
+    for a, b, r1, r2 in zip(w1q, w2q, rs1, rs2):
+        if a.dtype != torch.int8 or b.dtype != torch.int8 or tuple(a.shape) != (2 * I, H) or \
+                tuple(b.shape) != (H, I) or not a.is_contiguous() or not b.is_contiguous() or \
+                r1.dtype != torch.int32 or r2.dtype != torch.int32 or \
+                tuple(r1.shape) != (2 * I,) or tuple(r2.shape) != (H,) or \
+                a.device.type != "cpu" or b.device.type != "cpu":
+            raise ValueError("int8 host experts must be contiguous host int8 [2I,H] / [H,I] codes "
+                             "with int32 row sums [2I] / [H]")
+    t1, _k1 = _ptr_table([int(a.data_ptr()) for a in w1q])
+    t2, _k2 = _ptr_table([int(b.data_ptr()) for b in w2q])
+    r1t, _k3 = _ptr_table([int(r.data_ptr()) for r in rs1])
+    r2t, _k4 = _ptr_table([int(r.data_ptr()) for r in rs2])
+    sc1 = np.ascontiguousarray(np.asarray(s1, dtype=np.float32).reshape(-1)) if n else \
+        np.zeros(1, np.float32)
+    sc2 = np.ascontiguousarray(np.asarray(s2, dtype=np.float32).reshape(-1)) if n else \
+        np.zeros(1, np.float32)
+    _host_check("moe355_host_experts_int8", host_lib().moe355_host_experts_int8(
+        _ptr(x), T, H, I, dtype_code(x.dtype), n, t1, t2, sc1.ctypes.data, sc2.ctypes.data,
+        r1t, r2t, slot_offsets.ctypes.data, slot_tokens.ctypes.data, slot_weights.ctypes.data,
+        int(act), int(n_threads), _ptr(out)))
 
 
 # ------------------------------------------------------------------ workspace

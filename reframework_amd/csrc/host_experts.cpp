@@ -9,6 +9,12 @@
 // down projection, and the routing weight applied in fp32 to each slot's y
 // before it is added to an fp32 output row.
 //
+// moe355_host_experts_int8 restates the reference's int8 host half itself:
+// symmetric per-tensor int8 codes for the weights (quantized once by
+// moe355_host_quantize_int8) and for each expert's block of token rows and of
+// intermediate rows, integer dot products (exact), dequantized in fp32 by the
+// product of the two scales. It reads half the bytes of the 16-bit path.
+//
 // Decode-sized inputs (a few tokens per expert) make this a weight stream:
 // every weight row is read once from host memory and multiplied against all
 // of an expert's token rows, which stay in L1/L2. Rows are split over the
@@ -369,13 +375,292 @@ void dot_rows(const float* a, int lda, const uint16_t* a16, int lda16, int m, in
   }
 }
 
+// ------------------------------------------------------------------- int8
+// Symmetric per-tensor codes of n fp32 values (the reference's
+// _sym_int8_quantize, reframework/moe/offload_cache.py:58-72): amax = max |v|;
+// amax <= 0 gives zero codes and scale 1; otherwise scale = amax / 127 in fp32
+// and code = clamp(round_half_even(v / scale), -127, 127), the division in
+// fp32 (torch's true division). Returns the scale.
+template <typename Get>
+float quantize_codes(size_t n, Get get, int8_t* q, int n_threads) {
+  float amax = 0.0f;
+#pragma omp parallel for reduction(max : amax) schedule(static) num_threads(n_threads) if (n > (1u << 20))
+  for (size_t i = 0; i < n; ++i) {
+    const float a = std::fabs(get(i));
+    if (a > amax) amax = a;
+  }
+  if (!(amax > 0.0f)) {
+    std::memset(q, 0, n);
+    return 1.0f;
+  }
+  const float scale = amax / 127.0f;
+#pragma omp parallel for schedule(static) num_threads(n_threads) if (n > (1u << 20))
+  for (size_t i = 0; i < n; ++i) {
+    float c = std::nearbyint(get(i) / scale);
+    c = c < -127.0f ? -127.0f : (c > 127.0f ? 127.0f : c);
+    q[i] = static_cast<int8_t>(c);
+  }
+  return scale;
+}
+
+// Dequantization multiplier of an int32 dot product: torch multiplies the
+// fp32 tensor by the Python float xs * s (a double product), which it casts
+// to fp32 first.
+inline float dequant_mul(float xs, float s) {
+  return static_cast<float>(static_cast<double>(xs) * static_cast<double>(s));
+}
+
+// Token rows of an int8 product are stored as unsigned codes (code + 128),
+// lda bytes apart: vpdpbusd multiplies unsigned by signed bytes, and the
+// excess 128 * sum_k w[r, k] is taken off with the weight row's code sum.
+constexpr int kKBlock8 = 1024;
+
+template <int MT>
+__attribute__((target("avx512f,avx512bw,avx512vnni")))
+void dot8_block_vnni(const uint8_t* a, int lda, int n, const int8_t* w, const int32_t* rsum,
+                     int r0, int r1, int32_t* out, int ldo) {
+  int32_t part[16][MT];
+  for (int r = 0; r < r1 - r0; ++r)
+    for (int t = 0; t < MT; ++t) part[r][t] = 0;
+  for (int kb = 0; kb < n; kb += kKBlock8) {
+    const int ke = (kb + kKBlock8) < n ? (kb + kKBlock8) : n;
+    const int kv = kb + ((ke - kb) & ~63);
+    for (int r = r0; r < r1; ++r) {
+      const int8_t* wr = w + static_cast<size_t>(r) * n;
+      for (int off = ke; off < ((ke + kKBlock8) < n ? (ke + kKBlock8) : n); off += 64)
+        _mm_prefetch(reinterpret_cast<const char*>(wr + off), _MM_HINT_T0);
+      __m512i acc[MT];
+      for (int t = 0; t < MT; ++t) acc[t] = _mm512_setzero_si512();
+      for (int k = kb; k < kv; k += 64) {
+        const __m512i wv = _mm512_loadu_si512(wr + k);
+        for (int t = 0; t < MT; ++t)
+          acc[t] = _mm512_dpbusd_epi32(acc[t], _mm512_loadu_si512(a + (size_t)t * lda + k), wv);
+      }
+      for (int t = 0; t < MT; ++t) {
+        int32_t s = _mm512_reduce_add_epi32(acc[t]);
+        for (int k = kv; k < ke; ++k) s += static_cast<int32_t>(a[(size_t)t * lda + k]) * wr[k];
+        part[r - r0][t] += s;
+      }
+    }
+  }
+  for (int r = r0; r < r1; ++r)
+    for (int t = 0; t < MT; ++t) out[(size_t)t * ldo + r] = part[r - r0][t] - 128 * rsum[r];
+}
+
+__attribute__((target("avx512f,avx512bw,avx512vnni")))
+void dot8_rows_vnni(const uint8_t* a, int lda, int m, int n, const int8_t* w, const int32_t* rsum,
+                    int r0, int r1, int32_t* out, int ldo) {
+  for (int t0 = 0; t0 < m; t0 += kMaxTok) {
+    const uint8_t* at = a + (size_t)t0 * lda;
+    int32_t* ot = out + (size_t)t0 * ldo;
+    switch ((m - t0) < kMaxTok ? (m - t0) : kMaxTok) {
+      case 1: dot8_block_vnni<1>(at, lda, n, w, rsum, r0, r1, ot, ldo); break;
+      case 2: dot8_block_vnni<2>(at, lda, n, w, rsum, r0, r1, ot, ldo); break;
+      case 3: dot8_block_vnni<3>(at, lda, n, w, rsum, r0, r1, ot, ldo); break;
+      case 4: dot8_block_vnni<4>(at, lda, n, w, rsum, r0, r1, ot, ldo); break;
+      case 5: dot8_block_vnni<5>(at, lda, n, w, rsum, r0, r1, ot, ldo); break;
+      case 6: dot8_block_vnni<6>(at, lda, n, w, rsum, r0, r1, ot, ldo); break;
+      case 7: dot8_block_vnni<7>(at, lda, n, w, rsum, r0, r1, ot, ldo); break;
+      default: dot8_block_vnni<8>(at, lda, n, w, rsum, r0, r1, ot, ldo); break;
+    }
+  }
+}
+
+// Without VNNI: both codes widened to int16 and multiplied by vpmaddwd (exact
+// int32 pair sums), so no code-sum correction is needed.
+template <int MT>
+__attribute__((target("avx2,fma,f16c")))
+void dot8_block_avx2(const uint8_t* a, int lda, int n, const int8_t* w, int r0, int r1,
+                     int32_t* out, int ldo) {
+  const __m256i bias = _mm256_set1_epi16(128);
+  int32_t part[16][MT];
+  for (int r = 0; r < r1 - r0; ++r)
+    for (int t = 0; t < MT; ++t) part[r][t] = 0;
+  for (int kb = 0; kb < n; kb += kKBlock8) {
+    const int ke = (kb + kKBlock8) < n ? (kb + kKBlock8) : n;
+    const int kv = kb + ((ke - kb) & ~15);
+    for (int r = r0; r < r1; ++r) {
+      const int8_t* wr = w + static_cast<size_t>(r) * n;
+      for (int off = ke; off < ((ke + kKBlock8) < n ? (ke + kKBlock8) : n); off += 64)
+        _mm_prefetch(reinterpret_cast<const char*>(wr + off), _MM_HINT_T0);
+      __m256i acc[MT];
+      for (int t = 0; t < MT; ++t) acc[t] = _mm256_setzero_si256();
+      for (int k = kb; k < kv; k += 16) {
+        const __m256i wv =
+            _mm256_cvtepi8_epi16(_mm_loadu_si128(reinterpret_cast<const __m128i*>(wr + k)));
+        for (int t = 0; t < MT; ++t) {
+          const __m256i av = _mm256_sub_epi16(
+              _mm256_cvtepu8_epi16(
+                  _mm_loadu_si128(reinterpret_cast<const __m128i*>(a + (size_t)t * lda + k))),
+              bias);
+          acc[t] = _mm256_add_epi32(acc[t], _mm256_madd_epi16(av, wv));
+        }
+      }
+      for (int t = 0; t < MT; ++t) {
+        __m128i s4 = _mm_add_epi32(_mm256_castsi256_si128(acc[t]), _mm256_extracti128_si256(acc[t], 1));
+        s4 = _mm_add_epi32(s4, _mm_shuffle_epi32(s4, 0x4e));
+        s4 = _mm_add_epi32(s4, _mm_shuffle_epi32(s4, 0xb1));
+        int32_t s = _mm_cvtsi128_si32(s4);
+        for (int k = kv; k < ke; ++k)
+          s += (static_cast<int32_t>(a[(size_t)t * lda + k]) - 128) * wr[k];
+        part[r - r0][t] += s;
+      }
+    }
+  }
+  for (int r = r0; r < r1; ++r)
+    for (int t = 0; t < MT; ++t) out[(size_t)t * ldo + r] = part[r - r0][t];
+}
+
+__attribute__((target("avx2,fma,f16c")))
+void dot8_rows_avx2(const uint8_t* a, int lda, int m, int n, const int8_t* w, int r0, int r1,
+                    int32_t* out, int ldo) {
+  constexpr int kTok = 4;
+  for (int t0 = 0; t0 < m; t0 += kTok) {
+    const uint8_t* at = a + (size_t)t0 * lda;
+    int32_t* ot = out + (size_t)t0 * ldo;
+    switch ((m - t0) < kTok ? (m - t0) : kTok) {
+      case 1: dot8_block_avx2<1>(at, lda, n, w, r0, r1, ot, ldo); break;
+      case 2: dot8_block_avx2<2>(at, lda, n, w, r0, r1, ot, ldo); break;
+      case 3: dot8_block_avx2<3>(at, lda, n, w, r0, r1, ot, ldo); break;
+      default: dot8_block_avx2<4>(at, lda, n, w, r0, r1, ot, ldo); break;
+    }
+  }
+}
+
+bool have_avx512vnni() {
+  static const bool ok = have_avx512() && __builtin_cpu_supports("avx512vnni");
+  return ok;
+}
+
+// out[t * ldo + r] = sum_k (a[t, k] - 128) * w[r, k], exact in int32 (|sum|
+// <= n * 127 * 127).
+void dot8_rows(const uint8_t* a, int lda, int m, int n, const int8_t* w, const int32_t* rsum,
+               int rows, int32_t* out, int ldo, int n_threads, Isa use) {
+  const int blocks = (rows + kRowBlock - 1) / kRowBlock;
+  const bool vnni = use >= kAvx512 && have_avx512vnni();
+#pragma omp parallel for schedule(static) num_threads(n_threads)
+  for (int b = 0; b < blocks; ++b) {
+    const int r0 = b * kRowBlock;
+    const int r1 = (r0 + kRowBlock) < rows ? (r0 + kRowBlock) : rows;
+    if (vnni)
+      dot8_rows_vnni(a, lda, m, n, w, rsum, r0, r1, out, ldo);
+    else
+      dot8_rows_avx2(a, lda, m, n, w, r0, r1, out, ldo);
+  }
+}
+
+// Codes of m fp32 rows of n (ld floats apart) as unsigned bytes, lda apart.
+float quantize_rows_u8(const float* v, int ld, int m, int n, uint8_t* out, int lda,
+                       std::vector<int8_t>& tmp) {
+  tmp.resize(static_cast<size_t>(m) * n);
+  const float s = quantize_codes(
+      static_cast<size_t>(m) * n,
+      [&](size_t i) { return v[(i / n) * ld + i % n]; }, tmp.data(), 1);
+  for (int j = 0; j < m; ++j)
+    for (int k = 0; k < n; ++k)
+      out[(size_t)j * lda + k] = static_cast<uint8_t>(tmp[(size_t)j * n + k] + 128);
+  return s;
+}
+
 }  // namespace
 
 extern "C" {
 
+int moe355_host_quantize_int8(const void* w, int rows, int cols, int dtype, int8_t* q,
+                              float* scale, int32_t* row_sums, int n_threads) {
+  if (!w || !q || !scale || !row_sums) return fail(MOE355_HOST_EINVAL, "null pointer argument");
+  if (rows <= 0 || cols <= 0) return fail(MOE355_HOST_EINVAL, "bad sizes");
+  if (dtype != MOE355_HOST_F32 && dtype != MOE355_HOST_BF16 && dtype != MOE355_HOST_F16)
+    return fail(MOE355_HOST_EINVAL, "dtype must be f32, bf16 or f16");
+  if (n_threads <= 0) n_threads = omp_get_max_threads();
+  const size_t n = static_cast<size_t>(rows) * cols;
+  *scale = quantize_codes(n, [&](size_t i) { return load_w(w, i, dtype); }, q, n_threads);
+#pragma omp parallel for schedule(static) num_threads(n_threads)
+  for (int r = 0; r < rows; ++r) {
+    int32_t sum = 0;
+    const int8_t* qr = q + static_cast<size_t>(r) * cols;
+    for (int c = 0; c < cols; ++c) sum += qr[c];
+    row_sums[r] = sum;
+  }
+  return 0;
+}
+
+int moe355_host_experts_int8(const void* x, int T, int H, int I, int dtype, int n_experts,
+                             const int8_t* const* w1q, const int8_t* const* w2q, const float* s1,
+                             const float* s2, const int32_t* const* rs1,
+                             const int32_t* const* rs2, const int32_t* slot_offsets,
+                             const int32_t* slot_tokens, const float* slot_weights, int act,
+                             int n_threads, float* out) {
+  if (!x || !out || !slot_offsets ||
+      (n_experts > 0 && (!w1q || !w2q || !s1 || !s2 || !rs1 || !rs2 || !slot_tokens ||
+                         !slot_weights)))
+    return fail(MOE355_HOST_EINVAL, "null pointer argument");
+  if (T < 0 || H <= 0 || I <= 0 || n_experts < 0)
+    return fail(MOE355_HOST_EINVAL, "bad sizes");
+  if (dtype != MOE355_HOST_F32 && dtype != MOE355_HOST_BF16 && dtype != MOE355_HOST_F16)
+    return fail(MOE355_HOST_EINVAL, "dtype must be f32, bf16 or f16");
+  if (act < 0 || act > 2) return fail(MOE355_HOST_EINVAL, "unknown activation code");
+  if (!have_avx2()) return fail(MOE355_HOST_ECPU, "the host CPU lacks AVX2/FMA/F16C");
+  if (slot_offsets[0] != 0) return fail(MOE355_HOST_EINVAL, "slot_offsets[0] must be 0");
+  for (int e = 0; e < n_experts; ++e) {
+    if (slot_offsets[e + 1] < slot_offsets[e])
+      return fail(MOE355_HOST_EINVAL, "slot_offsets must be non-decreasing");
+    if (!w1q[e] || !w2q[e] || !rs1[e] || !rs2[e])
+      return fail(MOE355_HOST_EINVAL, "null expert weight pointer");
+  }
+  const int n_slots = n_experts > 0 ? slot_offsets[n_experts] : 0;
+  for (int s = 0; s < n_slots; ++s)
+    if (slot_tokens[s] < 0 || slot_tokens[s] >= T)
+      return fail(MOE355_HOST_EINVAL, "slot token index out of range");
+  if (n_threads <= 0) n_threads = omp_get_max_threads();
+  const Isa use = isa();
+
+  std::vector<float> xa, inter, row;
+  std::vector<int32_t> acc1, acc2;
+  std::vector<uint8_t> xq, iq;
+  std::vector<int8_t> tmp;
+  for (int e = 0; e < n_experts; ++e) {
+    const int s0 = slot_offsets[e], m = slot_offsets[e + 1] - s0;
+    if (m == 0) continue;
+    // the expert's token rows in fp32, then their codes (one scale for the block)
+    xa.resize(static_cast<size_t>(m) * H);
+    for (int j = 0; j < m; ++j) {
+      const size_t src = static_cast<size_t>(slot_tokens[s0 + j]) * H;
+      for (int h = 0; h < H; ++h) xa[(size_t)j * H + h] = load_w(x, src + h, dtype);
+    }
+    const int ldx = H + 64, ldi = I + 64;  // rows 64 B apart from a multiple of 1 KB
+    xq.assign(static_cast<size_t>(m) * ldx, 128);
+    const float xs = quantize_rows_u8(xa.data(), H, m, H, xq.data(), ldx, tmp);
+    acc1.assign(static_cast<size_t>(m) * 2 * I, 0);
+    dot8_rows(xq.data(), ldx, m, H, w1q[e], rs1[e], 2 * I, acc1.data(), 2 * I, n_threads, use);
+    const float m1 = dequant_mul(xs, s1[e]);
+    inter.resize(static_cast<size_t>(m) * I);
+    for (int j = 0; j < m; ++j)
+      for (int i = 0; i < I; ++i) {
+        const float g = static_cast<float>(acc1[(size_t)j * 2 * I + i]) * m1;
+        const float u = static_cast<float>(acc1[(size_t)j * 2 * I + I + i]) * m1;
+        inter[(size_t)j * I + i] = act_mul(act, g, u);
+      }
+    iq.assign(static_cast<size_t>(m) * ldi, 128);
+    const float is = quantize_rows_u8(inter.data(), I, m, I, iq.data(), ldi, tmp);
+    acc2.assign(static_cast<size_t>(m) * H, 0);
+    dot8_rows(iq.data(), ldi, m, I, w2q[e], rs2[e], H, acc2.data(), H, n_threads, use);
+    const float m2 = dequant_mul(is, s2[e]);
+    for (int j = 0; j < m; ++j) {
+      float* o = out + static_cast<size_t>(slot_tokens[s0 + j]) * H;
+      const float wt = slot_weights[s0 + j];
+      for (int h = 0; h < H; ++h) {
+        const float y = static_cast<float>(acc2[(size_t)j * H + h]) * m2;
+        o[h] += y * wt;
+      }
+    }
+  }
+  return 0;
+}
+
 const char* moe355_host_last_error(void) { return g_err.c_str(); }
 
-int moe355_host_version(void) { return 100; }
+int moe355_host_version(void) { return 101; }
 
 int moe355_host_experts(const void* x, int T, int H, int I, int dtype, int n_experts,
                         const void* const* w1, const void* const* w2,

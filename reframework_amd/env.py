@@ -101,6 +101,15 @@ def get_moe_split_copy_depth() -> int:
     return max(0, _get_int("RE_MOE_SPLIT_COPY_DEPTH", 2))
 
 
+def get_moe_split_int8() -> bool:
+    """RE_MOE_SPLIT_INT8 (not in the reference): 1 runs the CPU/GPU split's
+    host half on the per-tensor int8 bank with the reference's int8 numerics
+    (fused_experts_cpu_int8, fused.py:140-197), half the host bytes per
+    expert; 0 (default) multiplies the staged 16-bit weights with the device
+    kernels' numerics."""
+    return _get_bool("RE_MOE_SPLIT_INT8", False)
+
+
 def get_moe_shuttle_steps() -> int:
     return _get_int("RE_MOE_SHUTTLE_STEPS", 0)
 

@@ -219,16 +219,19 @@ class FusedMoE(BaseOP):
         self._cache.attach_predictor(window=window)
         self._predictor = self._cache._predictor
 
-    def enable_cpu_split(self) -> None:
+    def enable_cpu_split(self, int8: Optional[bool] = None) -> None:
         """Turn on the CPU/GPU split forward for this offloaded layer
         (reference: moe_layer.py:263-282, 523-627): experts not resident in
         device memory are computed on the host cores while the GPU runs the
         resident ones. The host half multiplies the staged 16-bit weights
-        (libmoe355_host) instead of an int8 copy, with the device kernels'
-        numerics. No-op for a layer without an offload cache."""
+        with the device kernels' numerics, or, with ``int8`` (default:
+        RE_MOE_SPLIT_INT8), the reference's per-tensor int8 bank with its
+        int8 numerics (quantize_int8_host + fused_experts_cpu_int8), half
+        the host bytes per expert. No-op for a layer without an offload
+        cache."""
         if self._cache is None:
             return
-        self._cache.enable_host_experts()
+        self._cache.enable_host_experts(int8=env.get_moe_split_int8() if int8 is None else int8)
         self._cpu_split_enabled = True
 
     def set_shuttle(self, shuttle: Optional[CpuShuttle]) -> None:
@@ -533,8 +536,10 @@ class FusedMoE(BaseOP):
         RE_CHUNK_SIZE > 0); resident ones with their copy landed run on the
         GPU into an fp32 accumulator, the rest on the host cores from the
         staged pool while the GPU works; the host sum is added in fp32 and the
-        total cast once. Each slot's output lands on its own token (the
-        reference indexes tokens as if top_k were 1, F6). Afterwards the
+        total cast once (the host half on the int8 bank with the reference's
+        int8 numerics when the split was enabled with int8). Each slot's
+        output lands on its own token (the reference indexes tokens as if
+        top_k were 1, F6). Afterwards the
         host-computed experts are copied to device memory while fewer than
         RE_MOE_SPLIT_COPY_DEPTH copies are in flight (the reference copies
         every one: reactive_load, moe_layer.py:601).
@@ -583,10 +588,18 @@ class FusedMoE(BaseOP):
             else:
                 x_host = xd.cpu()
                 host_out = torch.zeros((T, H), dtype=torch.float32, pin_memory=cache._pinned)
-            _capi.host_experts(x_host, [cache._host[e][0] for e in host_ids],
-                               [cache._host[e][1] for e in host_ids],
-                               np.asarray(offs, np.int32), np.asarray(toks or [0], np.int32),
-                               np.asarray(wts or [0.0], np.float32), act, host_out)
+            slots = (np.asarray(offs, np.int32), np.asarray(toks or [0], np.int32),
+                     np.asarray(wts or [0.0], np.float32))
+            if cache.host_int8:
+                bank = [cache._int8_host[e] for e in host_ids]
+                sums = [cache._int8_rowsums[e] for e in host_ids]
+                _capi.host_experts_int8(x_host, [b[0] for b in bank], [b[1] for b in bank],
+                                        [b[2] for b in bank], [b[3] for b in bank],
+                                        [r[0] for r in sums], [r[1] for r in sums], *slots, act,
+                                        host_out)
+            else:
+                _capi.host_experts(x_host, [cache._host[e][0] for e in host_ids],
+                                   [cache._host[e][1] for e in host_ids], *slots, act, host_out)
             if stg is not None:
                 _capi.merge_host_f32(acc, stg.ptr + o_out, out, stream)
             else:

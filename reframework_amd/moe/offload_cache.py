@@ -47,18 +47,25 @@ from reframework_amd import _capi, env
 logger = logging.getLogger(__name__)
 
 
-def _sym_int8_quantize(w: torch.Tensor) -> Tuple[torch.Tensor, float]:
-    """Symmetric per-tensor int8 codes and scale, ``w ~= q * scale``.
+def _quantize_int8(w: torch.Tensor) -> Tuple[torch.Tensor, float, torch.Tensor]:
+    """(codes shaped like ``w``, scale, int32 code sums of its last-dim rows)
+    by libmoe355_host's symmetric per-tensor rule."""
+    if w.numel() == 0:
+        return (torch.zeros_like(w, dtype=torch.int8, device="cpu"), 1.0,
+                torch.zeros(w.shape[:-1] if w.dim() else (), dtype=torch.int32).reshape(-1))
+    h = w.detach().cpu().contiguous()
+    rows = h.reshape(-1, h.shape[-1]) if h.dim() >= 2 else h.reshape(1, -1)
+    q, scale, rs = _capi.host_quantize_int8(rows)
+    return q.reshape(h.shape), scale, rs
 
-    The largest magnitude maps to +-127; an all-zero tensor gets scale 1.0
-    (reference: offload_cache.py:58-72).
-    """
-    amax = float(w.abs().max().float()) if w.numel() else 0.0
-    if amax <= 0:
-        return torch.zeros_like(w, dtype=torch.int8), 1.0
-    scale = amax / 127.0
-    q = torch.clamp(torch.round(w.float() / scale), -127, 127).to(torch.int8).contiguous()
-    return q, float(scale)
+
+def _sym_int8_quantize(w: torch.Tensor) -> Tuple[torch.Tensor, float]:
+    """Symmetric per-tensor int8 codes and scale, ``w ~= q * scale``
+    (reference: offload_cache.py:58-72): scale = max |w| / 127 in fp32, codes
+    the fp32 quotient ``w / scale`` rounded half to even and clamped to +-127;
+    an all-zero tensor gets scale 1.0. Computed by libmoe355_host."""
+    q, scale, _ = _quantize_int8(w)
+    return q, scale
 
 
 @dataclass
@@ -185,12 +192,15 @@ class _HostPool:
     holder itself is dropped, i.e. when the last cache reading it lets go or
     replaces it)."""
 
-    __slots__ = ("buf", "_last", "touched")
+    __slots__ = ("buf", "_last", "touched", "int8")
 
     def __init__(self, buf: torch.Tensor) -> None:
         self.buf = buf
         self._last: Dict[int, object] = {}  # copy stream handle -> last copy event
         self.touched = False  # every page read once by the host (see touch_pages)
+        # the int8 bank of the pool's experts, built once for every cache
+        # reading the pool: ([(q1, q2, s1, s2)], [(row sums 1, row sums 2)])
+        self.int8: Optional[Tuple[list, list]] = None
 
     def touch_pages(self) -> None:
         """Read one element of every 4 KiB page from the host. The driver
@@ -329,6 +339,9 @@ class ExpertOffloadCache:
         self._bw_headroom: float = 0.9
         self._cpu_split = False
         self._int8_host: List[Tuple[torch.Tensor, torch.Tensor, float, float]] = []
+        # int32 code sums of each int8 expert's rows (w1, w2), for the host kernels
+        self._int8_rowsums: List[Tuple[torch.Tensor, torch.Tensor]] = []
+        self._host_int8 = False  # the split's host half runs on the int8 bank
         # HBM slot pool (cuda devices only)
         self._slot_of: Dict[int, _Slot] = {}
         self._free_slots: List[_Slot] = []
@@ -396,6 +409,8 @@ class ExpertOffloadCache:
         self._host_off = list(other._host_off)
         self._pinned = other._pinned
         self._int8_host = []
+        self._int8_rowsums = []
+        self._host_int8 = False
         self._cpu_split = False
         self._loaded()
 
@@ -461,14 +476,25 @@ class ExpertOffloadCache:
         self.measure_bandwidth()
 
     def quantize_int8_host(self) -> None:
-        """Per-expert symmetric int8 host bank (reference: offload_cache.py:386-407)."""
+        """Per-expert symmetric int8 host bank (reference: offload_cache.py:386-407).
+        Caches reading one staged pool (``share_host``) build it once and
+        share it."""
         if not self._host:
             return
-        self._int8_host = []
-        for w1, w2 in self._host:
-            q1, s1 = _sym_int8_quantize(w1)
-            q2, s2 = _sym_int8_quantize(w2)
-            self._int8_host.append((q1, q2, s1, s2))
+        shared = self._host_pool is not None and self._host_pool.int8 is not None
+        if shared:  # another cache on the same staged pool built it
+            bank, sums = self._host_pool.int8
+        else:
+            bank, sums = [], []
+            for w1, w2 in self._host:
+                q1, s1, r1 = _quantize_int8(w1)
+                q2, s2, r2 = _quantize_int8(w2)
+                bank.append((q1, q2, s1, s2))
+                sums.append((r1, r2))
+            if self._host_pool is not None:
+                self._host_pool.int8 = (bank, sums)
+        self._int8_host = list(bank)
+        self._int8_rowsums = list(sums)
         self._cpu_split = True
 
     def cpu_banks(self, indices: Sequence[int]):
@@ -652,17 +678,27 @@ class ExpertOffloadCache:
                      torch.empty((0, H, I), dtype=self.dtype, device=self.device), {})
         return banks, misses
 
-    def enable_host_experts(self) -> None:
+    def enable_host_experts(self, int8: bool = False) -> None:
         """Arm the CPU/GPU split for this cache: experts that are not
-        resident are computed on the host cores straight from the staged
-        pool (libmoe355_host), so no int8 bank is built (the reference's
-        quantize_int8_host, offload_cache.py:386-407, stays available)."""
+        resident are computed on the host cores (libmoe355_host). By default
+        straight from the staged 16-bit pool with the device kernels'
+        numerics; with ``int8`` from the reference's per-tensor int8 bank
+        (quantize_int8_host, offload_cache.py:386-407), built here, which
+        reads half the bytes per expert."""
         if not self._host:
             return
         _capi.host_lib()  # a missing host library fails here, not mid-forward
-        if self._host_pool is not None:
+        if int8:
+            self.quantize_int8_host()
+        elif self._host_pool is not None:
             self._host_pool.touch_pages()
+        self._host_int8 = bool(int8)
         self._cpu_split = True
+
+    @property
+    def host_int8(self) -> bool:
+        """Whether the split's host half runs on the int8 bank."""
+        return self._host_int8
 
     def split_slots(self, indices: Sequence[int]):
         """Split ``indices`` for the CPU/GPU split forward (reference:

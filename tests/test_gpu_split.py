@@ -101,3 +101,68 @@ def test_split_forward_matches_oracle(dtype, T, H, I, exact, n_shared, dev, monk
         err = oracle.max_rel(outs[step].float().cpu().numpy(), ref)
         print(f"  step {step}: max_rel {err:.2e}", flush=True)
         assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_split_forward_int8_host_half_matches_oracle(exact, dev, monkeypatch):
+    """The split with the int8 host bank (the reference's numerics for the
+    host half, fused_experts_cpu_int8, fused.py:140-197): every step equals
+    the fp64 oracle on the experts that ran on the GPU plus the int8 oracle
+    on the ones that ran on the host (recorded from the host calls), within
+    the bf16 bar. The bf16 host path's bar alone would not hold: the int8
+    half is ~4-5 % off the exact layer."""
+    E, K, T, H, I = 8, 2, 8, 512, 512
+    dtype = torch.bfloat16
+    monkeypatch.setenv("RE_MAX_PACK", "2")
+    if exact:
+        monkeypatch.setenv("RE_CHUNK_SIZE", "8")
+    else:
+        monkeypatch.delenv("RE_CHUNK_SIZE", raising=False)
+    banner(f"split forward, int8 host half, exact={exact}")
+    moe, layer, _ = _layer(E, K, H, I, dtype, seed=3)
+    moe.gate.data = moe.gate.data.to(dev)
+    cache = moe.build_offload_cache(dev, lru_capacity=2)
+    moe.enable_cpu_split(int8=True)
+    assert moe.cpu_split and cache.host_int8
+    code_of = {cache._int8_host[e][0].data_ptr(): e for e in range(E)}
+    calls = []
+    real = _capi.host_experts_int8
+
+    def record(x, w1q, *args, **kw):
+        calls.append(([code_of[q.data_ptr()] for q in w1q], args[5].copy(), args[6].copy(),
+                      args[7].copy()))
+        return real(x, w1q, *args, **kw)
+
+    monkeypatch.setattr(_capi, "host_experts_int8", record)
+    outs, xs, routes, host = [], [], [], []
+    for step in range(5):
+        x = synth.make_tokens(T, H, dtype, seed=200 + step).to(dev)
+        xs.append(x)
+        routes.append(moe.route(x))
+        n = len(calls)
+        outs.append(moe(x))
+        host.append(calls[n:])
+    torch.cuda.synchronize()
+    assert cache.stats.host_experts > 0 and cache.stats.hits > 0
+    for step in range(5):
+        wn, idn = (t.cpu().numpy() for t in routes[step])
+        if not exact:
+            kept = truncated_request(idn, wn, 2)
+            idn = np.where(np.isin(idn, kept), idn, -1)
+        x = xs[step].cpu()
+        on_host = [e for c in host[step] for e in c[0]]
+        ref = oracle.fused_experts(x, layer["w1"], layer["w2"], wn,
+                                   np.where(np.isin(idn, on_host), -1, idn))
+        for ids_c, offs, toks, wts in host[step]:
+            bank = [cache._int8_host[e] for e in ids_c]
+            ref = ref + oracle.experts_int8(x, [b[0].numpy() for b in bank],
+                                            [b[1].numpy() for b in bank], [b[2] for b in bank],
+                                            [b[3] for b in bank], offs, toks, wts, 0)
+        # the host calls cover exactly the kept slots of the host experts
+        want = sorted((t, e) for t in range(T) for e in idn[t] if e in on_host)
+        got = sorted((int(tk), e) for ids_c, offs, toks, _ in host[step]
+                     for k, e in enumerate(ids_c) for tk in toks[offs[k]:offs[k + 1]])
+        assert got == want
+        err = oracle.max_rel(outs[step].float().cpu().numpy(), ref)
+        print(f"  step {step}: {len(on_host)} experts on the host, max_rel {err:.2e}", flush=True)
+        assert err <= TOL[dtype]

@@ -117,4 +117,97 @@ def test_host_library_exports_every_declared_symbol():
     assert set(declared) == set(_capi._HOST_SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.moe355_host_version() == 100
+    assert lib.moe355_host_version() == 101
+
+
+# ------------------------------------------------------------------- int8
+# The int8 host experts restate the reference's fused_experts_cpu_int8
+# (reframework/moe/fused.py:140-197) step for step: integer products are
+# exact and the fp32 steps are the same operations in the same order as the
+# oracle's restatement (tests/test_oracle_int8.py pins that), so the library
+# must match the oracle bit for bit, on every instruction-set path.
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("shape", [(40, 72), (256, 130), (3, 1)])
+def test_host_quantize_int8_matches_oracle(dt, shape):
+    g = torch.Generator().manual_seed(shape[0] + shape[1])
+    w = (torch.randn(*shape, generator=g) * 0.03).to(dt)
+    q, s, rs = _capi.host_quantize_int8(w)
+    oq, os_ = oracle.quantize_int8(w)
+    assert s == os_
+    assert np.array_equal(q.numpy(), oq)
+    assert np.array_equal(rs.numpy(), oq.astype(np.int64).sum(axis=1))
+    z = torch.zeros(4, 9, dtype=dt)
+    qz, sz, rz = _capi.host_quantize_int8(z)
+    assert sz == 1.0 and not qz.any() and not rz.any()
+
+
+def _int8_bank(w1, w2):
+    bank = [(_capi.host_quantize_int8(a), _capi.host_quantize_int8(b)) for a, b in zip(w1, w2)]
+    return ([b[0][0] for b in bank], [b[1][0] for b in bank], [b[0][1] for b in bank],
+            [b[1][1] for b in bank], [b[0][2] for b in bank], [b[1][2] for b in bank])
+
+
+@pytest.mark.parametrize("isa", ["avx2", "avx512"])
+@pytest.mark.parametrize("dt,H,I,act,T", [
+    (torch.bfloat16, 256, 384, 0, 11), (torch.bfloat16, 200, 136, 1, 9),
+    (torch.float16, 512, 256, 2, 5), (torch.float32, 192, 160, 0, 13),
+    (torch.bfloat16, 64, 40, 0, 1), (torch.bfloat16, 1100, 70, 0, 19)])
+def test_host_experts_int8_match_oracle_bit_exact(dt, H, I, act, T, isa, monkeypatch):
+    """Random routing over 5 experts, 3 on the host, with 64/16-wide tails
+    and more than 8 tokens per expert (two token passes)."""
+    monkeypatch.setenv("MOE355_HOST_ISA", isa)
+    E, K = 5, 2
+    x, w1, w2, ids, w = _case(T, H, I, E, K, dt, seed=H + I + T)
+    host = [3, 0, 4]
+    offs, toks, wts = _slots(ids, w, host)
+    q1, q2, s1, s2, r1, r2 = _int8_bank([w1[e] for e in host], [w2[e] for e in host])
+    out = torch.zeros(T, H, dtype=torch.float32)
+    _capi.host_experts_int8(x, q1, q2, s1, s2, r1, r2, offs, toks, wts, act, out)
+    want = oracle.experts_int8(x, [q.numpy() for q in q1], [q.numpy() for q in q2], s1, s2,
+                               offs, toks, wts, act)
+    assert np.array_equal(out.numpy(), want)
+    # and the int8 path stays near the exact layer (the reference's quantization error)
+    ids_h = np.where(np.isin(ids, host), ids, -1)
+    exact = oracle.fused_experts(x, w1, w2, w, ids_h, activation=act)
+    assert oracle.max_rel(out.numpy().astype(np.float64), exact) <= 0.1
+
+
+def test_host_experts_int8_mixtral_shape_decode():
+    """Two Mixtral-8x7B experts (H=4096, I=14336) for 8 decode tokens, bit
+    for bit the oracle's, and the reference's ~4-5 % quantization error
+    against the exact layer."""
+    H, I, T = 4096, 14336, 8
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w1 = [(torch.randn(2 * I, H, generator=g) * 0.02).to(torch.bfloat16) for _ in range(2)]
+    w2 = [(torch.randn(H, I, generator=g) * 0.02).to(torch.bfloat16) for _ in range(2)]
+    ids = np.array([[0, 1], [0, -1], [1, 0], [-1, -1], [0, -1], [1, -1], [0, 1], [-1, -1]])
+    w = np.random.default_rng(2).random((T, 2)).astype(np.float32)
+    offs, toks, wts = _slots(ids, w, [0, 1])
+    q1, q2, s1, s2, r1, r2 = _int8_bank(w1, w2)
+    out = torch.zeros(T, H, dtype=torch.float32)
+    _capi.host_experts_int8(x, q1, q2, s1, s2, r1, r2, offs, toks, wts, 0, out)
+    want = oracle.experts_int8(x, [q.numpy() for q in q1], [q.numpy() for q in q2], s1, s2,
+                               offs, toks, wts, 0)
+    assert np.array_equal(out.numpy(), want)
+    assert np.all(out.numpy()[[3, 7]] == 0)
+    err = oracle.max_rel(out.numpy().astype(np.float64), oracle.fused_experts(x, w1, w2, w, ids))
+    assert 1e-3 < err < 0.1
+
+
+def test_host_experts_int8_rejects_bad_arguments():
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    q1, q2 = torch.zeros(32, 64, dtype=torch.int8), torch.zeros(64, 16, dtype=torch.int8)
+    r1, r2 = torch.zeros(32, dtype=torch.int32), torch.zeros(64, dtype=torch.int32)
+    out = torch.zeros(2, 64)
+    ok = (np.array([0, 1], np.int32), np.array([1], np.int32), np.array([1.0], np.float32))
+    _capi.host_experts_int8(x, [q1], [q2], [1.0], [1.0], [r1], [r2], *ok, 0, out)
+    with pytest.raises(_capi.MoeLibError, match="out of range"):
+        _capi.host_experts_int8(x, [q1], [q2], [1.0], [1.0], [r1], [r2], ok[0],
+                                np.array([5], np.int32), ok[2], 0, out)
+    with pytest.raises(ValueError):
+        _capi.host_experts_int8(x, [q1.float()], [q2], [1.0], [1.0], [r1], [r2], *ok, 0, out)
+    with pytest.raises(ValueError):
+        _capi.host_experts_int8(x, [q1], [q2], [1.0], [1.0], [r1[:5]], [r2], *ok, 0, out)
