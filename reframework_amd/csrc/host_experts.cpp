@@ -384,7 +384,7 @@ void dot_rows(const float* a, int lda, const uint16_t* a16, int lda16, int m, in
 template <typename Get>
 float quantize_codes(size_t n, Get get, int8_t* q, int n_threads) {
   float amax = 0.0f;
-#pragma omp parallel for reduction(max : amax) schedule(static) num_threads(n_threads) if (n > (1u << 20))
+#pragma omp parallel for reduction(max : amax) schedule(static) num_threads(n_threads) if (n > (1u << 14))
   for (size_t i = 0; i < n; ++i) {
     const float a = std::fabs(get(i));
     if (a > amax) amax = a;
@@ -394,7 +394,7 @@ float quantize_codes(size_t n, Get get, int8_t* q, int n_threads) {
     return 1.0f;
   }
   const float scale = amax / 127.0f;
-#pragma omp parallel for schedule(static) num_threads(n_threads) if (n > (1u << 20))
+#pragma omp parallel for schedule(static) num_threads(n_threads) if (n > (1u << 14))
   for (size_t i = 0; i < n; ++i) {
     float c = std::nearbyint(get(i) / scale);
     c = c < -127.0f ? -127.0f : (c > 127.0f ? 127.0f : c);
@@ -415,33 +415,52 @@ inline float dequant_mul(float xs, float s) {
 // excess 128 * sum_k w[r, k] is taken off with the weight row's code sum.
 constexpr int kKBlock8 = 1024;
 
+// R weight rows at a time against MT token rows: each token vector loaded
+// from L1 feeds R vpdpbusd, so the loads per product drop from (MT + 1) / MT
+// to (MT + R) / (R * MT) (R * MT accumulators; R = 2 at 5-8 tokens, 4 below).
+template <int MT, int R>
+__attribute__((target("avx512f,avx512bw,avx512vnni")))
+inline void dot8_rows_r_vnni(const uint8_t* a, int lda, int kb, int ke, int kv, const int8_t* w,
+                             int n, int r, int32_t (*part)[MT]) {
+  const int8_t* wr[R];
+  for (int q = 0; q < R; ++q) {
+    wr[q] = w + static_cast<size_t>(r + q) * n;
+    for (int off = ke; off < ((ke + kKBlock8) < n ? (ke + kKBlock8) : n); off += 64)
+      _mm_prefetch(reinterpret_cast<const char*>(wr[q] + off), _MM_HINT_T0);
+  }
+  __m512i acc[R][MT];
+  for (int q = 0; q < R; ++q)
+    for (int t = 0; t < MT; ++t) acc[q][t] = _mm512_setzero_si512();
+  for (int k = kb; k < kv; k += 64) {
+    __m512i wv[R];
+    for (int q = 0; q < R; ++q) wv[q] = _mm512_loadu_si512(wr[q] + k);
+    for (int t = 0; t < MT; ++t) {
+      const __m512i av = _mm512_loadu_si512(a + (size_t)t * lda + k);
+      for (int q = 0; q < R; ++q) acc[q][t] = _mm512_dpbusd_epi32(acc[q][t], av, wv[q]);
+    }
+  }
+  for (int q = 0; q < R; ++q)
+    for (int t = 0; t < MT; ++t) {
+      int32_t s = _mm512_reduce_add_epi32(acc[q][t]);
+      for (int k = kv; k < ke; ++k) s += static_cast<int32_t>(a[(size_t)t * lda + k]) * wr[q][k];
+      part[q][t] += s;
+    }
+}
+
 template <int MT>
 __attribute__((target("avx512f,avx512bw,avx512vnni")))
 void dot8_block_vnni(const uint8_t* a, int lda, int n, const int8_t* w, const int32_t* rsum,
                      int r0, int r1, int32_t* out, int ldo) {
+  constexpr int R = MT > 4 ? 2 : 4;
   int32_t part[16][MT];
   for (int r = 0; r < r1 - r0; ++r)
     for (int t = 0; t < MT; ++t) part[r][t] = 0;
   for (int kb = 0; kb < n; kb += kKBlock8) {
     const int ke = (kb + kKBlock8) < n ? (kb + kKBlock8) : n;
     const int kv = kb + ((ke - kb) & ~63);
-    for (int r = r0; r < r1; ++r) {
-      const int8_t* wr = w + static_cast<size_t>(r) * n;
-      for (int off = ke; off < ((ke + kKBlock8) < n ? (ke + kKBlock8) : n); off += 64)
-        _mm_prefetch(reinterpret_cast<const char*>(wr + off), _MM_HINT_T0);
-      __m512i acc[MT];
-      for (int t = 0; t < MT; ++t) acc[t] = _mm512_setzero_si512();
-      for (int k = kb; k < kv; k += 64) {
-        const __m512i wv = _mm512_loadu_si512(wr + k);
-        for (int t = 0; t < MT; ++t)
-          acc[t] = _mm512_dpbusd_epi32(acc[t], _mm512_loadu_si512(a + (size_t)t * lda + k), wv);
-      }
-      for (int t = 0; t < MT; ++t) {
-        int32_t s = _mm512_reduce_add_epi32(acc[t]);
-        for (int k = kv; k < ke; ++k) s += static_cast<int32_t>(a[(size_t)t * lda + k]) * wr[k];
-        part[r - r0][t] += s;
-      }
-    }
+    int r = r0;
+    for (; r + R <= r1; r += R) dot8_rows_r_vnni<MT, R>(a, lda, kb, ke, kv, w, n, r, &part[r - r0]);
+    for (; r < r1; ++r) dot8_rows_r_vnni<MT, 1>(a, lda, kb, ke, kv, w, n, r, &part[r - r0]);
   }
   for (int r = r0; r < r1; ++r)
     for (int t = 0; t < MT; ++t) out[(size_t)t * ldo + r] = part[r - r0][t] - 128 * rsum[r];
@@ -549,16 +568,15 @@ void dot8_rows(const uint8_t* a, int lda, int m, int n, const int8_t* w, const i
   }
 }
 
-// Codes of m fp32 rows of n (ld floats apart) as unsigned bytes, lda apart.
-float quantize_rows_u8(const float* v, int ld, int m, int n, uint8_t* out, int lda,
-                       std::vector<int8_t>& tmp) {
-  tmp.resize(static_cast<size_t>(m) * n);
-  const float s = quantize_codes(
-      static_cast<size_t>(m) * n,
-      [&](size_t i) { return v[(i / n) * ld + i % n]; }, tmp.data(), 1);
-  for (int j = 0; j < m; ++j)
-    for (int k = 0; k < n; ++k)
-      out[(size_t)j * lda + k] = static_cast<uint8_t>(tmp[(size_t)j * n + k] + 128);
+// Codes of m fp32 rows of n (contiguous) as unsigned bytes, lda apart.
+float quantize_rows_u8(const float* v, int m, int n, uint8_t* out, int lda,
+                       std::vector<int8_t>& tmp, int n_threads) {
+  const size_t total = static_cast<size_t>(m) * n;
+  tmp.resize(total);
+  const float s = quantize_codes(total, [&](size_t i) { return v[i]; }, tmp.data(), n_threads);
+#pragma omp parallel for schedule(static) num_threads(n_threads) if (total > (1u << 14))
+  for (size_t i = 0; i < total; ++i)
+    out[(i / n) * lda + i % n] = static_cast<uint8_t>(tmp[i] + 128);
   return s;
 }
 
@@ -630,30 +648,31 @@ int moe355_host_experts_int8(const void* x, int T, int H, int I, int dtype, int 
     }
     const int ldx = H + 64, ldi = I + 64;  // rows 64 B apart from a multiple of 1 KB
     xq.assign(static_cast<size_t>(m) * ldx, 128);
-    const float xs = quantize_rows_u8(xa.data(), H, m, H, xq.data(), ldx, tmp);
+    const float xs = quantize_rows_u8(xa.data(), m, H, xq.data(), ldx, tmp, n_threads);
     acc1.assign(static_cast<size_t>(m) * 2 * I, 0);
     dot8_rows(xq.data(), ldx, m, H, w1q[e], rs1[e], 2 * I, acc1.data(), 2 * I, n_threads, use);
     const float m1 = dequant_mul(xs, s1[e]);
     inter.resize(static_cast<size_t>(m) * I);
-    for (int j = 0; j < m; ++j)
-      for (int i = 0; i < I; ++i) {
-        const float g = static_cast<float>(acc1[(size_t)j * 2 * I + i]) * m1;
-        const float u = static_cast<float>(acc1[(size_t)j * 2 * I + I + i]) * m1;
-        inter[(size_t)j * I + i] = act_mul(act, g, u);
-      }
+    const int mi = m * I;
+#pragma omp parallel for schedule(static) num_threads(n_threads)
+    for (int ji = 0; ji < mi; ++ji) {
+      const int j = ji / I, i = ji % I;
+      const float g = static_cast<float>(acc1[(size_t)j * 2 * I + i]) * m1;
+      const float u = static_cast<float>(acc1[(size_t)j * 2 * I + I + i]) * m1;
+      inter[ji] = act_mul(act, g, u);
+    }
     iq.assign(static_cast<size_t>(m) * ldi, 128);
-    const float is = quantize_rows_u8(inter.data(), I, m, I, iq.data(), ldi, tmp);
+    const float is = quantize_rows_u8(inter.data(), m, I, iq.data(), ldi, tmp, n_threads);
     acc2.assign(static_cast<size_t>(m) * H, 0);
     dot8_rows(iq.data(), ldi, m, I, w2q[e], rs2[e], H, acc2.data(), H, n_threads, use);
     const float m2 = dequant_mul(is, s2[e]);
-    for (int j = 0; j < m; ++j) {
-      float* o = out + static_cast<size_t>(slot_tokens[s0 + j]) * H;
-      const float wt = slot_weights[s0 + j];
-      for (int h = 0; h < H; ++h) {
+    // one slot per (token, expert): every output element is written once here
+#pragma omp parallel for schedule(static) num_threads(n_threads)
+    for (int h = 0; h < H; ++h)
+      for (int j = 0; j < m; ++j) {
         const float y = static_cast<float>(acc2[(size_t)j * H + h]) * m2;
-        o[h] += y * wt;
+        out[static_cast<size_t>(slot_tokens[s0 + j]) * H + h] += y * slot_weights[s0 + j];
       }
-    }
   }
   return 0;
 }
@@ -718,23 +737,24 @@ int moe355_host_experts(const void* x, int T, int H, int I, int dtype, int n_exp
       inter16.assign(static_cast<size_t>(m) * ldi16, 0);
     else
       inter.assign(static_cast<size_t>(m) * ldi, 0.0f);
-    for (int j = 0; j < m; ++j)
-      for (int i = 0; i < I; ++i) {
-        const float v = act_mul(act, gu[(size_t)j * 2 * I + i], gu[(size_t)j * 2 * I + I + i]);
-        if (dp)
-          inter16[(size_t)j * ldi16 + i] = f32_to_bf16(v);
-        else
-          inter[(size_t)j * ldi + i] = round_to_type(v, dtype);
-      }
+    const int mi = m * I;
+#pragma omp parallel for schedule(static) num_threads(n_threads)
+    for (int ji = 0; ji < mi; ++ji) {
+      const int j = ji / I, i = ji % I;
+      const float v = act_mul(act, gu[(size_t)j * 2 * I + i], gu[(size_t)j * 2 * I + I + i]);
+      if (dp)
+        inter16[(size_t)j * ldi16 + i] = f32_to_bf16(v);
+      else
+        inter[(size_t)j * ldi + i] = round_to_type(v, dtype);
+    }
     // down: [m, H]
     y.assign(static_cast<size_t>(m) * H, 0.0f);
     dot_rows(inter.data(), ldi, inter16.data(), ldi16, m, I, w2[e], dtype, H, y.data(), H,
              n_threads, use);
-    for (int j = 0; j < m; ++j) {
-      float* o = out + static_cast<size_t>(slot_tokens[s0 + j]) * H;
-      const float wt = slot_weights[s0 + j];
-      for (int h = 0; h < H; ++h) o[h] += wt * y[(size_t)j * H + h];
-    }
+#pragma omp parallel for schedule(static) num_threads(n_threads)
+    for (int h = 0; h < H; ++h)
+      for (int j = 0; j < m; ++j)
+        out[static_cast<size_t>(slot_tokens[s0 + j]) * H + h] += slot_weights[s0 + j] * y[(size_t)j * H + h];
   }
   return 0;
 }
