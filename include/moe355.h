@@ -291,6 +291,16 @@ int moe355_host_staging_free(void* host_ptr);
 int moe355_copy_to_host(void* host_dst, const void* src, size_t bytes, void* stream);
 
 /*
+ * moe355_copy_to_host for n <= 4 regions in one kernel launch: src[k]
+ * (device, bytes[k]) to host_dst + dst_offsets[k], all 16-byte aligned. The
+ * split forward hands a step's routing ids, weights and hidden states to the
+ * host this way (the .tolist() / .cpu() of moe_layer.py:523-627), paying one
+ * launch and one release of the writes to host memory instead of three.
+ */
+int moe355_copy_to_host_multi(void* host_dst, int n, const void* const* src,
+                              const size_t* dst_offsets, const size_t* bytes, void* stream);
+
+/*
  * out[i] = (dtype) (acc[i] + host_src[i]) for i < n, reading host_src
  * (fp32 in mapped pinned memory, written by the host before the call) from
  * the kernel: the merge `out.float() + cpu_out.to(dev)` then `.to(x2.dtype)`

@@ -96,6 +96,7 @@ _SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "moe355_host_staging_alloc": (_I, [_Z, ctypes.POINTER(ctypes.c_void_p)]),
     "moe355_host_staging_free": (_I, [_P]),
     "moe355_copy_to_host": (_I, [_P, _P, _Z, _P]),
+    "moe355_copy_to_host_multi": (_I, [_P, _I, _P, _P, _P, _P]),
     "moe355_merge_host_f32": (_I, [_P, _P, _Z, _I, _P, _P]),
 }
 
@@ -407,6 +408,20 @@ def copy_to_host(host_dst: int, src: torch.Tensor, nbytes: int,
     memory at address ``host_dst`` by a kernel on the stream."""
     s = stream if stream is not None else stream_handle(src.device)
     _check("moe355_copy_to_host", lib().moe355_copy_to_host(host_dst, _ptr(src), nbytes, s))
+
+
+def copy_to_host_multi(host_dst: int, regions, stream: Optional[int] = None) -> None:
+    """moe355_copy_to_host_multi: ``regions`` = [(src tensor, byte offset in
+    the host buffer, bytes)] (at most 4), copied by one kernel on the stream."""
+    n = len(regions)
+    if n == 0:
+        return
+    s = stream if stream is not None else stream_handle(regions[0][0].device)
+    srcs = (ctypes.c_void_p * n)(*[int(t.data_ptr()) for t, _, _ in regions])
+    offs = (ctypes.c_size_t * n)(*[int(o) for _, o, _ in regions])
+    sizes = (ctypes.c_size_t * n)(*[int(b) for _, _, b in regions])
+    _check("moe355_copy_to_host_multi",
+           lib().moe355_copy_to_host_multi(host_dst, n, srcs, offs, sizes, s))
 
 
 def merge_host_f32(acc: torch.Tensor, host_src: int, out: torch.Tensor,

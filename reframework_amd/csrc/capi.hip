@@ -679,6 +679,30 @@ int moe355_copy_to_host(void* host_dst, const void* src, size_t bytes, void* str
   return check_hip(launch_copy_bytes(src, dst, bytes, as_stream(stream)), "copy_to_host launch");
 }
 
+int moe355_copy_to_host_multi(void* host_dst, int n, const void* const* src,
+                              const size_t* dst_offsets, const size_t* bytes, void* stream) {
+  if (n < 0 || n > kMaxCopyRegions)
+    return fail(MOE355_EINVAL, "n=%d regions outside [0, %d]", n, kMaxCopyRegions);
+  if (n == 0) return MOE355_OK;
+  if (!host_dst || !src || !dst_offsets || !bytes)
+    return fail(MOE355_EINVAL, "NULL host_dst, src, dst_offsets or bytes");
+  void* dst = nullptr;
+  if (int rc = device_view(host_dst, &dst, "host_dst")) return rc;
+  CopyRegions r{};
+  r.count = n;
+  for (int k = 0; k < n; ++k) {
+    if (bytes[k] && !src[k]) return fail(MOE355_EINVAL, "NULL src[%d]", k);
+    if ((reinterpret_cast<uintptr_t>(src[k]) | dst_offsets[k] |
+         reinterpret_cast<uintptr_t>(host_dst)) & 15)
+      return fail(MOE355_EINVAL, "src[%d], host_dst and dst_offsets[%d] must be 16-byte aligned",
+                  k, k);
+    r.src[k] = static_cast<const uint8_t*>(src[k]);
+    r.dst[k] = static_cast<uint8_t*>(dst) + dst_offsets[k];
+    r.bytes[k] = bytes[k];
+  }
+  return check_hip(launch_copy_regions(r, as_stream(stream)), "copy_to_host_multi launch");
+}
+
 int moe355_merge_host_f32(const float* acc, const float* host_src, size_t n, int dtype, void* out,
                           void* stream) {
   if (!valid_dtype(dtype)) return fail(MOE355_EINVAL, "unknown dtype %d", dtype);

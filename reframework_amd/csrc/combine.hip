@@ -245,6 +245,20 @@ __global__ __launch_bounds__(kThreads) void copy_bytes_kernel(const uint8_t* src
   for (size_t i = n16 * 16 + t; i < n; i += stride) dst[i] = src[i];
 }
 
+// Up to kMaxRegions regions in one launch (each grid-strided in turn): the
+// routing and hidden states a split step hands to the host, so that one
+// kernel, and one release of its writes to host memory, serves them all.
+__global__ __launch_bounds__(kThreads) void copy_regions_kernel(const CopyRegions r) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  const size_t t = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+  for (int k = 0; k < r.count; ++k) {
+    const size_t n = r.bytes[k], n16 = n / 16;
+    for (size_t i = t; i < n16; i += stride)
+      reinterpret_cast<uint4*>(r.dst[k])[i] = reinterpret_cast<const uint4*>(r.src[k])[i];
+    for (size_t i = n16 * 16 + t; i < n; i += stride) r.dst[k][i] = r.src[k][i];
+  }
+}
+
 // out = acc + host, rounded once to OutT: the host half of the split forward
 // read straight from host memory (16-byte vectors; n a multiple of 4).
 template <typename OutT>
@@ -270,6 +284,17 @@ hipError_t launch_copy_bytes(const void* src, void* dst, size_t n, hipStream_t s
   if (blocks > 1024) blocks = 1024;
   copy_bytes_kernel<<<dim3(blocks), dim3(kThreads), 0, s>>>(static_cast<const uint8_t*>(src),
                                                            static_cast<uint8_t*>(dst), n);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_regions(const CopyRegions& r, hipStream_t s) {
+  size_t most = 0;
+  for (int k = 0; k < r.count; ++k) most = r.bytes[k] > most ? r.bytes[k] : most;
+  if (most == 0) return hipSuccess;
+  size_t blocks = (most / 16 + kThreads - 1) / kThreads;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 1024) blocks = 1024;
+  copy_regions_kernel<<<dim3(blocks), dim3(kThreads), 0, s>>>(r);
   return hipGetLastError();
 }
 

@@ -290,6 +290,15 @@ hipError_t launch_add_rmsnorm_router(const NormArgs& a, const RouterArgs& ra, in
                                      hipStream_t s);
 hipError_t launch_cast_f32(const float* src, void* dst, size_t n, int dtype, hipStream_t s);
 hipError_t launch_copy_bytes(const void* src, void* dst, size_t n, hipStream_t s);
+// Up to four byte regions (16-byte aligned sources and destinations).
+constexpr int kMaxCopyRegions = 4;
+struct CopyRegions {
+  const uint8_t* src[kMaxCopyRegions];
+  uint8_t* dst[kMaxCopyRegions];
+  size_t bytes[kMaxCopyRegions];
+  int count;
+};
+hipError_t launch_copy_regions(const CopyRegions& r, hipStream_t s);
 hipError_t launch_merge_host(const float* acc, const float* host, void* out, size_t n, int dtype,
                              hipStream_t s);
 

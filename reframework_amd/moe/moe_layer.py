@@ -508,10 +508,10 @@ class FusedMoE(BaseOP):
             return ids32.reshape(-1).tolist(), w32.reshape(-1).tolist(), None
         stream = _capi.stream_handle(dev)
         stg = _capi.staging(dev, stream)
-        _capi.copy_to_host(stg.ptr, ids32, T * K * 4, stream)
-        _capi.copy_to_host(stg.ptr + o_w, w32, T * K * 4, stream)
+        regions = [(ids32, 0, T * K * 4), (w32, o_w, T * K * 4)]
         if xd is not None:
-            _capi.copy_to_host(stg.ptr + o_x, xd, xd.numel() * xd.element_size(), stream)
+            regions.append((xd, o_x, xd.numel() * xd.element_size()))
+        _capi.copy_to_host_multi(stg.ptr, regions, stream)
         done = torch.cuda.Event()
         done.record(torch.cuda.current_stream(dev))
         done.synchronize()
@@ -561,10 +561,18 @@ class FusedMoE(BaseOP):
         else:
             run = self._kept_experts(ids_host, w_host)
         w1s, w2s, local_index, host_ids = cache.split_slots(run)
-        acc = torch.zeros((T, H), dtype=torch.float32, device=dev)
         expert_map = [-1] * self.num_experts
         for g, loc in local_index.items():
             expert_map[g] = loc
+        if not host_ids and (w1s or len(self.shared_w1)):
+            # every expert resident: the combine rounds the fp32 sum straight
+            # into the output (0 + sum, the same single rounding as below)
+            out = self._experts(xd, w, ids, act, [t.data_ptr() for t in w1s],
+                                [t.data_ptr() for t in w2s], expert_map=expert_map)
+            cache.mark_read(local_index)
+            self._record_split(M, run, ids_host)
+            return out
+        acc = torch.zeros((T, H), dtype=torch.float32, device=dev)
         if w1s or len(self.shared_w1):
             self._experts(xd, w, ids, act, [t.data_ptr() for t in w1s],
                           [t.data_ptr() for t in w2s], expert_map=expert_map, out=acc,
@@ -609,13 +617,18 @@ class FusedMoE(BaseOP):
             cache.load_while_idle(host_ids, env.get_moe_split_copy_depth())
         else:
             _capi.cast_f32(acc, out)
+        self._record_split(M, run, ids_host)
+        return out
+
+    def _record_split(self, M: int, run: List[int], ids_host: List[int]) -> None:
+        """The split step's routed set for the lookahead predictor; dropped
+        slots read as the first kept id, as in _forward_offload."""
         if self._predictor is not None:
             ran = set(run)
-            fallback = min(run) if run else -1  # the first kept id, as in _forward_offload
+            fallback = min(run) if run else -1
             routed = [i if i in ran else fallback for i in ids_host]
             self._predictor.record_step(routed, is_prefill=(M > 1),
                                         forward_ms=self._since_last_step_ms())
-        return out
 
     def _forward_streaming(self, xd: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
                            act: int) -> torch.Tensor:
