@@ -448,6 +448,11 @@ class ExpertOffloadCache:
         self._release_all()
         self._lru = OrderedDict()
         self.stats.reset()
+        # an int8 bank describes the previous pool's weights
+        self._int8_host = []
+        self._int8_rowsums = []
+        if self._cpu_split:  # an armed split reads the new pool: rebuild what it needs
+            self.enable_host_experts(int8=self._host_int8)
         logger.info("ExpertOffloadCache staged %d experts (%s) in %s host pool; LRU cap=%d",
                     len(self._host), self.dtype, "pinned" if self._pinned else "pageable",
                     self.lru_capacity)
@@ -495,6 +500,7 @@ class ExpertOffloadCache:
                 self._host_pool.int8 = (bank, sums)
         self._int8_host = list(bank)
         self._int8_rowsums = list(sums)
+        self._host_int8 = True  # as in the reference, the split's host half uses this bank
         self._cpu_split = True
 
     def cpu_banks(self, indices: Sequence[int]):

@@ -336,6 +336,32 @@ def test_int8_host_bank():
     assert int(q1.abs().max()) <= 127
 
 
+def test_int8_bank_follows_a_reloaded_pool():
+    """Restaging the pool (load) while the int8 split is armed rebuilds the
+    bank from the new weights; quantize_int8_host alone selects the int8 host
+    half, as in the reference; the 16-bit split drops the bank."""
+    cache = _cache(E=2, cap=2, H=8, I=4)
+    cache.enable_host_experts(int8=True)
+    assert cache.cpu_split and cache.host_int8
+    new = [{"w1": torch.randn(8, 8, dtype=torch.float16) * 5,
+            "w2": torch.randn(8, 4, dtype=torch.float16) * 5} for _ in range(2)]
+    cache.load(new)
+    assert cache.cpu_split and cache.host_int8 and len(cache._int8_host) == 2
+    for e in range(2):
+        q1, q2, s1, s2 = cache._int8_host[e]
+        assert torch.allclose(q1.float() * s1, new[e]["w1"].float(), atol=s1 / 2 + 1e-6)
+        assert torch.allclose(q2.float() * s2, new[e]["w2"].float(), atol=s2 / 2 + 1e-6)
+        r1, r2 = cache._int8_rowsums[e]
+        assert torch.equal(r1, q1.int().sum(dim=1)) and torch.equal(r2, q2.int().sum(dim=1))
+    cache.enable_host_experts(int8=False)
+    assert cache.cpu_split and not cache.host_int8
+    cache.load(new)
+    assert cache.cpu_split and not cache.host_int8 and not cache._int8_host
+    fresh = _cache(E=2, cap=2, H=8, I=4)
+    fresh.quantize_int8_host()
+    assert fresh.cpu_split and fresh.host_int8
+
+
 def test_cpu_shuttle_decay():
     sh = CpuShuttle(n_steps=2)
     sh.send(torch.zeros(4, dtype=torch.float32))  # 16 bytes
