@@ -23,7 +23,10 @@ layers, each with the truncating forward (RE_MAX_PACK=2) and the exact
 streaming forward (RE_CHUNK_SIZE=2 / 1); and the CPU/GPU split forward, where
 the experts not resident run on the host cores (its residency depends on copy
 timing, so only outputs, counts that must add up, and the slot bound are
-checked).
+checked), with the 16-bit host half and with the int8 one. The int8 host
+half has the reference's int8 numerics (fused_experts_cpu_int8, fused.py:
+140-197): its experts are checked against the oracle's int8 restatement on the
+slots each host call was given, the rest against the fp64 oracle.
 """
 
 from __future__ import annotations
@@ -84,6 +87,7 @@ MODES = [
     ("pool_truncate", "pool", "truncate", None),
     ("pool_exact_chunk1", "pool", "exact", 1),
     ("per_layer_split_truncate", "per_layer", "split", None),
+    ("per_layer_split_int8_truncate", "per_layer", "split_int8", None),
 ]
 
 
@@ -103,11 +107,25 @@ def test_offload_decode_mixtral_shape(mode, stack, dev, monkeypatch):
         moe._cache.use_pool(pool)
         moe._cache.stats.reset()
         moe._cpu_split_enabled = False
-        if fwd == "split":
-            moe.enable_cpu_split()
+        if fwd.startswith("split"):
+            moe.enable_cpu_split(int8=fwd == "split_int8")
         r = _Routed(moe)
         monkeypatch.setattr(moe, "_route32", r)
         routers.append(r)
+    # the int8 host half: which experts ran on the host, with which slots, per forward
+    host_calls = {}
+    if fwd == "split_int8":
+        code_of = [{m._cache._int8_host[e][0].data_ptr(): e for e in range(E)} for m in layers]
+        real = _capi.host_experts_int8
+        current = {}
+
+        def record(x, w1q, *args, **kw):
+            host_calls.setdefault(current["n"], []).append(
+                ([code_of[current["li"]][q.data_ptr()] for q in w1q], args[5].copy(),
+                 args[6].copy(), args[7].copy()))
+            return real(x, w1q, *args, **kw)
+
+        monkeypatch.setattr(_capi, "host_experts_int8", record)
     ins, outs = [], []
     try:
         for st in range(STEPS):
@@ -116,6 +134,8 @@ def test_offload_decode_mixtral_shape(mode, stack, dev, monkeypatch):
                 routers[li].route = (torch.from_numpy(w[st, li]).to(dev),
                                      torch.from_numpy(ids[st, li]).to(dev))
                 ins.append(y)
+                if fwd == "split_int8":
+                    current.update(n=len(outs), li=li)
                 y = moe(y)
                 outs.append(y)
         torch.cuda.synchronize()
@@ -123,11 +143,12 @@ def test_offload_decode_mixtral_shape(mode, stack, dev, monkeypatch):
         for moe in layers:
             moe._cpu_split_enabled = False
             moe._cache._cpu_split = False
+            moe._cache._host_int8 = False
     print(f"  forwards done: {len(outs)}", flush=True)
 
     # residency decisions against the brute-force replay
     biggest = 2 if fwd != "exact" else chunk
-    if fwd == "split":
+    if fwd.startswith("split"):
         runs = sum(len(truncated_request(ids[st, li], w[st, li], 2))
                    for st in range(STEPS) for li in range(N_LAYERS))
         st_ = [m._cache.stats for m in layers]
@@ -172,12 +193,28 @@ def test_offload_decode_mixtral_shape(mode, stack, dev, monkeypatch):
             w1 = [host[e][0] for e in range(E)]
             w2 = [host[e][1] for e in range(E)]
             got = outs[n].float().cpu().numpy().astype(np.float64)
-            exact = oracle.fused_experts(x_in, w1, w2, w[st, li], ii)
+            int8_part = 0.0
+            if fwd == "split_int8":
+                # the host experts with the reference's int8 numerics (the oracle's
+                # restatement, which the host library matches bit for bit); the
+                # GPU part on the others
+                on_host = [e for c in host_calls.get(n, []) for e in c[0]]
+                want = sorted((t, e) for t in range(T) for e in ii[t] if e in on_host)
+                seen = sorted((int(tk), e) for ids_c, offs, toks, _ in host_calls.get(n, [])
+                              for k, e in enumerate(ids_c) for tk in toks[offs[k]:offs[k + 1]])
+                assert seen == want, (st, li)
+                for ids_c, offs, toks, wts in host_calls.get(n, []):
+                    bank = [moe._cache._int8_host[e] for e in ids_c]
+                    int8_part = int8_part + oracle.experts_int8(
+                        x_in, [b[0].numpy() for b in bank], [b[1].numpy() for b in bank],
+                        [b[2] for b in bank], [b[3] for b in bank], offs, toks, wts, 0)
+                ii = np.where(np.isin(ii, on_host), -1, ii)
+            exact = oracle.fused_experts(x_in, w1, w2, w[st, li], ii) + int8_part
             err = oracle.max_rel(got, exact)
             worst = max(worst, err)
             assert err <= 2e-2, (st, li, err)
             rounded, allow = oracle.fused_experts_bound(x_in, w1, w2, w[st, li], ii, 0,
                                                         ROUND[torch.bfloat16])
-            assert_matches_rounded(got, rounded, allow, torch.bfloat16)
+            assert_matches_rounded(got, rounded + int8_part, allow, torch.bfloat16)
     print(f"  {STEPS * N_LAYERS} layer outputs x {T} tokens: worst max_rel vs fp64 {worst:.2e}",
           flush=True)
