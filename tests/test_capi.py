@@ -139,6 +139,15 @@ def test_staging_entry_points_reject_bad_arguments_before_any_hip_call():
     assert lib.moe355_merge_host_f32(0x1000, 0x2000, 8, 7, 0x3000, None) == -1
     assert lib.moe355_host_staging_alloc(16, None) == -1
     assert lib.moe355_host_staging_free(None) == 0
+    # the multi-region copy: region count, NULL arrays, alignment, all before any HIP call
+    srcs = (ctypes.c_void_p * 5)(0x2000, 0x3000, 0x4000, 0x5000, 0x6000)
+    offs = (ctypes.c_size_t * 5)(0, 16, 32, 48, 64)
+    sizes = (ctypes.c_size_t * 5)(16, 16, 16, 16, 16)
+    assert lib.moe355_copy_to_host_multi(0x1000, 0, srcs, offs, sizes, None) == 0
+    assert lib.moe355_copy_to_host_multi(0x1000, 5, srcs, offs, sizes, None) == -1
+    assert "regions" in lib.moe355_last_error().decode()
+    assert lib.moe355_copy_to_host_multi(None, 2, srcs, offs, sizes, None) == -1
+    assert lib.moe355_copy_to_host_multi(0x1000, 2, None, offs, sizes, None) == -1
 
 
 def test_zero_tokens_is_a_no_op():

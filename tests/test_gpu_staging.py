@@ -32,6 +32,31 @@ def test_copy_to_host_moves_every_byte(nbytes, dev):
     assert np.all(host[nbytes:] == 0xA5)  # nothing past the end is written
 
 
+@pytest.mark.parametrize("sizes", [(8, 8, 8192), (64, 64), (16,), (0, 48, 70, 1 << 16)])
+def test_copy_to_host_multi_moves_every_region(sizes, dev):
+    """One kernel for up to four regions (the split's ids, weights and hidden
+    states), each landing at its own 16-byte aligned offset, nothing written
+    between or past them."""
+    banner(f"copy_to_host_multi {sizes}")
+    stg = _capi.HostStaging(2 << 20)
+    g = torch.Generator().manual_seed(sum(sizes))
+    srcs = [torch.randint(0, 256, (max(n, 16),), dtype=torch.uint8, generator=g).to(dev)
+            for n in sizes]
+    offs, o = [], 256
+    for n in sizes:
+        offs.append(o)
+        o += (n + 64 + 15) // 16 * 16  # a 64-byte gap after each region
+    host = stg.array(0, np.uint8, o + 64)
+    host[:] = 0xA5
+    _capi.copy_to_host_multi(stg.ptr, [(t, off, n) for t, off, n in zip(srcs, offs, sizes)])
+    torch.cuda.synchronize()
+    written = np.zeros(o + 64, dtype=bool)
+    for t, off, n in zip(srcs, offs, sizes):
+        assert np.array_equal(host[off:off + n], t[:n].cpu().numpy())
+        written[off:off + n] = True
+    assert np.all(host[~written] == 0xA5)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_merge_host_equals_fp32_add_rounded_once(dtype, dev):
     banner(f"merge_host_f32 {dtype}")
