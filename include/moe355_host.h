@@ -75,7 +75,8 @@ int moe355_host_quantize_int8(const void* w, int rows, int cols, int dtype, int8
  * slot's weight, added to out in fp32. w1q[e] [2I, H] and w2q[e] [H, I] are
  * codes with scales s1[e], s2[e] and row code sums rs1[e] [2I], rs2[e] [H]
  * from moe355_host_quantize_int8. Slots and out as moe355_host_experts (each
- * slot's own token, not the reference's i % M). */
+ * slot's own token, not the reference's i % M). H and I at most 65536 (the
+ * integer sums stay in int32). */
 int moe355_host_experts_int8(const void* x, int T, int H, int I, int dtype, int n_experts,
                              const int8_t* const* w1q, const int8_t* const* w2q, const float* s1,
                              const float* s2, const int32_t* const* rs1,

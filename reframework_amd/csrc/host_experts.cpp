@@ -410,6 +410,9 @@ inline float dequant_mul(float xs, float s) {
   return static_cast<float>(static_cast<double>(xs) * static_cast<double>(s));
 }
 
+// Longest K of an int8 product: (code + 128) * w sums stay below 2^31.
+constexpr int kMaxInt8K = 65536;
+
 // Token rows of an int8 product are stored as unsigned codes (code + 128),
 // lda bytes apart: vpdpbusd multiplies unsigned by signed bytes, and the
 // excess 128 * sum_k w[r, k] is taken off with the weight row's code sum.
@@ -615,6 +618,9 @@ int moe355_host_experts_int8(const void* x, int T, int H, int I, int dtype, int 
     return fail(MOE355_HOST_EINVAL, "null pointer argument");
   if (T < 0 || H <= 0 || I <= 0 || n_experts < 0)
     return fail(MOE355_HOST_EINVAL, "bad sizes");
+  // the biased products (code + 128) * w sum to at most n * 255 * 127 in int32
+  if (H > kMaxInt8K || I > kMaxInt8K)
+    return fail(MOE355_HOST_EINVAL, "H and I must be at most 65536 for the int8 products");
   if (dtype != MOE355_HOST_F32 && dtype != MOE355_HOST_BF16 && dtype != MOE355_HOST_F16)
     return fail(MOE355_HOST_EINVAL, "dtype must be f32, bf16 or f16");
   if (act < 0 || act > 2) return fail(MOE355_HOST_EINVAL, "unknown activation code");

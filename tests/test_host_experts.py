@@ -16,6 +16,8 @@ split indexes tokens as if K were 1, F6).
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -211,3 +213,11 @@ def test_host_experts_int8_rejects_bad_arguments():
         _capi.host_experts_int8(x, [q1.float()], [q2], [1.0], [1.0], [r1], [r2], *ok, 0, out)
     with pytest.raises(ValueError):
         _capi.host_experts_int8(x, [q1], [q2], [1.0], [1.0], [r1[:5]], [r2], *ok, 0, out)
+    # K past 65536 would overflow the int32 sums: refused by the library itself
+    lib = _capi.host_lib()
+    one = (ctypes.c_void_p * 1)(q1.data_ptr())
+    rc = lib.moe355_host_experts_int8(x.data_ptr(), 2, 70000, 16, _capi.BF16, 1, one, one,
+                                      ok[2].ctypes.data, ok[2].ctypes.data, one, one,
+                                      ok[0].ctypes.data, ok[1].ctypes.data, ok[2].ctypes.data, 0,
+                                      0, out.data_ptr())
+    assert rc == -1 and b"65536" in lib.moe355_host_last_error()
