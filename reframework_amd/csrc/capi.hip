@@ -97,7 +97,7 @@ int device_cu_count() {
 
 extern "C" {
 
-int moe355_version(void) { return 100; }
+int moe355_version(void) { return 101; }
 
 const char* moe355_last_error(void) { return g_err; }
 

@@ -22,7 +22,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_constants():
-    assert _capi.version() == 100
+    assert _capi.version() == 101
     text = open(_capi.HEADER_PATH).read()
     assert "#define MOE355_MAX_EXPERTS 256" in text
     assert ctypes.sizeof(_capi.Plan) == 12 * 4 + 9 * 8
