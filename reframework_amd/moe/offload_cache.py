@@ -180,6 +180,24 @@ def _note_inflight(device: torch.device, event) -> None:
     evs.append(event)
 
 
+# One host->device copy stream per device, shared by every cache on it. A
+# process gets a few hardware queues (GPU_MAX_HW_QUEUES, 4 by default) and
+# streams beyond them share queues: a copy stream on the compute stream's
+# queue puts the marker that ends each of its copies in that queue, so the
+# kernels queued after it wait for the copy (6 ms for a Mixtral expert). With
+# a stream per layer cache (32 in the offload decode) some always shared it.
+_COPY_STREAMS: Dict[int, "torch.cuda.Stream"] = {}
+
+
+def _copy_stream_for(device: torch.device) -> "torch.cuda.Stream":
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    stream = _COPY_STREAMS.get(idx)
+    if stream is None:
+        stream = torch.cuda.Stream(device=device)  # default priority
+        _COPY_STREAMS[idx] = stream
+    return stream
+
+
 class _HostPool:
     """Owner of one staged host buffer, shared by every cache that reads it
     (``share_host``).
@@ -828,7 +846,7 @@ class ExpertOffloadCache:
     # --------------------------------------------------------------- internals
     def _side_stream(self) -> torch.cuda.Stream:
         if self._copy_stream is None:
-            self._copy_stream = torch.cuda.Stream(device=self.device)  # default priority
+            self._copy_stream = _copy_stream_for(self.device)
         return self._copy_stream
 
     def _acquire_slot(self) -> _Slot:
