@@ -16,7 +16,7 @@ state dict, offload wiring (``build_offload_cache``, ``attach_predictor``,
     lookahead, then the experts run (moe_layer.py:426-442, 477-513).
   * streaming offload (``RE_CHUNK_SIZE`` > 0): every routed expert, in chunks
     of that many experts, accumulated in fp32 (moe_layer.py:354-420). Chunk
-    i+1's host->HBM copies are queued on the cache's side stream while chunk
+    i+1's host->HBM copies are queued on the device's copy stream while chunk
     i's kernels run.
   * CPU/GPU split (``enable_cpu_split``, moe_layer.py:523-627): the experts
     the offload forward would run (``RE_MAX_PACK`` truncation, or every routed

@@ -14,7 +14,10 @@ What changes on MI355X is how bytes move:
     ``[2I,H]`` followed by w2 ``[H,I]``. Evicted slots go to a free list and
     are reused; nothing is reallocated per miss.
   * A miss is one ``hipMemcpyAsync`` (libmoe355 ``moe355_h2d_async``) from the
-    pinned pool into a slot on a side stream, with an event recorded behind it.
+    pinned pool into a slot on the device's copy stream (one per device,
+    shared by every cache: per-cache streams beyond the process's hardware
+    queues land on the compute stream's queue, whose kernels then wait for
+    the copies), with an event recorded behind it.
     The host does not wait: compute streams wait on the slot's event right
     before the kernels that read it (:meth:`prefetch_slots`), so the copy of
     one expert overlaps whatever is already queued, e.g. the lookahead loads
