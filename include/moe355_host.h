@@ -33,7 +33,7 @@ extern "C" {
 #define MOE355_HOST_EINVAL (-1)
 #define MOE355_HOST_ECPU (-2)
 
-/* Version of this ABI (101). */
+/* Version of this ABI (102). */
 int moe355_host_version(void);
 
 /* Message of the last failed call on this thread. */
@@ -65,6 +65,14 @@ int moe355_host_experts(const void* x, int T, int H, int I, int dtype, int n_exp
  * quantize_int8_host (reframework/moe/offload_cache.py:58-72, 386-407). */
 int moe355_host_quantize_int8(const void* w, int rows, int cols, int dtype, int8_t* q,
                               float* scale, int32_t* row_sums, int n_threads);
+
+/* row_sums[r] = sum of row r's codes of a [rows, cols] int8 matrix: the row
+ * sums moe355_host_experts_int8 needs, for codes that did not come from
+ * moe355_host_quantize_int8 (the int8 banks fused_experts_cpu_int8 is handed,
+ * reframework/moe/fused.py:140-151, as packed by cpu_banks,
+ * reframework/moe/offload_cache.py:409-434). */
+int moe355_host_int8_row_sums(const int8_t* q, int rows, int cols, int32_t* row_sums,
+                              int n_threads);
 
 /* moe355_host_experts on int8 weights with the reference's numerics
  * (fused_experts_cpu_int8, reframework/moe/fused.py:140-197): per expert, the

@@ -113,6 +113,7 @@ _HOST_SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "moe355_host_last_error": (ctypes.c_char_p, []),
     "moe355_host_experts": (_I, [_P, _I, _I, _I, _I, _I, _PP, _PP, _P, _P, _P, _I, _I, _P]),
     "moe355_host_quantize_int8": (_I, [_P, _I, _I, _I, _P, _P, _P, _I]),
+    "moe355_host_int8_row_sums": (_I, [_P, _I, _I, _P, _I]),
     "moe355_host_experts_int8": (_I, [_P, _I, _I, _I, _I, _I, _PP, _PP, _P, _P, _PP, _PP, _P, _P,
                                       _P, _I, _I, _P]),
 }
@@ -519,6 +520,17 @@ def host_quantize_int8(w: torch.Tensor, n_threads: int = 0):
         _ptr(w), rows, cols, dtype_code(w.dtype), _ptr(q), ctypes.addressof(scale), _ptr(rs),
         int(n_threads)))
     return q, float(scale.value), rs
+
+
+def host_int8_row_sums(q: torch.Tensor, n_threads: int = 0) -> torch.Tensor:
+    """moe355_host_int8_row_sums: int32 sums of the rows of a contiguous host
+    int8 [rows, cols] matrix of codes."""
+    if q.device.type != "cpu" or q.dtype != torch.int8 or q.dim() != 2 or not q.is_contiguous():
+        raise ValueError("host_int8_row_sums takes a contiguous host int8 [rows, cols] tensor")
+    rs = torch.empty((q.shape[0],), dtype=torch.int32)
+    _host_check("moe355_host_int8_row_sums", host_lib().moe355_host_int8_row_sums(
+        _ptr(q), q.shape[0], q.shape[1], _ptr(rs), int(n_threads)))
+    return rs
 
 
 def host_experts_int8(x: torch.Tensor, w1q: Sequence[torch.Tensor], w2q: Sequence[torch.Tensor],

@@ -583,6 +583,17 @@ float quantize_rows_u8(const float* v, int m, int n, uint8_t* out, int lda,
   return s;
 }
 
+// row_sums[r] = sum of row r's int8 codes (exact in int32 for cols < 2^24)
+void code_row_sums(const int8_t* q, int rows, int cols, int32_t* row_sums, int n_threads) {
+#pragma omp parallel for schedule(static) num_threads(n_threads)
+  for (int r = 0; r < rows; ++r) {
+    int32_t sum = 0;
+    const int8_t* qr = q + static_cast<size_t>(r) * cols;
+    for (int c = 0; c < cols; ++c) sum += qr[c];
+    row_sums[r] = sum;
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -596,13 +607,16 @@ int moe355_host_quantize_int8(const void* w, int rows, int cols, int dtype, int8
   if (n_threads <= 0) n_threads = omp_get_max_threads();
   const size_t n = static_cast<size_t>(rows) * cols;
   *scale = quantize_codes(n, [&](size_t i) { return load_w(w, i, dtype); }, q, n_threads);
-#pragma omp parallel for schedule(static) num_threads(n_threads)
-  for (int r = 0; r < rows; ++r) {
-    int32_t sum = 0;
-    const int8_t* qr = q + static_cast<size_t>(r) * cols;
-    for (int c = 0; c < cols; ++c) sum += qr[c];
-    row_sums[r] = sum;
-  }
+  code_row_sums(q, rows, cols, row_sums, n_threads);
+  return 0;
+}
+
+int moe355_host_int8_row_sums(const int8_t* q, int rows, int cols, int32_t* row_sums,
+                              int n_threads) {
+  if (!q || !row_sums) return fail(MOE355_HOST_EINVAL, "null pointer argument");
+  if (rows <= 0 || cols <= 0) return fail(MOE355_HOST_EINVAL, "bad sizes");
+  if (n_threads <= 0) n_threads = omp_get_max_threads();
+  code_row_sums(q, rows, cols, row_sums, n_threads);
   return 0;
 }
 
@@ -685,7 +699,7 @@ int moe355_host_experts_int8(const void* x, int T, int H, int I, int dtype, int 
 
 const char* moe355_host_last_error(void) { return g_err.c_str(); }
 
-int moe355_host_version(void) { return 101; }
+int moe355_host_version(void) { return 102; }
 
 int moe355_host_experts(const void* x, int T, int H, int I, int dtype, int n_experts,
                         const void* const* w1, const void* const* w2,

@@ -166,3 +166,65 @@ def test_split_forward_int8_host_half_matches_oracle(exact, dev, monkeypatch):
         err = oracle.max_rel(outs[step].float().cpu().numpy(), ref)
         print(f"  step {step}: {len(on_host)} experts on the host, max_rel {err:.2e}", flush=True)
         assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype,T,K,E,H,I", [
+    (torch.bfloat16, 37, 2, 8, 512, 768),
+    (torch.float16, 300, 2, 8, 256, 512),
+    (torch.float32, 16, 6, 12, 256, 128),
+])
+def test_masked_halves_match_oracle(dtype, T, K, E, H, I, dev):
+    """The split's halves as the reference's module functions
+    (fused_experts_masked on the GPU, fused_experts_cpu_int8 on the host,
+    fused.py:90-197) over complementary masks: the GPU half within the bar of
+    the fp64 oracle on its active slots (tokens without one exactly zero),
+    and the sum of both halves within the bar of the oracle's fp64 GPU part
+    plus its int8 host part."""
+    from reframework_amd.moe.fused import fused_experts_cpu_int8, fused_experts_masked
+    banner(f"masked halves {dtype} T={T} K={K} E={E} H={H} I={I}")
+    g = torch.Generator().manual_seed(T + E)
+    w1 = [(torch.randn(2 * I, H, generator=g) * 0.05).to(dtype) for _ in range(E)]
+    w2 = [(torch.randn(H, I, generator=g) * 0.05).to(dtype) for _ in range(E)]
+    x = (torch.randn(T, H, generator=g) * 0.7).to(dtype)
+    rng = np.random.default_rng(T * K)
+    ids = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int64)
+    w = rng.random((T, K)).astype(np.float32)
+    on_gpu = rng.random((T, K)) < 0.5
+    on_gpu[0] = False  # a token with no GPU slot
+    out = fused_experts_masked(x.to(dev), torch.stack(w1).to(dev), torch.stack(w2).to(dev),
+                               torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+                               torch.from_numpy(on_gpu).to(dev))
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and out.shape == (T, H)
+    got = out.float().cpu().numpy()
+    ref = oracle.fused_experts(x, w1, w2, w, np.where(on_gpu, ids, -1))
+    err = oracle.max_rel(got, ref)
+    print(f"  GPU half: max_rel {err:.2e}", flush=True)
+    assert err <= TOL[dtype]
+    assert not got[~on_gpu.any(axis=1)].any()
+    # the host half over the other slots, from int8 banks
+    q1 = [_capi.host_quantize_int8(a) for a in w1]
+    q2 = [_capi.host_quantize_int8(b) for b in w2]
+    w1q, w2q = torch.stack([q[0] for q in q1]), torch.stack([q[0] for q in q2])
+    s1 = torch.tensor([q[1] for q in q1], dtype=torch.float32)
+    s2 = torch.tensor([q[1] for q in q2], dtype=torch.float32)
+    on_host = ~on_gpu
+    host = fused_experts_cpu_int8(x.to(dev), w1q, w2q, s1, s2, torch.from_numpy(w).to(dev),
+                                  torch.from_numpy(ids).to(dev), torch.from_numpy(on_host).to(dev))
+    used, offs, toks, wts = [], [0], [], []
+    for e in range(E):
+        t, k = np.nonzero(on_host & (ids == e))
+        if len(t):
+            used.append(e)
+            toks += t.tolist()
+            wts += w[t, k].tolist()
+            offs.append(len(toks))
+    ref_host = oracle.experts_int8(x, [w1q[e].numpy() for e in used],
+                                   [w2q[e].numpy() for e in used], [float(s1[e]) for e in used],
+                                   [float(s2[e]) for e in used], np.asarray(offs, np.int32),
+                                   np.asarray(toks, np.int32), np.asarray(wts, np.float32))
+    assert np.array_equal(host.numpy(), ref_host)
+    total = (out.float() + host.to(dev)).to(dtype).float().cpu().numpy()
+    err = oracle.max_rel(total, ref + ref_host)
+    print(f"  both halves: max_rel {err:.2e}", flush=True)
+    assert err <= TOL[dtype]

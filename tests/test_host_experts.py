@@ -119,7 +119,7 @@ def test_host_library_exports_every_declared_symbol():
     assert set(declared) == set(_capi._HOST_SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.moe355_host_version() == 101
+    assert lib.moe355_host_version() == 102
 
 
 # ------------------------------------------------------------------- int8
