@@ -90,6 +90,8 @@ inline float act_mul(int act, float g, float u) {
 // t in [0, m). a is fp32 (m rows of n), W rows are 16-bit or fp32.
 
 constexpr int kMaxTok = 8;  // token rows per pass over a weight row
+// Rows of W split in blocks of kRowBlock over the threads (static schedule).
+constexpr int kRowBlock = 16;
 
 template <int DT>
 __attribute__((target("avx512f,avx512bw")))
@@ -188,38 +190,70 @@ void dot_rows_avx512(const float* a, int lda, int m, int n, const void* w, int d
 // bf16 weights against bf16 token rows with vdpbf16ps: each instruction
 // multiplies 32 bf16 pairs (products exact in fp32) and adds them to 16 fp32
 // sums, half the instructions of convert + FMA per weight. The intermediate
-// is already rounded to bf16, so the token rows lose nothing.
+// is already rounded to bf16, so the token rows lose nothing. R weight rows
+// at a time, so one token vector feeds R instructions (R = 2 at 5-8 tokens,
+// 4 below); each (row, token) keeps its 16 lane sums across K blocks in vpart
+// and they are added across lanes once per row.
+template <int MT, int R>
+__attribute__((target("avx512f,avx512bw,avx512bf16")))
+inline void dot_rows_r_bf16dp(const uint16_t* a, int lda, int kb, int ke, int kv, const uint16_t* w,
+                              int n, int r, __m512 (*vpart)[MT], float (*part)[MT]) {
+  const uint16_t* wr[R];
+#pragma GCC unroll 4
+  for (int q = 0; q < R; ++q) {
+    wr[q] = w + static_cast<size_t>(r + q) * n;
+    prefetch_next_block<MOE355_HOST_BF16>(w, static_cast<size_t>(r + q) * n, ke, n);
+  }
+  __m512 acc[R][MT];
+#pragma GCC unroll 4
+  for (int q = 0; q < R; ++q)
+#pragma GCC unroll 8
+    for (int t = 0; t < MT; ++t) acc[q][t] = vpart[q][t];
+  for (int k = kb; k < kv; k += 32) {
+    __m512bh wv[R];
+#pragma GCC unroll 4
+    for (int q = 0; q < R; ++q) wv[q] = (__m512bh)_mm512_loadu_si512(wr[q] + k);
+#pragma GCC unroll 8
+    for (int t = 0; t < MT; ++t) {
+      const __m512bh av = (__m512bh)_mm512_loadu_si512(a + (size_t)t * lda + k);
+#pragma GCC unroll 4
+      for (int q = 0; q < R; ++q) acc[q][t] = _mm512_dpbf16_ps(acc[q][t], wv[q], av);
+    }
+  }
+#pragma GCC unroll 4
+  for (int q = 0; q < R; ++q)
+#pragma GCC unroll 8
+    for (int t = 0; t < MT; ++t) {
+      vpart[q][t] = acc[q][t];
+      for (int k = kv; k < ke; ++k)
+        part[q][t] += bf16_to_f32(wr[q][k]) * bf16_to_f32(a[(size_t)t * lda + k]);
+    }
+}
+
 template <int MT>
 __attribute__((target("avx512f,avx512bw,avx512bf16")))
 void dot_block_bf16dp(const uint16_t* a, int lda, int n, const uint16_t* w, int r0, int r1,
                       float* out, int ldo) {
-  float part[16][MT];
+  constexpr int R = MT > 4 ? 2 : 4;
+  __m512 vpart[kRowBlock][MT];
+  float part[kRowBlock][MT];
   for (int r = 0; r < r1 - r0; ++r)
-    for (int t = 0; t < MT; ++t) part[r][t] = 0.0f;
+    for (int t = 0; t < MT; ++t) {
+      vpart[r][t] = _mm512_setzero_ps();
+      part[r][t] = 0.0f;
+    }
   for (int kb = 0; kb < n; kb += kKBlock) {
     const int ke = (kb + kKBlock) < n ? (kb + kKBlock) : n;
     const int kv = kb + ((ke - kb) & ~31);
-    for (int r = r0; r < r1; ++r) {
-      const size_t row = static_cast<size_t>(r) * n;
-      prefetch_next_block<MOE355_HOST_BF16>(w, row, ke, n);
-      __m512 acc[MT];
-      for (int t = 0; t < MT; ++t) acc[t] = _mm512_setzero_ps();
-      for (int k = kb; k < kv; k += 32) {
-        const __m512bh wv = (__m512bh)_mm512_loadu_si512(w + row + k);
-        for (int t = 0; t < MT; ++t)
-          acc[t] = _mm512_dpbf16_ps(acc[t], wv,
-                                    (__m512bh)_mm512_loadu_si512(a + (size_t)t * lda + k));
-      }
-      for (int t = 0; t < MT; ++t) {
-        float s = _mm512_reduce_add_ps(acc[t]);
-        for (int k = kv; k < ke; ++k)
-          s += bf16_to_f32(w[row + k]) * bf16_to_f32(a[(size_t)t * lda + k]);
-        part[r - r0][t] += s;
-      }
-    }
+    int r = r0;
+    for (; r + R <= r1; r += R)
+      dot_rows_r_bf16dp<MT, R>(a, lda, kb, ke, kv, w, n, r, &vpart[r - r0], &part[r - r0]);
+    for (; r < r1; ++r)
+      dot_rows_r_bf16dp<MT, 1>(a, lda, kb, ke, kv, w, n, r, &vpart[r - r0], &part[r - r0]);
   }
   for (int r = r0; r < r1; ++r)
-    for (int t = 0; t < MT; ++t) out[(size_t)t * ldo + r] = part[r - r0][t];
+    for (int t = 0; t < MT; ++t)
+      out[(size_t)t * ldo + r] = _mm512_reduce_add_ps(vpart[r - r0][t]) + part[r - r0][t];
 }
 
 __attribute__((target("avx512f,avx512bw,avx512bf16")))
@@ -353,9 +387,6 @@ Isa isa() {
   return best;
 }
 
-// Rows of W split in blocks of kRowBlock over the threads (static schedule).
-constexpr int kRowBlock = 16;
-
 // a: the token rows in fp32 (lda floats apart); a16: the same rows as bf16
 // bits (lda16 elements apart), used by the vdpbf16ps path for bf16 weights.
 void dot_rows(const float* a, int lda, const uint16_t* a16, int lda16, int m, int n,
@@ -421,10 +452,14 @@ constexpr int kKBlock8 = 1024;
 // R weight rows at a time against MT token rows: each token vector loaded
 // from L1 feeds R vpdpbusd, so the loads per product drop from (MT + 1) / MT
 // to (MT + R) / (R * MT) (R * MT accumulators; R = 2 at 5-8 tokens, 4 below).
+// The 16 lane sums of each (row, token) are carried across K blocks in vpart
+// and reduced across lanes once per row (integer sums: any order is exact);
+// a reduction per K block cost about as many instructions as the products of
+// the block at 8 tokens.
 template <int MT, int R>
 __attribute__((target("avx512f,avx512bw,avx512vnni")))
 inline void dot8_rows_r_vnni(const uint8_t* a, int lda, int kb, int ke, int kv, const int8_t* w,
-                             int n, int r, int32_t (*part)[MT]) {
+                             int n, int r, __m512i (*vpart)[MT], int32_t (*part)[MT]) {
   const int8_t* wr[R];
   for (int q = 0; q < R; ++q) {
     wr[q] = w + static_cast<size_t>(r + q) * n;
@@ -432,19 +467,27 @@ inline void dot8_rows_r_vnni(const uint8_t* a, int lda, int kb, int ke, int kv, 
       _mm_prefetch(reinterpret_cast<const char*>(wr[q] + off), _MM_HINT_T0);
   }
   __m512i acc[R][MT];
+#pragma GCC unroll 4
   for (int q = 0; q < R; ++q)
-    for (int t = 0; t < MT; ++t) acc[q][t] = _mm512_setzero_si512();
+#pragma GCC unroll 8
+    for (int t = 0; t < MT; ++t) acc[q][t] = vpart[q][t];
   for (int k = kb; k < kv; k += 64) {
     __m512i wv[R];
+#pragma GCC unroll 4
     for (int q = 0; q < R; ++q) wv[q] = _mm512_loadu_si512(wr[q] + k);
+#pragma GCC unroll 8
     for (int t = 0; t < MT; ++t) {
       const __m512i av = _mm512_loadu_si512(a + (size_t)t * lda + k);
+#pragma GCC unroll 4
       for (int q = 0; q < R; ++q) acc[q][t] = _mm512_dpbusd_epi32(acc[q][t], av, wv[q]);
     }
   }
+#pragma GCC unroll 4
   for (int q = 0; q < R; ++q)
+#pragma GCC unroll 8
     for (int t = 0; t < MT; ++t) {
-      int32_t s = _mm512_reduce_add_epi32(acc[q][t]);
+      vpart[q][t] = acc[q][t];
+      int32_t s = 0;
       for (int k = kv; k < ke; ++k) s += static_cast<int32_t>(a[(size_t)t * lda + k]) * wr[q][k];
       part[q][t] += s;
     }
@@ -455,18 +498,26 @@ __attribute__((target("avx512f,avx512bw,avx512vnni")))
 void dot8_block_vnni(const uint8_t* a, int lda, int n, const int8_t* w, const int32_t* rsum,
                      int r0, int r1, int32_t* out, int ldo) {
   constexpr int R = MT > 4 ? 2 : 4;
-  int32_t part[16][MT];
+  __m512i vpart[kRowBlock][MT];
+  int32_t part[kRowBlock][MT];
   for (int r = 0; r < r1 - r0; ++r)
-    for (int t = 0; t < MT; ++t) part[r][t] = 0;
+    for (int t = 0; t < MT; ++t) {
+      vpart[r][t] = _mm512_setzero_si512();
+      part[r][t] = 0;
+    }
   for (int kb = 0; kb < n; kb += kKBlock8) {
     const int ke = (kb + kKBlock8) < n ? (kb + kKBlock8) : n;
     const int kv = kb + ((ke - kb) & ~63);
     int r = r0;
-    for (; r + R <= r1; r += R) dot8_rows_r_vnni<MT, R>(a, lda, kb, ke, kv, w, n, r, &part[r - r0]);
-    for (; r < r1; ++r) dot8_rows_r_vnni<MT, 1>(a, lda, kb, ke, kv, w, n, r, &part[r - r0]);
+    for (; r + R <= r1; r += R)
+      dot8_rows_r_vnni<MT, R>(a, lda, kb, ke, kv, w, n, r, &vpart[r - r0], &part[r - r0]);
+    for (; r < r1; ++r)
+      dot8_rows_r_vnni<MT, 1>(a, lda, kb, ke, kv, w, n, r, &vpart[r - r0], &part[r - r0]);
   }
   for (int r = r0; r < r1; ++r)
-    for (int t = 0; t < MT; ++t) out[(size_t)t * ldo + r] = part[r - r0][t] - 128 * rsum[r];
+    for (int t = 0; t < MT; ++t)
+      out[(size_t)t * ldo + r] =
+          _mm512_reduce_add_epi32(vpart[r - r0][t]) + part[r - r0][t] - 128 * rsum[r];
 }
 
 __attribute__((target("avx512f,avx512bw,avx512vnni")))
