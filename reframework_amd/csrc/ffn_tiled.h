@@ -381,14 +381,19 @@ void ffn_tiled16_kernel(const FfnArgs a) {
   // last reads time to land; at smaller J the same pattern compressed. All 8
   // token blocks are read whatever J is, so the reads do not depend on the
   // next item's J. The MFMAs are volatile assembly, so this program order is
-  // the issue order (the reads and loads cannot move across them).
+  // the issue order (the reads and loads cannot move across them). Weight
+  // block i's J MFMAs run token blocks up for even i and down for odd i, so
+  // consecutive MFMAs share one operand also where i changes: one operand
+  // change per MFMA instead of two at each of the 7 row changes (Mixtral
+  // shape, 4096 tokens: gate_up 1469 -> 1459 us over three interleaved pairs,
+  // outputs bit-identical; each accumulator still sums k in order).
   auto sub = [&](auto sc, int bw, int bx, int h, auto issue, auto jc) {
     constexpr int S = decltype(sc)::value, J = decltype(jc)::value, M = 8 * J;
     using NS = std::integral_constant<int, 1 - S>;
     wait_lgkm0();
     const uint32_t av = abase[h] + bw * kBufBytes, bv = bbase[h] + bx * kBufBytes;
     static_for<0, M>([&](auto mc) {
-      constexpr int m = decltype(mc)::value, i = m / J, j = m % J;
+      constexpr int m = decltype(mc)::value, i = m / J, j = (i & 1) ? J - 1 - m % J : m % J;
       if constexpr (std::is_same<T, bf16>::value)
         accr::mma_bf16<S, i, j>();
       else
