@@ -524,3 +524,51 @@ def test_shared_pool_with_lookahead_matches_resident(dev, monkeypatch):
     assert predicts > 0 and evictions > 0
     for o, w in zip(outs, wants):
         assert torch.allclose(o.float(), w.float(), rtol=0, atol=2e-3 * w.float().abs().max().item())
+
+
+@pytest.mark.parametrize("mode", ["resident", "offload", "streaming", "split", "split_int8",
+                                  "with_norm"])
+def test_zero_tokens_on_every_forward_path(mode, dev, monkeypatch):
+    """An empty batch [0, H] gives an empty [0, H] output on every forward
+    path, as the reference's does (its route, top-k and per-expert loop run
+    on empty tensors: moe_layer.py:320-344, 451-519, 523-627), and a batch
+    after it is still right."""
+    banner(f"zero tokens, {mode}")
+    E, K, H, I = 8, 2, 256, 512
+    dtype = torch.bfloat16
+    monkeypatch.setenv("RE_MAX_PACK", "2")
+    monkeypatch.delenv("RE_CHUNK_SIZE", raising=False)
+    moe = _build(E, K, H, I, dtype)
+    w1 = [p.detach().clone() for p in moe.experts_w1]
+    w2 = [p.detach().clone() for p in moe.experts_w2]
+    if mode in ("resident", "with_norm"):
+        moe = moe.to(dev)
+    else:
+        moe.gate.data = moe.gate.data.to(dev)
+        moe.build_offload_cache(dev, lru_capacity=8)
+        if mode == "streaming":
+            monkeypatch.setenv("RE_CHUNK_SIZE", "4")
+        if mode.startswith("split"):
+            moe.enable_cpu_split(int8=mode.endswith("int8"))
+    x0 = torch.empty(0, H, dtype=dtype, device=dev)
+    if mode == "with_norm":
+        from reframework_amd.layers import RMSNorm
+        norm = RMSNorm(H, 1e-6).to(dev)
+        out, res = moe.forward_with_norm(x0, torch.empty_like(x0), norm)
+        assert res.shape == (0, H)
+    else:
+        out = moe(x0)
+    torch.cuda.synchronize()
+    assert out.shape == (0, H) and out.dtype == dtype
+    # the layer still works on the next batch: with every expert resident
+    # (capacity 8) the output is the full layer's
+    x = synth.make_tokens(5, H, dtype, seed=4)
+    if mode.startswith("split") or mode in ("offload", "streaming"):
+        monkeypatch.setenv("RE_MAX_PACK", "8")
+    rw, rids = moe.route(x.to(dev))
+    got = moe(x.to(dev)).float().cpu().numpy()
+    assert got.shape == (5, H)
+    if mode == "split_int8":
+        return  # host experts on int8 codes: checked against the int8 oracle in test_gpu_split
+    ref = oracle.fused_experts(x, w1, w2, rw.cpu().numpy(), rids.cpu().numpy())
+    assert oracle.max_rel(got, ref) <= TOL[dtype]
