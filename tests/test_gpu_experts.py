@@ -187,6 +187,11 @@ CASES = [
     ("bf16_unaligned", 40, 2, 4, 136, 200, "bf16", _capi.PATH_SIMT),
     ("decode_i1408", 6, 2, 8, 256, 1408, "bf16", _capi.PATH_MFMA_SKINNY),
     ("decode_unaligned_k", 4, 2, 4, 160, 96, "bf16", _capi.PATH_SIMT),
+    # many small experts, top-8 (Qwen3-MoE 128 experts; 256 is the library's maximum)
+    ("e128_k8_prefill", 2048, 8, 128, 512, 256, "bf16", _capi.PATH_MFMA_TILED),
+    ("e128_k8_half_tiles", 600, 8, 128, 512, 256, "bf16", _capi.PATH_MFMA_TILED128),
+    ("e256_k8_half_tiles", 1024, 8, 256, 256, 256, "bf16", _capi.PATH_MFMA_TILED128),
+    ("e256_k8_decode", 4, 8, 256, 256, 128, "bf16", _capi.PATH_MFMA_SKINNY),
 ]
 
 

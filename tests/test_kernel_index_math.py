@@ -431,6 +431,11 @@ TILED_CASES = [
      lambda: _ids_of([257, 300, 513, 700, 1025, 1, 32, 255, 1200, 1200, 1200])),
     ("balanced_e16", 3078, 512, 1536, 16,
      lambda: _ids_of([29, 94, 140, 187, 257, 281, 369, 514, 1, 33, 64, 97, 128, 160, 224, 500])),
+    # the many-expert top-8 cases of the GPU expert tests (same routing)
+    ("e128_k8_prefill", 2048, 512, 256, 128, lambda: skewed_ids(2048, 8, 128, seed=2048, skew=1.0)),
+    ("e128_k8_half_tiles", 600, 512, 256, 128, lambda: skewed_ids(600, 8, 128, seed=600, skew=1.0)),
+    ("e256_k8_half_tiles", 1024, 256, 256, 256,
+     lambda: skewed_ids(1024, 8, 256, seed=1024, skew=1.0)),
 ]
 
 
