@@ -572,3 +572,38 @@ def test_zero_tokens_on_every_forward_path(mode, dev, monkeypatch):
         return  # host experts on int8 codes: checked against the int8 oracle in test_gpu_split
     ref = oracle.fused_experts(x, w1, w2, rw.cpu().numpy(), rids.cpu().numpy())
     assert oracle.max_rel(got, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("E,K,renorm,T", [(128, 8, True, 300), (128, 8, False, 5), (256, 8, True, 64)])
+def test_many_experts_layer_matches_oracle(E, K, renorm, T, dev):
+    """Many small experts with top-8 (Qwen3-MoE's 128, the library's maximum
+    of 256), with and without renormalised weights, through FusedMoE.forward:
+    routing bit-exact on the layer's own fp32 logits except near-ties, output
+    within the bf16 bar of the oracle on the layer's routing."""
+    banner(f"FusedMoE E={E} K={K} renorm={renorm} T={T}")
+    H, I, dtype = 512, 256, torch.bfloat16
+    moe = FusedMoE(num_experts=E, top_k=K, hidden_size=H, intermediate_size=I, dtype=dtype,
+                   renormalize=renorm)
+    layer = synth.make_layer(synth.MoEShape("t", H, E, K, I), dtype, seed=E + T, sigma_w=0.02)
+    sd = {"gate.weight": layer["gate"]}
+    for e in range(E):
+        sd[f"experts.{e}.gate_proj.weight"] = layer["w1"][e][:I]
+        sd[f"experts.{e}.up_proj.weight"] = layer["w1"][e][I:]
+        sd[f"experts.{e}.down_proj.weight"] = layer["w2"][e]
+    moe.load_state_dict(sd)
+    gate = moe.gate.detach().clone()
+    moe = moe.to(dev)
+    x = synth.make_tokens(T, H, dtype, seed=T)
+    out = moe(x.to(dev))
+    rw, rids = moe.route(x.to(dev))
+    torch.cuda.synchronize()
+    lg = oracle.router_logits(x, gate, None, round_mode=1)
+    ow, oids = oracle.topk(lg, K, renorm)
+    assert (rids.cpu().numpy() == oids).all(1).mean() > 0.95
+    if not renorm:
+        # softmax over all experts, not renormalised: the kept weights sum below 1
+        assert float(rw.sum(1).max()) < 1.0
+    ref = oracle.fused_experts(x, layer["w1"], layer["w2"], rw.cpu().numpy(), rids.cpu().numpy())
+    err = oracle.max_rel(out.float().cpu().numpy(), ref)
+    print(f"  max_rel {err:.2e}", flush=True)
+    assert err <= TOL[dtype]
