@@ -479,13 +479,14 @@ int run_fused(const moe355_plan& p, const void* x, const void* const* w1, const 
               const int32_t* expert_map, int map_len, int act, void* out, int accumulate_f32,
               void* workspace, void* stream) {
   int rc;
-  if (p.path == MOE355_PATH_MFMA_SKINNY && p.rows <= 16 && p.E <= 32) {
-    // Decode sizes: the gate_up workgroups group the routed slots themselves
-    // (one launch fewer; the permute's outputs are still written for down and
-    // combine). Every workgroup pays the grouping (one round per distinct
-    // expert) before its weight stream, and a CU runs several workgroups in
-    // turn, so this pays only for a few slots over few experts: Mixtral one
-    // token 124.6 -> 122.7 us; 64 experts top-6 at 8 tokens went 132 -> 150.
+  if (p.path == MOE355_PATH_MFMA_SKINNY && p.rows <= 64) {
+    // Decode sizes (<= 64 routed slots, one wave's worth): the gate_up
+    // workgroups group the routed slots themselves (one launch fewer; the
+    // permute's outputs are still written for down and combine). Every
+    // workgroup pays the grouping before its weight stream: a few LDS
+    // operations and one wave scan, whatever the number of distinct experts
+    // (an earlier form took one round per distinct expert, which made 64
+    // experts top-6 at 8 tokens 132 -> 150 us, so it ran only up to 16 slots).
     PermuteArgs pa;
     if ((rc = permute_args(&p, topk_ids, ids_int64, expert_map, map_len, workspace, &pa))) return rc;
     if ((rc = gate_up_impl(&p, x, w1, act, workspace, stream, &pa))) return rc;

@@ -69,68 +69,95 @@ __device__ __forceinline__ u32x4 load16_stream(const void* p) {
 
 // Grouping of <= 64 routed slots by one wave, the same stable counting sort
 // as the permute kernels (experts ascending, slots ascending within an
-// expert): lane s holds slot s. Distinct experts are taken in ascending order
-// (at most 64 rounds of a wave minimum and a ballot). Returns, for token tile
-// ttile, its expert, first row and row end in meta[1..3] and the tile count
-// in meta[0]; rowsrc[row] = source token of each permuted row. With
-// write_global the wave also writes the permute's outputs (offsets,
-// slot_to_row, row_src, tile_map with kRows-row tiles) for the later stages.
-__device__ void group_small(const PermuteArgs& pa, int ttile, bool write_global, int* meta,
-                            int* rowsrc, int* dist_e, int* dist_start) {
+// expert): lane s holds slot s. Each slot ORs its bit into its expert's 64-bit
+// mask in LDS; an expert's row count is its mask's popcount and a slot's rank
+// among its expert's slots the popcount of the mask bits below it, so no step
+// depends on how many distinct experts there are. Lane l owns experts 4 l ..
+// 4 l + 3 (E <= 256); one wave scan gives every expert's first row and first
+// tile. Returns, for token tile ttile, its expert, first row and row end in
+// meta[1..3] and the tile count in meta[0]; rowsrc[row] = source token of each
+// permuted row. With write_global the wave also writes the permute's outputs
+// (offsets, slot_to_row, row_src, tile_map with kRows-row tiles in expert
+// order) for the later stages.
+constexpr int kGroupExpertsPerLane = 4;
+static_assert(kGroupExpertsPerLane * kWave >= kMaxExperts, "experts per lane");
+
+__device__ void group_slots(const PermuteArgs& pa, int ttile, bool write_global, int* meta,
+                            int* rowsrc, unsigned long long* emask, int* estart) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int e = lane < pa.R ? routed_expert(pa, lane) : -1;
-  const unsigned long long lt_mask = (1ull << lane) - 1ull;
-  unsigned long long todo = __ballot(e >= 0);
-  int row = -1, start = 0, tstart = 0, nd = 0;
-  int te = -1, trow0 = 0, tend = 0;
-  while (todo) {
-    int emin = ((todo >> lane) & 1ull) ? e : INT_MAX;
+  constexpr int P = kGroupExpertsPerLane;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) emin = min(emin, __shfl_xor(emin, o, kWave));
-    const unsigned long long m = __ballot(e == emin);
-    const int cnt = __popcll(m), nt = (cnt + kRows - 1) / kRows;
-    if (e == emin) row = start + __popcll(m & lt_mask);
-    if (ttile >= tstart && ttile < tstart + nt) {
-      te = emin;
-      trow0 = start + (ttile - tstart) * kRows;
-      tend = min(trow0 + kRows, start + cnt);
-    }
-    if (write_global && lane < nt) {
-      pa.tile_map[2 + 2 * (tstart + lane)] = emin;
-      pa.tile_map[3 + 2 * (tstart + lane)] = start + lane * kRows;
-    }
-    if (lane == 0) {
-      dist_e[nd] = emin;
-      dist_start[nd] = start;
-    }
-    ++nd;
-    start += cnt;
-    tstart += nt;
-    todo &= ~m;
+  for (int i = 0; i < P; ++i) emask[P * lane + i] = 0ull;
+  const int e = lane < pa.R ? routed_expert(pa, lane) : -1;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (e >= 0) atomicOr(&emask[e], 1ull << lane);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // this lane's experts: row counts and tile counts, then exclusive scans
+  int cnt[P], nt[P], rows = 0, tiles = 0;
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int x = P * lane + i;
+    cnt[i] = x < pa.E ? __popcll(emask[x]) : 0;
+    nt[i] = (cnt[i] + kRows - 1) / kRows;
+    rows += cnt[i];
+    tiles += nt[i];
   }
-  if (row >= 0) rowsrc[row] = lane / pa.K;
+  int rscan = rows, tscan = tiles;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int rv = __shfl_up(rscan, o, kWave), tv = __shfl_up(tscan, o, kWave);
+    if (lane >= o) {
+      rscan += rv;
+      tscan += tv;
+    }
+  }
+  const int total_rows = __shfl(rscan, kWave - 1, kWave);
+  const int total_tiles = __shfl(tscan, kWave - 1, kWave);
+  int rstart = rscan - rows, tstart = tscan - tiles;
   if (lane == 0) {
-    meta[0] = tstart;
-    meta[1] = te;
-    meta[2] = trow0;
-    meta[3] = tend;
+    meta[0] = total_tiles;
+    meta[1] = -1;
+    meta[2] = 0;
+    meta[3] = 0;
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int x = P * lane + i;
+    if (x < pa.E) {
+      estart[x] = rstart;
+      if (ttile >= tstart && ttile < tstart + nt[i]) {
+        const int r0 = rstart + (ttile - tstart) * kRows;
+        meta[1] = x;
+        meta[2] = r0;
+        meta[3] = min(r0 + kRows, rstart + cnt[i]);
+      }
+      if (write_global) {
+        pa.offsets[x] = rstart;
+        for (int j = 0; j < nt[i]; ++j) {
+          pa.tile_map[2 + 2 * (tstart + j)] = x;
+          pa.tile_map[3 + 2 * (tstart + j)] = rstart + j * kRows;
+        }
+      }
+    }
+    rstart += cnt[i];
+    tstart += nt[i];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  const int row = e >= 0 ? estart[e] + __popcll(emask[e] & lt_mask) : -1;
+  if (row >= 0) rowsrc[row] = lane / pa.K;
   if (!write_global) return;
   if (lane < pa.R) pa.slot_to_row[lane] = row;
   if (row >= 0) pa.row_src[row] = lane / pa.K;
   if (lane == 0) {
-    pa.tile_map[0] = tstart;
+    pa.offsets[pa.E] = total_rows;
+    pa.tile_map[0] = total_tiles;
     pa.tile_map[1] = kRows;
-  }
-  // offsets[x] = rows of experts below x: the start of the first present
-  // expert >= x (the distinct experts are ascending), else the total.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  for (int x = lane; x <= pa.E; x += kWave) {
-    int off = start;
-    for (int d = nd - 1; d >= 0; --d)
-      if (dist_e[d] >= x) off = dist_start[d];
-    pa.offsets[x] = off;
   }
 }
 
@@ -145,12 +172,13 @@ __global__ __launch_bounds__(kThreads) void ffn_skinny_kernel(const FfnArgs a) {
   const int group = blockIdx.x * kWavesPerBlock + wave;
   const int ttile = blockIdx.y, split = blockIdx.z;
   int e, row0, row_end;
-  __shared__ int s_meta[4], s_rowsrc[kWave], s_dist_e[kWave], s_dist_start[kWave];
+  __shared__ int s_meta[4], s_rowsrc[kWave], s_estart[kGroupExpertsPerLane * kWave];
+  __shared__ unsigned long long s_emask[kGroupExpertsPerLane * kWave];
   if (kSelfPermute) {
     // Every wave reaches the barrier before any returns.
     if (wave == 0)
-      group_small(a.perm, ttile, blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0, s_meta,
-                  s_rowsrc, s_dist_e, s_dist_start);
+      group_slots(a.perm, ttile, blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0, s_meta,
+                  s_rowsrc, s_emask, s_estart);
     __syncthreads();
     if (ttile >= s_meta[0] || group >= a.n_wtiles) return;
     e = s_meta[1];

@@ -97,26 +97,27 @@ def test_permute_bit_exact(T, K, E, ids64, drop, dev):
 
 
 @pytest.mark.parametrize("T,K,E,ids64,drop", [
-    # grouped inside gate_up (<= 16 slots over <= 32 experts)
+    # grouped inside gate_up (<= 64 routed slots)
     (1, 2, 8, False, False), (8, 2, 8, True, True), (4, 4, 32, False, True),
-    (5, 3, 16, True, False), (2, 8, 32, False, False),
-    # permute launch, same checks
-    (16, 2, 8, True, True), (32, 2, 8, False, False), (8, 6, 64, True, False),
-    (8, 8, 256, True, True), (3, 6, 64, False, True),
+    (5, 3, 16, True, False), (2, 8, 32, False, False), (16, 2, 8, True, True),
+    (32, 2, 8, False, False), (8, 6, 64, True, False), (8, 8, 256, True, True),
+    (3, 6, 64, False, True), (64, 1, 8, False, False), (16, 4, 16, True, True),
+    # permute launch (more than 64 slots), same checks
+    (16, 6, 64, False, False), (12, 8, 256, True, True),
 ])
 def test_decode_grouping_inside_gate_up_bit_exact(T, K, E, ids64, drop, dev):
-    """At decode sizes (skinny path, <= 16 routed slots over <= 32 experts)
-    fused_experts skips the permute launch: the gate_up workgroups group the
-    slots themselves and workgroup 0 writes the permute's outputs. Those
-    outputs must equal the oracle's grouping bit for bit, and the layer output
-    (also accumulated into fp32) the staged path's (larger cases take the
-    permute launch and are held to the same checks)."""
+    """At decode sizes (skinny path, <= 64 routed slots) fused_experts skips
+    the permute launch: the gate_up workgroups group the slots themselves and
+    workgroup 0 writes the permute's outputs. Those outputs must equal the
+    oracle's grouping bit for bit, and the layer output (also accumulated into
+    fp32) the staged path's (larger cases take the permute launch and are held
+    to the same checks)."""
     H, I = 256, 256
     banner(f"decode grouping in gate_up T={T} K={K} E={E} ids64={ids64} drop={drop}")
     ids = skewed_ids(T, K, E, seed=T * E + K, skew=1.2)
     emap = [(-1 if e % 5 == 3 else e) for e in range(E)] if drop else None
     plan = _capi.make_plan(T, H, I, E, K, _capi.BF16)
-    assert plan.path == _capi.PATH_MFMA_SKINNY and plan.rows <= 64
+    assert plan.path == _capi.PATH_MFMA_SKINNY
     w1, w2 = make_bank(E, H, I, torch.bfloat16, seed=T + E)
     w1d = [w.to(dev).contiguous() for w in w1]
     w2d = [w.to(dev).contiguous() for w in w2]
@@ -146,7 +147,7 @@ def test_decode_grouping_inside_gate_up_bit_exact(T, K, E, ids64, drop, dev):
     counts = np.diff(offsets)
     # the in-kernel grouping lists the experts by id, the permute launch in
     # the interleaved size order
-    order = range(E) if R <= 16 and E <= 32 else tile_order(counts)
+    order = range(E) if R <= 64 else tile_order(counts)
     want = [(e, offsets[e] + j * tile_height(counts[e], plan.tile_rows)) for e in order
             for j in range(-(-counts[e] // plan.tile_rows))]
     tm = read_ws(plan, ws, plan.off_tile_map, 2 + 2 * plan.max_tiles)

@@ -24,8 +24,9 @@ addresses, before any of it runs on a GPU:
     zero-filled padding row, and every valid row is read; token and weight
     offsets stay in their 32-bit buffer ranges.
   * the weight-streaming kernel's in-kernel grouping (ffn_skinny.hip,
-    group_small): its outputs must equal the permute's, and every tile it
-    hands a workgroup must lie inside one expert's rows.
+    group_slots): its outputs must equal the permute's, every LDS, meta and
+    global index must stay in its array, and every tile it hands a workgroup
+    must lie inside one expert's rows.
 
 Shapes: the workloads the throughput figures are quoted on (Mixtral 1, 16,
 256 and 4096 tokens; Phi-3.5 2048 with Zipf-skewed routing; the fine-grained
@@ -467,56 +468,110 @@ def test_tiled_schedule_on_other_cu_counts(cus):
 
 
 # --------------------------------------------------- skinny in-kernel grouping
-def emulate_group_small(ids, E, emap=None, rows=16):
-    """Replays group_small: one wave groups <= 64 slots (lane s = slot s)."""
+GROUP_PER_LANE = 4  # kGroupExpertsPerLane
+
+
+def emulate_group_slots(ids, E, max_tiles, emap=None, rows=16, ttile=0):
+    """Replays group_slots: one wave groups <= 64 slots (lane s = slot s)
+    through per-expert 64-bit slot masks in LDS, lane l owning experts
+    4 l .. 4 l + 3, with every LDS, meta and global index checked against
+    its array."""
     T, K = ids.shape
     R = T * K
-    assert R <= WAVE
+    assert R <= WAVE and E <= GROUP_PER_LANE * WAVE
+    emask = [None] * (GROUP_PER_LANE * WAVE)   # LDS: unset until zeroed
+    estart = [None] * (GROUP_PER_LANE * WAVE)
+    rowsrc = [None] * WAVE
+    for lane in range(WAVE):
+        for i in range(GROUP_PER_LANE):
+            emask[GROUP_PER_LANE * lane + i] = 0
     e = np.full(WAVE, -1, np.int64)
     e[:R] = _routed(ids.reshape(-1), emap, E)
-    todo = e >= 0
-    start = tstart = 0
+    for lane in range(WAVE):
+        if e[lane] >= 0:
+            assert 0 <= e[lane] < len(emask)
+            emask[e[lane]] |= 1 << lane
+    cnt = np.zeros((WAVE, GROUP_PER_LANE), np.int64)
+    for lane in range(WAVE):
+        for i in range(GROUP_PER_LANE):
+            x = GROUP_PER_LANE * lane + i
+            cnt[lane, i] = bin(emask[x]).count("1") if x < E else 0
+    nt = -(-cnt // rows)
+    rows_l, tiles_l = cnt.sum(1), nt.sum(1)
+    rstart0 = np.concatenate([[0], np.cumsum(rows_l)[:-1]])
+    tstart0 = np.concatenate([[0], np.cumsum(tiles_l)[:-1]])
+    total_rows, total_tiles = int(rows_l.sum()), int(tiles_l.sum())
+    assert total_tiles <= max_tiles
+    offsets = np.full(E + 1, POISON, np.int64)
+    tile_map = {}
+    meta = [total_tiles, -1, 0, 0]
+    hits = 0
+    for lane in range(WAVE):
+        rs, ts = int(rstart0[lane]), int(tstart0[lane])
+        for i in range(GROUP_PER_LANE):
+            x = GROUP_PER_LANE * lane + i
+            if x < E:
+                estart[x] = rs
+                if ts <= ttile < ts + nt[lane, i]:
+                    r0 = rs + (ttile - ts) * rows
+                    meta[1:] = [x, r0, min(r0 + rows, rs + int(cnt[lane, i]))]
+                    hits += 1
+                offsets[x] = rs
+                for j in range(int(nt[lane, i])):
+                    assert 2 + 2 * (ts + j) + 1 < 2 + 2 * max_tiles
+                    tile_map[ts + j] = (x, rs + j * rows)
+            rs += int(cnt[lane, i])
+            ts += int(nt[lane, i])
+    assert hits == (1 if ttile < total_tiles else 0)
+    offsets[E] = total_rows
     slot_to_row = np.full(R, -1, np.int64)
     row_src = {}
-    tile_map = []
-    dist = []
-    while todo.any():
-        emin = int(e[todo].min())
-        m = e == emin
-        cnt = int(m.sum())
-        nt = -(-cnt // rows)
-        lanes = np.nonzero(m)[0]
-        for rk, ln in enumerate(lanes):
-            slot_to_row[ln] = start + rk
-            assert start + rk not in row_src
-            row_src[start + rk] = ln // K
-        for j in range(nt):
-            tile_map.append((emin, start + j * rows))
-        dist.append((emin, start))
-        start += cnt
-        tstart += nt
-        todo &= ~m
-    offsets = np.empty(E + 1, np.int64)
-    for x in range(E + 1):
-        off = start
-        for de, ds in reversed(dist):
-            if de >= x:
-                off = ds
-        offsets[x] = off
-    return offsets, slot_to_row, row_src, tile_map
+    for lane in range(WAVE):
+        if e[lane] < 0:
+            continue
+        assert estart[e[lane]] is not None
+        below = emask[e[lane]] & ((1 << lane) - 1)
+        row = estart[e[lane]] + bin(below).count("1")
+        assert 0 <= row < total_rows <= R <= len(rowsrc)
+        assert row not in row_src
+        rowsrc[row] = lane // K
+        row_src[row] = lane // K
+        slot_to_row[lane] = row
+    return offsets, slot_to_row, row_src, [tile_map[j] for j in range(total_tiles)], meta
 
 
 @pytest.mark.parametrize("T,K,E,drop", [(1, 2, 8, False), (8, 2, 8, True), (4, 4, 32, True),
-                                        (2, 8, 32, False), (5, 3, 16, False)])
+                                        (2, 8, 32, False), (5, 3, 16, False), (16, 2, 8, False),
+                                        (32, 2, 8, True), (8, 6, 64, False), (8, 8, 256, True),
+                                        (3, 6, 64, True), (20, 3, 8, False), (64, 1, 8, False),
+                                        (16, 4, 16, True)])
 def test_skinny_grouping_equals_permute_and_stays_in_bounds(T, K, E, drop):
     ids = skewed_ids(T, K, E, seed=T * E + K, skew=1.2)
     emap = [(-1 if x % 5 == 3 else x) for x in range(E)] if drop else None
     plan = _capi.make_plan(T, 4096, 14336, E, K, _capi.BF16)
-    assert plan.path == _capi.PATH_MFMA_SKINNY and plan.rows <= 16 and E <= 32
-    offsets, s2r, rsrc, tmap = emulate_group_small(ids, E, emap)
+    assert plan.path == _capi.PATH_MFMA_SKINNY and plan.rows <= 64
     o_off, o_s2r, o_src = oracle.permute(ids, E, emap)
-    assert np.array_equal(offsets, o_off) and np.array_equal(s2r, o_s2r)
-    assert all(o_src[r] == t for r, t in rsrc.items())
-    assert len(tmap) <= plan.max_tiles
-    for (e, row0) in tmap:  # each tile inside its expert's rows
-        assert o_off[e] <= row0 < o_off[e + 1]
+    for ttile in range(plan.max_tiles):
+        offsets, s2r, rsrc, tmap, meta = emulate_group_slots(ids, E, plan.max_tiles, emap,
+                                                             ttile=ttile)
+        assert np.array_equal(offsets, o_off) and np.array_equal(s2r, o_s2r)
+        assert all(o_src[r] == t for r, t in rsrc.items()) and len(rsrc) == o_off[-1]
+        for (e, row0) in tmap:  # each tile inside its expert's rows, in expert order
+            assert o_off[e] <= row0 < o_off[e + 1]
+        assert [e for e, _ in tmap] == sorted(e for e, _ in tmap)
+        if ttile < meta[0]:  # the workgroup's tile is the map's
+            e, r0, r1 = meta[1:]
+            assert tmap[ttile] == (e, r0) and r0 < r1 <= o_off[e + 1]
+
+
+def test_skinny_grouping_fine_grained_decode_with_shared_columns():
+    """The fine-grained layer at 8 tokens: 6 routed slots and the 2 shared
+    columns per token, 64 slots over 66 experts (one wave's worth)."""
+    ids = _finegrained_ids(8)
+    plan = _capi.make_plan(8, 2048, 1408, 66, 8, _capi.BF16)
+    assert plan.path == _capi.PATH_MFMA_SKINNY and plan.rows == 64
+    o_off, o_s2r, o_src = oracle.permute(ids, 66)
+    for ttile in range(plan.max_tiles):
+        offsets, s2r, rsrc, tmap, meta = emulate_group_slots(ids, 66, plan.max_tiles, ttile=ttile)
+        assert np.array_equal(offsets, o_off) and np.array_equal(s2r, o_s2r)
+        assert all(o_src[r] == t for r, t in rsrc.items())
