@@ -125,7 +125,7 @@ int moe355_make_plan_path(int T, int H, int I, int E, int K, int dtype, int path
   std::memset(p, 0, sizeof(*p));
   p->T = T; p->H = H; p->I = I; p->E = E; p->K = K; p->dtype = dtype;
   p->rows = static_cast<int>(R);
-  p->n_blocks = static_cast<int>((R + kPermuteChunk - 1) / kPermuteChunk);
+  p->n_blocks = R <= kPermuteSingleMax ? 1 : static_cast<int>((R + kPermuteChunk - 1) / kPermuteChunk);
   const int act_e = static_cast<int>(R < E ? (R > 0 ? R : 1) : E);
   const long long avg = R / act_e;
 

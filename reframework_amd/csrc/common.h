@@ -27,7 +27,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 constexpr int kMaxExperts = MOE355_MAX_EXPERTS;
-constexpr int kPermuteChunk = 1024;  // routed slots per permute block
+constexpr int kPermuteChunk = 256;       // routed slots per block of the count + scatter launches
+constexpr int kPermuteSingleMax = 1024;  // up to this many slots one block does the whole permute
 
 // ---------------------------------------------------------------- conversions
 template <typename T>

@@ -4,7 +4,9 @@
 // which visits experts in ascending id and, inside an expert, slots in
 // ascending flat (t,k) order. Two launches, no host round trip:
 //   1. count:   each block histograms kPermuteChunk slots into LDS and writes
-//               its per-expert counts;
+//               its per-expert counts (256 slots a block, one per thread: at
+//               1024 a block ranked its slots in four dependent rounds, and
+//               the scatter of 8192 slots ran on 8 CUs);
 //   2. scatter: each block rebuilds the global expert starts and its own
 //               prefix from the count table, ranks its slots stably with
 //               wavefront ballots, and writes slot_to_row / row_src. Block 0
@@ -18,7 +20,8 @@ namespace moe355 {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRounds = kPermuteChunk / kThreads;
+constexpr int kRounds = kPermuteChunk / kThreads;            // count + scatter launches
+constexpr int kSingleRounds = kPermuteSingleMax / kThreads;  // the one-block permute
 constexpr int kWaves = kThreads / kWave;
 static_assert(kMaxExperts <= 256, "the scatter ranks slots by the 8 bits of the expert id");
 
@@ -39,8 +42,8 @@ __global__ __launch_bounds__(kThreads) void count_kernel(const PermuteArgs a) {
   for (int e = tid; e < a.E; e += kThreads) a.block_counts[b * a.E + e] = hist[e];
 }
 
-// kSingle: all slots fit one block (decode sizes); the block counts them itself
-// and the separate count launch is skipped.
+// kSingle: all slots fit one block (up to kPermuteSingleMax); the block counts
+// them itself and the separate count launch is skipped.
 template <bool kSingle>
 __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) {
   __shared__ int base[kMaxExperts];     // first row of this block's slots of expert e
@@ -59,7 +62,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
+    for (int r = 0; r < kSingleRounds; ++r) {
       const int slot = r * kThreads + tid;
       if (slot < a.R) {
         const int e = routed_expert(a, slot);
@@ -210,7 +213,8 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(const PermuteArgs a) 
 
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
   // Rounds past the last routed slot have nothing to rank.
-  for (int r = 0; r < kRounds && b * kPermuteChunk + r * kThreads < a.R; ++r) {
+  constexpr int rounds = kSingle ? kSingleRounds : kRounds;
+  for (int r = 0; r < rounds && b * kPermuteChunk + r * kThreads < a.R; ++r) {
     for (int i = tid; i < kWaves * a.E; i += kThreads) wave_cnt[i / a.E][i % a.E] = 0;
     __syncthreads();
     const int slot = b * kPermuteChunk + r * kThreads + tid;

@@ -45,8 +45,8 @@ from reframework_amd import _capi
 
 WAVE, THREADS = 64, 256
 WAVES = THREADS // WAVE
-CHUNK = 1024          # kPermuteChunk
-ROUNDS = CHUNK // THREADS
+CHUNK = 256           # kPermuteChunk: slots per block of the count + scatter launches
+SINGLE_MAX = 1024     # kPermuteSingleMax: up to this many slots one block permutes
 POISON = -(1 << 40)   # an LDS word nobody wrote
 
 
@@ -103,11 +103,12 @@ def emulate_permute(ids, E, tile_rows, max_tiles, emap=None, zero_first_row_only
     T, K = ids.shape
     R = T * K
     e_of = _routed(ids.reshape(-1), emap, E)
-    n_blocks = -(-R // CHUNK)
-    counts = np.zeros((n_blocks, E), np.int64)  # count_kernel
+    n_blocks = 1 if R <= SINGLE_MAX else -(-R // CHUNK)
+    rounds = SINGLE_MAX // THREADS if n_blocks == 1 else CHUNK // THREADS
+    counts = np.zeros((n_blocks, E), np.int64)  # count_kernel (or the one block's own count)
     for s in range(R):
         if e_of[s] >= 0:
-            counts[s // CHUNK, e_of[s]] += 1
+            counts[0 if n_blocks == 1 else s // CHUNK, e_of[s]] += 1
     slot_to_row = np.full(R, POISON, np.int64)
     row_src = np.full(R, POISON, np.int64)
     offsets = tile_map = None
@@ -141,7 +142,7 @@ def emulate_permute(ids, E, tile_rows, max_tiles, emap=None, zero_first_row_only
                 tile_map += [e, int(start[e] + (j - place_start[lo]) * h)]
         wave_cnt = np.full((WAVES, 256), POISON, np.int64)  # LDS at kernel start
         r = 0
-        while r < ROUNDS and b * CHUNK + r * THREADS < R:
+        while r < rounds and b * CHUNK + r * THREADS < R:
             # per-round zeroing, as the kernel indexes it
             for i in range(WAVES * E):
                 if zero_first_row_only:
@@ -215,6 +216,7 @@ def test_permute_emulation_in_bounds_and_equal_to_oracle(name, make, E, emap):
     ids = make()
     T, K = ids.shape
     plan = _capi.make_plan(T, 4096, 14336, E, K, _capi.BF16)
+    assert plan.n_blocks == (1 if T * K <= SINGLE_MAX else -(-T * K // CHUNK))
     offsets, s2r, src, tile_map = emulate_permute(ids, E, plan.tile_rows, plan.max_tiles, emap)
     o_off, o_s2r, o_src = oracle.permute(ids, E, emap)
     assert np.array_equal(offsets, o_off)
