@@ -577,3 +577,31 @@ def test_skinny_grouping_fine_grained_decode_with_shared_columns():
         offsets, s2r, rsrc, tmap, meta = emulate_group_slots(ids, 66, plan.max_tiles, ttile=ttile)
         assert np.array_equal(offsets, o_off) and np.array_equal(s2r, o_s2r)
         assert all(o_src[r] == t for r, t in rsrc.items())
+
+
+# ------------------------------------------------ random shapes (CPU replay)
+import _random_shapes  # noqa: E402
+
+
+@pytest.mark.parametrize("c", _random_shapes.ALL, ids=_random_shapes.name)
+def test_random_shapes_index_math_in_bounds(c):
+    """The configurations of tests/test_gpu_random_shapes.py, replayed here
+    first: the permute (or the in-kernel grouping at <= 64 slots) equal to the
+    oracle's grouping and in bounds, and the tiled schedules covering every
+    item once within their buffers."""
+    T, K, E = c["T"], c["K"], c["E"]
+    ids = skewed_ids(T, K, E, c["seed"], c["skew"])
+    emap = c["emap"]
+    plan = _capi.make_plan(T, c["H"], c["I"], E, K, _random_shapes.DTYPES[c["dt"]])
+    o_off, o_s2r, _ = oracle.permute(ids, E, emap)
+    if plan.path == _capi.PATH_MFMA_SKINNY and plan.rows <= 64:
+        for t in range(plan.max_tiles):
+            offsets, s2r, _, _, _ = emulate_group_slots(ids, E, plan.max_tiles, emap, ttile=t)
+            assert np.array_equal(offsets, o_off) and np.array_equal(s2r, o_s2r)
+    else:
+        offsets, s2r, _, _ = emulate_permute(ids, E, plan.tile_rows, plan.max_tiles, emap)
+        assert np.array_equal(offsets, o_off) and np.array_equal(s2r, o_s2r)
+    if plan.path in (_capi.PATH_MFMA_TILED, _capi.PATH_MFMA_TILED128):
+        counts = np.diff(o_off)
+        emulate_tiled(counts, plan, True)
+        emulate_tiled(counts, plan, False)
