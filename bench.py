@@ -719,8 +719,8 @@ def config_norm_router(dev, steps, warmup, tokens=(1, 16, 4096)):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build runs the MoE layer on a single MI355X "
-              "(expert sharding across GPUs is described in DESIGN.md, not launched).",
+        print("bench.py measures one GPU: the MoE layer runs on a single MI355X; sharding "
+              "experts across GPUs is designed but not implemented, so --gpus N > 1 is refused.",
               file=sys.stderr)
         sys.exit(2)
     import torch
