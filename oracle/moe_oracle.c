@@ -2,8 +2,8 @@
  * moe_oracle.c — CPU restatement of Reframework's MoE layer forward.
  *
  * TEST INFRASTRUCTURE ONLY. The parity tests, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the checker
- * (or the timed CPU baseline). The product (reframework_amd, libmoe355) never
+ * cpu_baseline leg of bench.py may load this library, and only as the oracle
+ * the results are compared against (or the timed CPU baseline). The product (reframework_amd, libmoe355) never
  * calls it.
  *
  * Every function restates the reference algorithm in double precision, from

@@ -1,7 +1,8 @@
 """Python side of the CPU oracle (test infrastructure only).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-this module, and only as the checker (or the timed CPU baseline). The product
+this module, and only as the oracle results are compared against (or the
+timed CPU baseline). The product
 package never imports it.
 
 ``moe_oracle.c`` holds the fp64 restatement of the reference algorithm; this

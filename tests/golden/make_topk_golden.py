@@ -6,7 +6,7 @@ bits of torch.softmax, are properties of the reference's torch call. This
 script runs that call (reframework/moe/fused.py:32-46) on fixed inputs and
 stores inputs and outputs as a fixture; the tests never import the reference.
 
-Development container only (the reference tree is not on the GPU box):
+Development host only (the reference tree is not present where the GPU tests run):
 
     python tests/golden/make_topk_golden.py
 
