@@ -227,6 +227,10 @@ int moe355_combine(const moe355_plan* plan, const float* topk_w, void* out, int 
  * The whole routed-expert computation: permute, gate_up, down, combine.
  * Replaces fused_experts (reframework/moe/fused.py:49-87); x, w1 and w2 share
  * `dtype`. workspace must hold plan.workspace_bytes (moe355_make_plan).
+ * A slot whose topk_w is exactly 0 is dropped like an unmapped one: it would
+ * add 0 * y. The reference's expert-parallel layer zeroes the weights of
+ * other ranks' experts and maps them to local row 0 (parallel/ep.py:137-143);
+ * those slots then cost nothing here instead of piling onto expert 0.
  */
 int moe355_fused_experts(const void* x, const void* const* w1, const void* const* w2,
                          const float* topk_w, const void* topk_ids, int ids_int64,

@@ -369,7 +369,8 @@ bool ragged_tiles(const moe355_plan* p) {
 // Checks the permute's arguments and fills its kernel arguments (the caller
 // has checked the plan and that it has rows).
 int permute_args(const moe355_plan* p, const void* topk_ids, int ids_int64,
-                 const int32_t* expert_map, int map_len, void* workspace, PermuteArgs* a) {
+                 const int32_t* expert_map, int map_len, void* workspace, PermuteArgs* a,
+                 const float* topk_w = nullptr) {
   if (map_len < 0 || map_len > MOE355_MAX_EXPERTS)
     return fail(MOE355_EUNSUPPORTED, "expert_map length %d outside [0, %d]", map_len,
                 MOE355_MAX_EXPERTS);
@@ -387,6 +388,7 @@ int permute_args(const moe355_plan* p, const void* topk_ids, int ids_int64,
   a->tile_rows = p->tile_rows; a->max_tiles = p->max_tiles;
   a->ids_int64 = ids_int64 != 0; a->map_len = map_len;
   for (int i = 0; i < map_len; ++i) a->map[i] = expert_map[i];
+  a->weights = topk_w;
   return MOE355_OK;
 }
 
@@ -399,14 +401,23 @@ int gate_up_impl(const moe355_plan* p, const void* x, const void* const* w1, int
 
 extern "C" {
 
-int moe355_permute(const moe355_plan* p, const void* topk_ids, int ids_int64,
-                   const int32_t* expert_map, int map_len, void* workspace, void* stream) {
+// The permute; with topk_w (the fused entry points), slots of weight 0 are
+// dropped as well.
+int permute_impl(const moe355_plan* p, const void* topk_ids, int ids_int64,
+                 const int32_t* expert_map, int map_len, const float* topk_w, void* workspace,
+                 void* stream) {
   int rc = check_plan(p);
   if (rc) return rc;
   PermuteArgs a;
-  if ((rc = permute_args(p, topk_ids, ids_int64, expert_map, map_len, workspace, &a))) return rc;
+  if ((rc = permute_args(p, topk_ids, ids_int64, expert_map, map_len, workspace, &a, topk_w)))
+    return rc;
   if (p->rows == 0) return MOE355_OK;
   return check_hip(launch_permute(a, as_stream(stream)), "permute launch");
+}
+
+int moe355_permute(const moe355_plan* p, const void* topk_ids, int ids_int64,
+                   const int32_t* expert_map, int map_len, void* workspace, void* stream) {
+  return permute_impl(p, topk_ids, ids_int64, expert_map, map_len, nullptr, workspace, stream);
 }
 
 int moe355_gate_up(const moe355_plan* p, const void* x, const void* const* w1, int act,
@@ -488,10 +499,12 @@ int run_fused(const moe355_plan& p, const void* x, const void* const* w1, const 
     // (an earlier form took one round per distinct expert, which made 64
     // experts top-6 at 8 tokens 132 -> 150 us, so it ran only up to 16 slots).
     PermuteArgs pa;
-    if ((rc = permute_args(&p, topk_ids, ids_int64, expert_map, map_len, workspace, &pa))) return rc;
+    if ((rc = permute_args(&p, topk_ids, ids_int64, expert_map, map_len, workspace, &pa, topk_w)))
+      return rc;
     if ((rc = gate_up_impl(&p, x, w1, act, workspace, stream, &pa))) return rc;
   } else {
-    if ((rc = moe355_permute(&p, topk_ids, ids_int64, expert_map, map_len, workspace, stream)))
+    if ((rc = permute_impl(&p, topk_ids, ids_int64, expert_map, map_len, topk_w, workspace,
+                           stream)))
       return rc;
     if ((rc = moe355_gate_up(&p, x, w1, act, workspace, stream))) return rc;
   }

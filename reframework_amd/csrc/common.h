@@ -204,12 +204,14 @@ struct PermuteArgs {
   int R, K, E, n_blocks, tile_rows, max_tiles;
   int ids_int64, map_len;  // map_len 0: no map
   int32_t map[kMaxExperts];
+  const float* weights;    // [R] routing weights, or nullptr: a slot of weight 0 is dropped
 };
 
 // Local expert of routed slot `slot`, or -1 when the slot is dropped (an id
 // the optional map sends negative or outside [0, E), or that lies outside the
-// map).
+// map; with weights, a slot of weight exactly 0, which would add 0 * y).
 __device__ __forceinline__ int routed_expert(const PermuteArgs& a, int slot) {
+  if (a.weights && a.weights[slot] == 0.0f) return -1;
   long long id = a.ids_int64 ? static_cast<const int64_t*>(a.ids)[slot]
                              : static_cast<long long>(static_cast<const int32_t*>(a.ids)[slot]);
   if (a.map_len > 0) {

@@ -344,3 +344,38 @@ def test_outputs_are_deterministic(dev):
     a = gpu_fused(x, w1, w2, w, ids)
     b = gpu_fused(x, w1, w2, w, ids)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("T", [4, 40, 700, 2048])
+def test_zero_weight_slots_are_dropped(T, dev):
+    """The reference's expert-parallel layer (parallel/ep.py:137-143) keeps
+    the experts 2-5 of 8 on this rank, maps the others to local row 0 and
+    zeroes their weights. fused_experts drops slots of weight 0: the output
+    equals the oracle's with those slots removed, and expert 0's rows are its
+    own slots only (the grouping inside gate_up at 4 tokens; the one-block
+    permute with 128-row tiles at 40; the multi-block permute with 256-row
+    tiles at 700 and 2048)."""
+    E_all, K, H, I = 8, 2, 256, 512
+    lo, hi = 2, 6
+    E = hi - lo
+    banner(f"zero-weight slots T={T}")
+    ids_g = skewed_ids(T, K, E_all, seed=T, skew=0.5)
+    local = (ids_g >= lo) & (ids_g < hi)
+    ids = np.where(local, ids_g - lo, 0).astype(np.int64)
+    w = np.random.default_rng(T).random((T, K)).astype(np.float32)
+    w_masked = np.where(local, w, 0.0).astype(np.float32)
+    w1, w2 = make_bank(E, H, I, torch.bfloat16, seed=T + 1)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
+    plan = _capi.make_plan(T, H, I, E, K, _capi.BF16)
+    ws = torch.full((plan.workspace_bytes,), 0x5A, dtype=torch.uint8, device=dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    w1d = [t.to(dev).contiguous() for t in w1]
+    w2d = [t.to(dev).contiguous() for t in w2]
+    _capi.fused_experts(x.to(dev), [t.data_ptr() for t in w1d], [t.data_ptr() for t in w2d], I,
+                        torch.from_numpy(w_masked).to(dev), torch.from_numpy(ids).to(dev), 0, out, ws)
+    torch.cuda.synchronize()
+    counts = np.diff(read_ws(plan, ws, plan.off_offsets, E + 1))
+    want = np.bincount((ids_g[local] - lo).reshape(-1), minlength=E)
+    assert np.array_equal(counts, want)
+    ids_dropped = np.where(local, ids, -1)
+    _check(out, x, w1, w2, w_masked, ids_dropped)
