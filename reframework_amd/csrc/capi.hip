@@ -301,7 +301,9 @@ int moe355_add_rmsnorm_router_topk(const void* x, const void* residual, void* re
                                    int K, int dtype, int renormalize, int round_logits,
                                    void* normed_out, float* logits_out, float* topk_w,
                                    int32_t* topk_ids, void* stream) {
-  if (!norm_router_fusable(T, H, E, dtype, logits_out != nullptr)) {
+  const bool mfma = !norm_router_fusable(T, H, E, dtype, logits_out != nullptr) &&
+                    norm_router_mfma_fusable(T, H, E, K, dtype);
+  if (!mfma && !norm_router_fusable(T, H, E, dtype, logits_out != nullptr)) {
     int rc = moe355_add_rmsnorm(x, residual, residual_out, norm_weight, norm_bias, weight_dtype,
                                 eps, T, H, dtype, normed_out, stream);
     if (rc) return rc;
@@ -332,6 +334,9 @@ int moe355_add_rmsnorm_router_topk(const void* x, const void* residual, void* re
   ra.T = T; ra.H = H; ra.E = E; ra.K = K;
   ra.renormalize = renormalize != 0; ra.round_logits = round_logits != 0;
   ra.entropy_k_min = 0; ra.out_ld = K;
+  if (mfma)
+    return check_hip(launch_add_rmsnorm_router_mfma(na, ra, dtype, as_stream(stream)),
+                     "add_rmsnorm_router_mfma launch");
   return check_hip(launch_add_rmsnorm_router(na, ra, dtype, as_stream(stream)),
                    "add_rmsnorm_router launch");
 }

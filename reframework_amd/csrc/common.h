@@ -289,6 +289,15 @@ hipError_t launch_combine(const CombineArgs& a, int out_dtype, hipStream_t s);
 // buffer lets the split router run instead.
 constexpr int kMaxRouterExperts = 64;
 bool norm_router_fusable(int T, int H, int E, int dtype, bool has_logits);
+// Prefill sizes (T >= kNormRouterMfmaMinRows, up to 16 experts): the one-launch
+// norm + MFMA router, bit for bit the norm kernel followed by the MFMA router.
+// It wins from ~2048 rows (H = 4096, 8 experts: 19.3 against 19.8 us at 2048,
+// 28 against 31 us at 4096); below, the two launches of the split path are
+// the faster.
+constexpr int kNormRouterMfmaMinRows = 2048;
+bool norm_router_mfma_fusable(int T, int H, int E, int K, int dtype);
+hipError_t launch_add_rmsnorm_router_mfma(const NormArgs& a, const RouterArgs& ra, int dtype,
+                                          hipStream_t s);
 hipError_t launch_add_rmsnorm_router(const NormArgs& a, const RouterArgs& ra, int dtype,
                                      hipStream_t s);
 hipError_t launch_cast_f32(const float* src, void* dst, size_t n, int dtype, hipStream_t s);

@@ -13,6 +13,7 @@
 #include <climits>
 
 #include "common.h"
+#include "dma_pipe.h"
 
 namespace moe355 {
 namespace {
@@ -363,6 +364,225 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_router_kernel(const Norm
               ra.topk_ids + static_cast<size_t>(t0 + t) * ra.out_ld, lane);
 }
 
+// Workgroup barrier after this wave's LDS accesses have completed; unlike
+// __syncthreads it does not wait for the wave's global loads and stores.
+__device__ __forceinline__ void lds_barrier() {
+  pipe::wait_lgkm0();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+constexpr int kNormRouterRows = 8;  // rows per workgroup of the prefill kernel
+
+// Residual add + RMSNorm + router at prefill sizes, 8 rows per workgroup, up
+// to 16 experts, H a multiple of 256 up to 2048 * CPT. The two-kernel path
+// there (add_rmsnorm_kernel, then the router's router_mfma_kernel) writes the
+// normed rows to HBM and reads them back; here they stay in an LDS tile:
+//   1. every load is issued at once: x rows straight into the tile with
+//      direct-to-LDS loads, residual rows into registers. After one wait,
+//      x + residual rounded to T goes back into the tile, and each thread sums
+//      its squares per row;
+//   2. the gate fragments of phase 3 are loaded (before any store, so that
+//      waiting for them does not wait for the stores); then per row the scale
+//      from the wave sums, and the thread's chunks of the tile go to
+//      residual_out, are scaled by it and the weight (+ bias), rounded to T,
+//      and go to out and back into the tile. Chunks, sums and their order are
+//      add_rmsnorm_kernel's, so residual_out and out are bit for bit its;
+//   3. the router's product with the same MFMA sequence per wave as
+//      router_mfma_kernel for one 16-expert group (wave w over the quarter
+//      [w H/4, (w+1) H/4), 32 k a step, ascending), A fragments from the tile
+//      (fragment rows 8-15 repeat rows 0-7; their results are dropped) and B
+//      fragments of the gate in registers (the gate is L2 resident); the
+//      quarter sums, the rounded logits plus bias and group16_topk follow
+//      that kernel, so logits and routing are bit for bit the two-kernel
+//      path's.
+// Eight rows (a 64 KB tile at H = 4096) let two workgroups share a CU. With
+// sixteen a workgroup had its CU to itself, its reads and its writes never
+// overlapped, and the kernel lost to the two-kernel path (4096 rows, H = 4096,
+// 8 experts: 36 against 31 us; with eight rows 28 us, and 54 against 58 us at
+// 8192 rows).
+// The tile holds row t's 16-byte chunk c at slot c ^ t of its row (rows
+// 2048 * CPT elements apart): the lanes of an MFMA fragment read its rows at
+// one chunk from distinct slots of one 128-byte span (conflict free). The
+// lane of thread tid fills slot tid + 256 c of each row, so the chunk a
+// thread works on in phases 1 and 2 (slot (tid + 256 c) ^ t) was loaded by
+// lane tid ^ t of its own wave: waiting for the wave's own loads suffices.
+// Slots past the row end (rows are the largest H apart) load zeros without
+// touching memory. Rows past T load the last row again and are not stored;
+// their logits are not written. Barriers wait for LDS only (s_waitcnt
+// lgkmcnt(0) + s_barrier): __syncthreads would also wait for the global
+// stores and the gate loads in flight.
+template <typename T, typename W, int CPT>
+__global__ __launch_bounds__(kThreads) void add_rmsnorm_router_mfma_kernel(const NormArgs a,
+                                                                           const RouterArgs ra) {
+  constexpr int N = Vec16<T>::N;  // elements per 16-byte chunk
+  constexpr int kTok = kNormRouterRows, kWaves = kThreads / kWave;
+  constexpr int kMaxH = CPT * kThreads * N;
+  constexpr int kPitch = kMaxH * static_cast<int>(sizeof(T));  // tile row, bytes
+  constexpr int kMaxB = kMaxH / 256;      // 64-k batches of a wave's quarter
+  __shared__ __attribute__((aligned(1024))) uint8_t tile[kTok * kPitch];
+  __shared__ float red[kTok][kWaves];
+  __shared__ float part[kWaves][16][16];
+  __shared__ float lg[kTok][16];
+  static_assert(sizeof(tile) + sizeof(red) + sizeof(part) + sizeof(lg) <= 160 * 1024, "LDS");
+
+  const int t0 = blockIdx.x * kTok, ntok = min(kTok, a.T - t0);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int chunks = a.H / N;
+  const uint32_t rowbytes = static_cast<uint32_t>(a.H) * sizeof(T);
+  const bool has_res = a.residual != nullptr;
+  auto slot = [&](int t, int ch) -> u32x4* {
+    return reinterpret_cast<u32x4*>(tile + t * kPitch + ((ch ^ t) << 4));
+  };
+
+  ParamChunk<W, N> wc[CPT], bc[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int ch = tid + c * kThreads;
+    if (ch < chunks) {
+      wc[c].load(static_cast<const W*>(a.weight), ch * N);
+      if (a.bias) bc[c].load(static_cast<const W*>(a.bias), ch * N);
+    }
+  }
+  float ss[kTok];
+  {
+    const __amdgpu_buffer_rsrc_t xsrc =
+        pipe::lds_rsrc(static_cast<const T*>(a.x) + static_cast<size_t>(t0) * a.H);
+    u32x4 rs[kTok][CPT];
+#pragma unroll
+    for (int t = 0; t < kTok; ++t) {
+      const int src = min(t, ntok - 1);
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const int s = tid + c * kThreads;  // the slot this lane fills, holding chunk s ^ t
+        const uint32_t off = s < chunks ? static_cast<uint32_t>(src) * rowbytes +
+                                              (static_cast<uint32_t>(s ^ t) << 4)
+                                        : pipe::kPadOffset;
+        pipe::dma16_rsrc(xsrc, off, 0, tile + t * kPitch + (wave * kWave + c * kThreads) * 16);
+        if (has_res && s < chunks)
+          rs[t][c] = *reinterpret_cast<const u32x4*>(
+              static_cast<const T*>(a.residual) + static_cast<size_t>(t0 + src) * a.H +
+              static_cast<size_t>(s) * N);
+      }
+    }
+    // All loads at once (a CU holds its 16 rows in flight), then one wait on
+    // every path: later LDS reads need no wait for the direct-to-LDS loads.
+    pipe::wait_vmcnt<0>();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+    for (int t = 0; t < kTok; ++t) {
+      ss[t] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const int ch = tid + c * kThreads;
+        if (ch >= chunks) continue;
+        u32x4* p = slot(t, ch);
+        float v[N];
+        Vec16<T>::unpack(*p, v);
+        if (has_res) {
+          float sv[N];
+          Vec16<T>::unpack(rs[t][c], sv);
+          // the sum is rounded to the storage dtype, as the reference adds there
+#pragma unroll
+          for (int i = 0; i < N; ++i) v[i] = to_f32(from_f32<T>(v[i] + sv[i]));
+          *p = pack16<T>(v);
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) ss[t] += v[i] * v[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kTok; ++t) {
+    const float s = wave_sum(ss[t]);
+    if (lane == 0) red[t][wave] = s;
+  }
+
+  // The gate's B fragments for phase 3, loaded before any store so that
+  // waiting for them does not wait for the stores: lane (r, kq) of wave w
+  // holds gate row min(r, E - 1), elements w H/4 + 64 b + 32 u + 8 kq .. + 7
+  // (rows past E load the last row again; their columns are dropped).
+  const int r16 = lane & 15, kq = lane >> 4;
+  const int nb = a.H / 256;
+  u32x4 gf[kMaxB][2];
+  {
+    const T* grow = static_cast<const T*>(ra.gate) + static_cast<size_t>(min(r16, ra.E - 1)) * a.H +
+                    wave * (a.H / kWaves) + kq * 8;
+#pragma unroll
+    for (int b = 0; b < kMaxB; ++b)
+      if (b < nb)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          gf[b][u] = *reinterpret_cast<const u32x4*>(grow + b * 64 + u * 32);
+  }
+  lds_barrier();
+
+#pragma unroll
+  for (int t = 0; t < kTok; ++t) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += red[t][w];
+    const float inv = 1.0f / sqrtf(tot / static_cast<float>(a.H) + a.eps);
+    const size_t row = static_cast<size_t>(t0 + t) * a.H;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = tid + c * kThreads;
+      if (ch >= chunks) continue;
+      u32x4* p = slot(t, ch);
+      const u32x4 sum = *p;
+      if (has_res && t < ntok)
+        *reinterpret_cast<u32x4*>(static_cast<T*>(a.residual_out) + row +
+                                  static_cast<size_t>(ch) * N) = sum;
+      float v[N], wv[N], bv[N], o[N];
+      Vec16<T>::unpack(sum, v);
+      wc[c].unpack(wv);
+      if (a.bias) bc[c].unpack(bv);
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        o[i] = v[i] * inv * wv[i];
+        if (a.bias) o[i] += bv[i];
+      }
+      const u32x4 pk = pack16<T>(o);
+      if (t < ntok)
+        *reinterpret_cast<u32x4*>(static_cast<T*>(a.out) + row + static_cast<size_t>(ch) * N) = pk;
+      *p = pk;
+    }
+  }
+  lds_barrier();
+
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  {
+    const int cbase = wave * (a.H / 32);  // first chunk of the wave's quarter
+#pragma unroll
+    for (int b = 0; b < kMaxB; ++b)
+      if (b < nb)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          acc = pipe::Mfma16<T>::mma(*slot(r16 % kTok, cbase + 8 * b + 4 * u + kq), gf[b][u], acc);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) part[wave][4 * kq + i][r16] = acc[i];
+  lds_barrier();
+  {
+    const int t = tid / 16, e = tid % 16;
+    if (t < kTok && t0 + t < a.T && e < ra.E) {
+      float l = (part[0][t][e] + part[1][t][e]) + (part[2][t][e] + part[3][t][e]);
+      if (ra.round_logits) l = to_f32(from_f32<T>(l));
+      if (ra.bias) l += ra.bias[e];
+      lg[t][e] = l;
+      if (ra.logits_out) ra.logits_out[static_cast<size_t>(t0 + t) * ra.E + e] = l;
+    }
+  }
+  lds_barrier();
+  const int tt = tid / 16;
+  if (tt < kTok && t0 + tt < a.T)
+    group16_topk<1>(lg[tt], ra.E, ra.K, ra.renormalize, 0,
+                    ra.topk_w + static_cast<size_t>(t0 + tt) * ra.out_ld,
+                    ra.topk_ids + static_cast<size_t>(t0 + tt) * ra.out_ld, tid & 15);
+}
+
 template <typename T, typename W, int CPT>
 hipError_t launch_norm_router_cpt(const NormArgs& a, const RouterArgs& ra, hipStream_t s) {
   const dim3 block(kThreads);
@@ -382,6 +602,23 @@ hipError_t launch_norm_router_cpt(const NormArgs& a, const RouterArgs& ra, hipSt
       add_rmsnorm_router_kernel<T, W, CPT, 1, 16><<<grid, block, 0, s>>>(a, ra);
   }
   return hipGetLastError();
+}
+
+template <typename T, typename W>
+hipError_t launch_norm_router_mfma_tw(const NormArgs& a, const RouterArgs& ra, hipStream_t s) {
+  const dim3 grid((a.T + kNormRouterRows - 1) / kNormRouterRows), block(kThreads);
+  if (a.H <= 2048)
+    add_rmsnorm_router_mfma_kernel<T, W, 1><<<grid, block, 0, s>>>(a, ra);
+  else
+    add_rmsnorm_router_mfma_kernel<T, W, 2><<<grid, block, 0, s>>>(a, ra);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_norm_router_mfma_t(const NormArgs& a, const RouterArgs& ra, hipStream_t s) {
+  if (a.weight_dtype == MOE355_BF16) return launch_norm_router_mfma_tw<T, bf16>(a, ra, s);
+  if (a.weight_dtype == MOE355_F16) return launch_norm_router_mfma_tw<T, f16>(a, ra, s);
+  return launch_norm_router_mfma_tw<T, float>(a, ra, s);
 }
 
 template <typename T, typename W>
@@ -446,6 +683,18 @@ hipError_t launch_add_rmsnorm_router(const NormArgs& a, const RouterArgs& ra, in
   if (a.T == 0) return hipSuccess;
   if (dtype == MOE355_BF16) return launch_norm_router_t<bf16>(a, ra, s);
   return launch_norm_router_t<f16>(a, ra, s);
+}
+
+bool norm_router_mfma_fusable(int T, int H, int E, int K, int dtype) {
+  return (dtype == MOE355_BF16 || dtype == MOE355_F16) && E >= 1 && E <= 16 && K >= 1 &&
+         K <= 8 && H >= 256 && H % 256 == 0 && H <= 4096 && T >= kNormRouterMfmaMinRows;
+}
+
+hipError_t launch_add_rmsnorm_router_mfma(const NormArgs& a, const RouterArgs& ra, int dtype,
+                                          hipStream_t s) {
+  if (a.T == 0) return hipSuccess;
+  if (dtype == MOE355_BF16) return launch_norm_router_mfma_t<bf16>(a, ra, s);
+  return launch_norm_router_mfma_t<f16>(a, ra, s);
 }
 
 hipError_t launch_add_rmsnorm(const NormArgs& a, int dtype, hipStream_t s) {

@@ -100,105 +100,6 @@ __global__ __launch_bounds__(kThreads) void router_kernel(const RouterArgs a) {
               a.topk_ids + static_cast<size_t>(t0 + t) * a.out_ld, lane);
 }
 
-// Softmax + top-k + renormalisation of one token by a 16-lane group (the
-// lanes l .. l + 15 of one wave, sub = l % 16): lane sub holds experts
-// sub + 16 j, j < NV. Selection as wave_topk (value, then lower id on exact
-// ties), each reduction a 4-step butterfly inside the group. Lane sub == 0
-// writes the results. K <= 8.
-template <int NV>
-__device__ void group16_topk(const float* lg, int E, int K, int renorm, int kmin, float* w_out,
-                             int32_t* id_out, int sub) {
-  float v[NV];
-  bool live[NV];
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int e = sub + 16 * j;
-    live[j] = e < E;
-    v[j] = live[j] ? lg[e] : -INFINITY;
-  }
-  float m = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < NV; ++j)
-    if (live[j]) m = fmaxf(m, v[j]);
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j)
-    if (live[j]) s += expf(v[j] - m);
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
-  float hs = 0.f;
-  if (kmin > 0) {
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      if (live[j]) {
-        const float p = expf(v[j] - m) / s;
-        hs += p * logf(fmaxf(p, 1e-9f));
-      }
-    }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) hs += __shfl_xor(hs, o, 16);
-    hs = -hs;
-  }
-  float psel[8];
-  int isel[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    psel[k] = 0.f;
-    isel[k] = 0;
-    if (k >= K) continue;
-    float bv = -INFINITY;
-    int bi = INT_MAX;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int e = sub + 16 * j;
-      if (live[j] && (v[j] > bv || (v[j] == bv && e < bi))) {
-        bv = v[j];
-        bi = e;
-      }
-    }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 16);
-      const int oi = __shfl_xor(bi, o, 16);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NV; ++j)
-      if (sub + 16 * j == bi) live[j] = false;
-    psel[k] = expf(bv - m) / s;
-    isel[k] = bi;
-  }
-  if (sub != 0) return;
-  int kd = K;
-  if (kmin > 0) {
-    const float hn = E > 1 ? hs / logf(static_cast<float>(E)) : 0.f;
-    const float kf = rintf(static_cast<float>(kmin) + static_cast<float>(K - kmin) * hn);
-    kd = static_cast<int>(fminf(fmaxf(kf, static_cast<float>(kmin)), static_cast<float>(K)));
-  }
-  float sum = 0.f;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    if (k < K) {
-      psel[k] = k < kd ? psel[k] : 0.f;
-      sum += psel[k];
-    }
-  }
-  const bool norm = kmin > 0 || renorm;
-  const float denom = kmin > 0 ? fmaxf(sum, 1e-9f) : sum;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    if (k < K) {
-      w_out[k] = norm ? psel[k] / denom : psel[k];
-      id_out[k] = isel[k];
-    }
-  }
-}
-
 template <typename T>
 struct Mfma16R;
 

@@ -114,8 +114,15 @@ def _fused(x, r, nw, nb, gate, bias, K, logits=True, renorm=True):
     (torch.bfloat16, 200, 1024, 33, 5, True, "same"),     # a one-expert last pass
     (torch.bfloat16, 5, 8192, 60, 4, False, "same"),      # widest rows, no residual
     (torch.bfloat16, 5, 512, 3, 3, True, "same"),         # K == E
-    # past the fused range (T * E > 8192): norm, then the MFMA router
+    # past the VALU kernel's range (T * E > 8192): the one-launch MFMA kernel
     (torch.bfloat16, 4096, 1024, 16, 2, True, "same"),
+    (torch.bfloat16, 4096, 4096, 8, 2, True, "same"),     # Mixtral prefill
+    (torch.float16, 2060, 2048, 16, 8, True, torch.float32),  # ragged last workgroup
+    (torch.bfloat16, 2100, 256, 5, 3, False, "same"),     # narrowest rows, no residual
+    # norm, then the MFMA router (below the one-launch kernel's 2048 rows)
+    (torch.bfloat16, 1030, 2048, 16, 2, True, "same"),
+    # norm, then the MFMA router (H not a multiple of 256)
+    (torch.bfloat16, 2048, 1032, 8, 2, True, "same"),
     (torch.float32, 9, 1024, 8, 2, True, torch.float32),  # fp32: norm, then router
     (torch.bfloat16, 9, 1024, 128, 8, True, "same"),      # E > 64: norm, then router
 ])
@@ -227,3 +234,39 @@ def test_forward_with_norm_matches_oracle(T, dev):
     rounded, allow = oracle.fused_experts_bound(xn, layer["w1"], layer["w2"], wn, idn, 0,
                                                 ROUND[torch.bfloat16])
     assert_matches_rounded(stored, rounded, allow, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dt,T,H,E,K,with_res,wdt", [
+    (torch.bfloat16, 4096, 4096, 8, 2, True, "same"),
+    (torch.bfloat16, 2050, 4096, 16, 4, True, torch.float32),
+    (torch.float16, 2055, 2048, 12, 8, False, "same"),
+    (torch.bfloat16, 2048, 512, 9, 2, True, torch.float16),
+    (torch.bfloat16, 8197, 3072, 3, 1, True, "same"),
+])
+def test_prefill_norm_router_equals_two_kernels(dt, T, H, E, K, with_res, wdt, dev):
+    """At prefill sizes the one-launch MFMA kernel keeps the normed rows in
+    LDS; every output is bit for bit the two-kernel path's (the norm, then the
+    router's MFMA kernel on the stored rows), logits included."""
+    banner(f"prefill norm+router {dt} T={T} H={H} E={E} K={K} residual={with_res} w={wdt}")
+    g = torch.Generator().manual_seed(T + H + E)
+    x = torch.randn(T, H, generator=g).to(dt).to(dev)
+    r = torch.randn(T, H, generator=g).to(dt).to(dev) if with_res else None
+    wt = dt if wdt == "same" else wdt
+    nw = (torch.rand(H, generator=g) + 0.5).to(wt).to(dev)
+    nb = (torch.randn(H, generator=g) * 0.1).to(wt).to(dev) if wdt == "same" else None
+    gate = (torch.randn(E, H, generator=g) * 0.02).to(dt).to(dev)
+    bias = (torch.randn(E, generator=g) * 0.5).to(dev)
+    nr, normed, lg, w, ids = _fused(x, r, nw, nb, gate, bias, K)
+    want_r = torch.empty_like(x) if with_res else None
+    want_n = torch.empty_like(x)
+    _capi.add_rmsnorm(x, r, want_r, nw, nb, 1e-5, want_n)
+    want_lg = torch.empty_like(lg)
+    want_w = torch.full_like(w, -7.0)
+    want_ids = torch.full_like(ids, -9)
+    _capi.router_topk(want_n, gate, bias, K, True, True, 0, want_w, want_ids, logits_out=want_lg)
+    torch.cuda.synchronize()
+    if with_res:
+        assert torch.equal(nr, want_r)
+    assert torch.equal(normed, want_n)
+    assert torch.equal(lg, want_lg)
+    assert torch.equal(ids, want_ids) and torch.equal(w, want_w)

@@ -605,3 +605,89 @@ def test_random_shapes_index_math_in_bounds(c):
         counts = np.diff(o_off)
         emulate_tiled(counts, plan, True)
         emulate_tiled(counts, plan, False)
+
+
+def emulate_norm_router_tile(H, E, T, t0):
+    """add_rmsnorm_router_mfma_kernel's addressing (norm.hip) for the
+    workgroup of rows t0.., restated: returns the tile byte offsets written
+    per (row, chunk), the logical (row, chunk) behind each MFMA A fragment,
+    and the gate element offsets of the B fragments. Checks bounds as it goes."""
+    N, TOK = 8, 8       # kNormRouterRows rows per workgroup
+    cpt = 1 if H <= 2048 else 2
+    max_h = cpt * THREADS * N
+    tile_bytes = TOK * max_h * 2
+    chunks, pitch = H // N, max_h * 2
+    ntok = min(TOK, T - t0)
+    assert ntok >= 1
+    slot = lambda t, ch: t * pitch + ((ch ^ t) << 4)
+    # direct-to-LDS loads: lane `lane` of wave w, pass c, row t writes the 16
+    # bytes at t * pitch + (64 w + 256 c) * 16 + 16 lane, holding x chunk s ^ t
+    # of row min(t, ntok - 1) (s = its thread's slot), or zeros past the row
+    loaded, filler = {}, {}
+    for t in range(TOK):
+        src = min(t, ntok - 1)
+        assert 0 <= t0 + src < T
+        for tid in range(THREADS):
+            w, lane = divmod(tid, WAVE)
+            for c in range(cpt):
+                s = tid + c * THREADS
+                dst = t * pitch + (w * WAVE + c * THREADS) * 16 + 16 * lane
+                assert 0 <= dst and dst + 16 <= tile_bytes and dst not in loaded
+                if s < chunks:
+                    assert (s ^ t) < chunks and src * H * 2 + ((s ^ t) << 4) + 16 <= H * 2 * ntok
+                    loaded[dst], filler[dst] = (t, s ^ t), tid
+                else:
+                    loaded[dst], filler[dst] = None, tid
+    written = {}
+    for t in range(TOK):
+        for tid in range(THREADS):
+            for c in range(cpt):
+                ch = tid + c * THREADS
+                if ch >= chunks:
+                    continue
+                off = slot(t, ch)
+                assert 0 <= off and off + 16 <= tile_bytes
+                # the slot holds this chunk, loaded by a lane of the same wave
+                assert loaded[off] == (t, ch) and filler[off] // WAVE == tid // WAVE
+                written[(t, ch)] = off
+    assert len(written) == TOK * chunks and len(set(written.values())) == len(written)
+    nb = H // 256
+    reads, gate = [], []
+    for wave in range(WAVES):
+        cbase = wave * (H // 32)
+        for b in range(nb):
+            for u in range(2):
+                offs = []
+                for lane in range(WAVE):
+                    r16, kq = lane & 15, lane >> 4
+                    C = cbase + 8 * b + 4 * u + kq
+                    assert C < chunks
+                    off = slot(r16 % TOK, C)  # fragment rows TOK.. repeat rows 0..
+                    assert off == written[(r16 % TOK, C)]
+                    if r16 < TOK:
+                        reads.append((r16, C))
+                    offs.append(off)
+                    g0 = min(r16, E - 1) * H + wave * (H // 4) + kq * 8 + b * 64 + u * 32
+                    assert min(r16, E - 1) < E and wave * (H // 4) + kq * 8 + b * 64 + u * 32 + 8 <= H
+                    gate.append(g0)
+                # the rows of one k group sit in distinct 16-byte slots of one
+                # 128-byte span (lanes of a repeated row read the same address)
+                for kq in range(4):
+                    grp = offs[16 * kq:16 * kq + TOK]
+                    assert len({(o % 128) // 16 for o in grp}) == TOK
+                    assert len({o // 128 % (pitch // 128) for o in grp}) == 1
+    return written, reads, gate
+
+
+@pytest.mark.parametrize("H,E,T,t0", [(4096, 8, 4096, 4088), (2048, 16, 2054, 2048),
+                                      (256, 5, 2000, 1992), (3072, 12, 2048, 0),
+                                      (512, 9, 2051, 2048), (1024, 16, 4096, 16)])
+def test_norm_router_mfma_tile_addressing(H, E, T, t0):
+    written, reads, gate = emulate_norm_router_tile(H, E, T, t0)
+    # every chunk of every row is read exactly once, by the wave owning its quarter
+    assert sorted(reads) == sorted(written)
+    # the A fragment of lane (r, kq), step (b, u) of wave w holds k = w H/4 +
+    # 64 b + 32 u + 8 kq .. + 7 of row r; the B fragment the same k of its gate
+    # row: per gate row, every k exactly once
+    k_of = sorted(g % H for g in gate)
+    assert k_of == sorted(list(range(0, H, 8)) * 16)
