@@ -46,8 +46,8 @@ def configs(seed: int, n: int, large: bool = False) -> List[Dict]:
     return out
 
 
-SMALL = configs(123, 80)
-LARGE = configs(7, 16, large=True)
+SMALL = configs(123, 80) + configs(2024, 120)
+LARGE = configs(7, 16, large=True) + configs(99, 24, large=True)
 ALL = SMALL + LARGE
 
 
