@@ -326,7 +326,7 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
         return split, wt, e, row0, min(row0 + height(e), ee)
 
     whole = np.zeros((S_d, R, n_wt), np.int64)
-    parts = {}
+    parts, kcover = {}, {}
     n_seq = n_full + n_units
     lds_rows = np.arange(256)
     # ragged launches (full tiles, <= 512 routed rows per active expert):
@@ -358,6 +358,8 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
                 assert u < cap, f"partial tile {u} past the {cap} the workspace holds"
                 it = n_full + u // S
                 split, wt, e, r0, r1 = decode_tile(it)
+                kb = (u % S) * (nk // S)  # decode_work's step range
+                kcover.setdefault(it, []).append((kb, kb + nk // S))
                 parts.setdefault(it, []).append(u % S)
             n = r1 - r0
             assert 1 <= n <= tile_rows
@@ -406,6 +408,9 @@ def emulate_tiled(counts, plan, gate_up, cus=256, T=None):
             L = next_item(pid, L)
     for it, ks in parts.items():
         assert sorted(ks) == list(range(S)), f"item {it}: K-parts {ks}"
+        # the parts' step ranges tile [0, nk) without gap or overlap
+        rng = sorted(kcover[it])
+        assert rng[0][0] == 0 and rng[-1][1] == nk and all(a[1] == b[0] for a, b in zip(rng, rng[1:]))
         split, wt, e, r0, r1 = decode_tile(it)
         whole[split, r0:r1, wt] += 1
     assert (whole == 1).all(), "a (split, row, weight tile) is not covered exactly once"
