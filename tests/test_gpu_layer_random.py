@@ -1,4 +1,4 @@
-"""GPU parity of FusedMoE over 24 seeded random configurations, each through
+"""GPU parity of FusedMoE over 48 seeded random configurations, each through
 one forward path (resident; offload with RE_MAX_PACK truncation; streaming
 offload in chunks; the CPU/GPU split, truncating or over every routed
 expert), for three steps: 4-64 experts, top-1..8, 1-300 tokens, bf16 / f16 /
@@ -45,7 +45,7 @@ def _configs(seed: int, n: int):
     return out
 
 
-CONFIGS = _configs(5, 24)
+CONFIGS = _configs(5, 24) + _configs(11, 24)
 
 
 def _name(c):
